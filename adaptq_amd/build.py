@@ -1,0 +1,88 @@
+"""In-tree build of the native parts (no cmake, no JIT cache).
+
+  adaptq_amd/libadaptq.so          C ABI + gfx950 kernels (hipcc)
+  adaptq_amd/adaptq_py*.so         pybind11 module (MHAContext), links the above
+
+Run ``python -m adaptq_amd.build`` or call :func:`build`.  Every call
+recompiles.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+import sysconfig
+from concurrent.futures import ThreadPoolExecutor
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+BUILD = os.path.join(PKG, "_build")
+LIB = os.path.join(PKG, "libadaptq.so")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HIPCC = os.path.join(ROCM, "bin", "hipcc")
+ARCH = "gfx950"
+
+# -ffp-contract=off keeps every a*b+c that is not written fmaf() as two
+# roundings (the bit-exact codec depends on it); correctly rounded fp32
+# divide/sqrt and preserved denormals match the reference's x86 arithmetic;
+# packed-FP32 instructions are disabled.
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
+    "-fhip-fp32-correctly-rounded-divide-sqrt", "-fno-gpu-flush-denormals-to-zero",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
+]
+
+SOURCES = ["append.hip", "decode.hip", "sparse.hip", "c_api.cpp", "vtable.cpp"]
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(" ".join(cmd) + "\n" + r.stdout + r.stderr)
+        raise RuntimeError(f"build step failed: {os.path.basename(cmd[-1])}")
+    return r
+
+
+def build_lib(jobs: int = 8) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+
+    def compile_one(src):
+        obj = os.path.join(BUILD, src + ".o")
+        lang = ["-x", "hip"]
+        _run([HIPCC, *HIP_FLAGS, *lang, "-c", os.path.join(CSRC, src), "-o", obj])
+        return obj
+
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(compile_one, SOURCES))
+    tmp = LIB + ".tmp"
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp,
+          f"-Wl,-rpath,{ROCM}/lib", "-Wl,-soname,libadaptq.so"])
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_pybind() -> str:
+    import pybind11
+
+    suffix = sysconfig.get_config_var("EXT_SUFFIX")
+    out = os.path.join(PKG, "adaptq_py" + suffix)
+    inc = sysconfig.get_paths()["include"]
+    tmp = out + ".tmp"
+    _run(["g++", "-O2", "-std=c++17", "-shared", "-fPIC", f"-I{pybind11.get_include()}",
+          f"-I{inc}", f"-I{os.path.join(ROOT, 'include')}",
+          os.path.join(CSRC, "adapter_python.cpp"), "-o", tmp,
+          f"-L{PKG}", "-ladaptq", "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, out)
+    return out
+
+
+def build(jobs: int = 8) -> None:
+    build_lib(jobs)
+    build_pybind()
+
+
+if __name__ == "__main__":
+    build()
+    print("built", LIB)

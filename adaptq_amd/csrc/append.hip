@@ -1,0 +1,391 @@
+// append.hip -- bit-exact quantise-and-insert kernel for gfx950.
+//
+// One lane encodes one vector end to end in VGPRs: the reference's codec is
+// order-sensitive only in its two left-to-right float sums (||x||^2 and the
+// clip sigma, core/quantizer.cpp:59-63 and :81-84), which a lane computes in
+// the same order; the FWHT butterflies are element-wise and so give the same
+// bits however they are scheduled.  Lanes map to consecutive tokens of one
+// head, so a wave reads 64 consecutive input rows and writes 64 consecutive
+// ring slots.
+//
+// Restated reference steps (file:line under /root/reference):
+//   s = sum x_i*x_i left to right         quantizer.cpp:59-63
+//   norm = sqrtf(s + 1e-12f); x *= 1/norm quantizer.cpp:66-69
+//   signs + butterflies, * RN(1/RN(sqrtp)) fwht.cpp:33-66
+//   * sqrtf(p)                            quantizer.cpp:73-75
+//   sigma, +-3 sigma clamp                quantizer.cpp:81-89
+//   binary-search index, NaN -> 1/3/7     codebook.cpp:119-144
+//   MSB-first pack                        quantizer.cpp:156-209
+//   ring insert, mirror                   ring_buffer.cpp:105-119, attention.cpp:338-366
+#include "launch.hpp"
+
+namespace aq {
+
+namespace {
+
+// Index of v in the B-bit codebook: the count of thresholds t with v >= t,
+// found by the reference's branchless binary search; thresholds are selected
+// with compares already made, so no table is indexed per lane.
+template <int B>
+__device__ __forceinline__ uint32_t quantize(float v) {
+  if (v != v) return B == 2 ? 1u : B == 3 ? 3u : 7u;
+  if constexpr (B == 2) {
+    bool c1 = v >= thr<2>(1);
+    bool c0 = v >= (c1 ? thr<2>(2) : thr<2>(0));
+    return (c1 ? 2u : 0u) | (c0 ? 1u : 0u);
+  } else if constexpr (B == 3) {
+    bool c2 = v >= thr<3>(3);
+    bool c1 = v >= (c2 ? thr<3>(5) : thr<3>(1));
+    float t0 = c2 ? (c1 ? thr<3>(6) : thr<3>(4)) : (c1 ? thr<3>(2) : thr<3>(0));
+    bool c0 = v >= t0;
+    return (c2 ? 4u : 0u) | (c1 ? 2u : 0u) | (c0 ? 1u : 0u);
+  } else {
+    bool c3 = v >= thr<4>(7);
+    bool c2 = v >= (c3 ? thr<4>(11) : thr<4>(3));
+    float t1 = c3 ? (c2 ? thr<4>(13) : thr<4>(9)) : (c2 ? thr<4>(5) : thr<4>(1));
+    bool c1 = v >= t1;
+    float t0 = c3 ? (c2 ? (c1 ? thr<4>(14) : thr<4>(12)) : (c1 ? thr<4>(10) : thr<4>(8)))
+                  : (c2 ? (c1 ? thr<4>(6) : thr<4>(4)) : (c1 ? thr<4>(2) : thr<4>(0)));
+    bool c0 = v >= t0;
+    return (c3 ? 8u : 0u) | (c2 ? 4u : 0u) | (c1 ? 2u : 0u) | (c0 ? 1u : 0u);
+  }
+}
+
+// Store nbytes (a compile-time count) from w[] to dst with the widest stores
+// the row alignment allows.
+template <int NB>
+__device__ __forceinline__ void store_row(uint8_t *dst, const uint32_t (&w)[(NB + 3) / 4],
+                                          int slot) {
+  if constexpr (NB % 16 == 0) {
+    uint4 *p = reinterpret_cast<uint4 *>(dst + (size_t)slot * NB);
+#pragma unroll
+    for (int i = 0; i < NB / 16; ++i) p[i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+  } else if constexpr (NB % 8 == 0) {
+    uint2 *p = reinterpret_cast<uint2 *>(dst + (size_t)slot * NB);
+#pragma unroll
+    for (int i = 0; i < NB / 8; ++i) p[i] = make_uint2(w[2 * i], w[2 * i + 1]);
+  } else if constexpr (NB % 4 == 0) {
+    uint32_t *p = reinterpret_cast<uint32_t *>(dst + (size_t)slot * NB);
+#pragma unroll
+    for (int i = 0; i < NB / 4; ++i) p[i] = w[i];
+  } else {
+    uint8_t *p = dst + (size_t)slot * NB;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) p[i] = (uint8_t)(w[i / 4] >> (8 * (i % 4)));
+  }
+}
+
+template <int P, int B>
+struct Row {
+  static constexpr int bytes = B == 16 ? 4 * P : (P * B + 7) / 8;
+  static constexpr int words = (bytes + 3) / 4;
+};
+
+// Encode n_tok tokens of one side (K or V) for n_ctx heads.
+template <int P, int B>
+__global__ __launch_bounds__(128) void append_kernel(HeadDesc *const *descs, int n_ctx,
+                                                     int side, const float *__restrict__ src,
+                                                     int n_tok, int dim, float inv_sqrt_p,
+                                                     float sqrt_p) {
+  const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= (long long)n_ctx * n_tok) return;
+  const int c = (int)(g / n_tok);
+  const int t = (int)(g - (long long)c * n_tok);
+  const HeadDesc *d = descs[c];
+  const RingState st = d->st;
+  const int cap = d->cap;
+  const float *x = src + ((size_t)c * n_tok + t) * dim;
+
+  // Token t survives the batch only if fewer than cap tokens follow it.
+  const bool write_ring = cap > 0 && t >= n_tok - cap;
+  const int slot = cap > 0 ? (int)(((long long)st.head + t) % cap) : 0;
+  const bool write_mirror = t < mirror_count(st, n_tok, cap, d->hyb);
+
+  float buf[P];
+  if (dim == P && (P % 4) == 0) {
+#pragma unroll
+    for (int i = 0; i < P; i += 4) {
+      float4 v = *reinterpret_cast<const float4 *>(x + i);
+      buf[i] = v.x;
+      buf[i + 1] = v.y;
+      buf[i + 2] = v.z;
+      buf[i + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < P; ++i) buf[i] = i < dim ? x[i] : 0.0f;
+  }
+
+  if (write_mirror) {
+    float *m = (side == 0 ? d->raw_k : d->raw_v) + (size_t)(st.raw_count + t) * dim;
+    for (int i = 0; i < dim; ++i) m[i] = x[i];
+  }
+  if (!write_ring) return;
+
+  uint8_t *codes = side == 0 ? d->k_codes : d->v_codes;
+  float *scales = side == 0 ? d->k_scale : d->v_scale;
+
+  if constexpr (B == 16) {
+    uint32_t w[Row<P, 16>::words];
+#pragma unroll
+    for (int i = 0; i < P; ++i) w[i] = __float_as_uint(buf[i]);
+    store_row<Row<P, 16>::bytes>(codes, w, slot);
+    scales[slot] = 1.0f;
+    return;
+  } else {
+    // ||x||^2 left to right; padded zeros add +0 and change nothing.
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < P; ++i) s = __fadd_rn(s, __fmul_rn(buf[i], buf[i]));
+    const float norm = sqrtf(__fadd_rn(s, 1e-12f));
+    const float inv = 1.0f / norm;
+#pragma unroll
+    for (int i = 0; i < P; ++i) buf[i] = __fmul_rn(buf[i], inv);
+
+    // Signs fused into the first butterfly stage (exact: a sign flip).
+    uint32_t sg[(P + 31) / 32];
+#pragma unroll
+    for (int k = 0; k < (P + 31) / 32; ++k) sg[k] = d->signs[k];
+#pragma unroll
+    for (int i = 0; i < P; i += 2) {
+      const uint32_t f0 = ((sg[i / 32] >> (i % 32)) & 1u) ^ 1u;
+      const uint32_t f1 = ((sg[(i + 1) / 32] >> ((i + 1) % 32)) & 1u) ^ 1u;
+      const float a = __uint_as_float(__float_as_uint(buf[i]) ^ (f0 << 31));
+      const float b = __uint_as_float(__float_as_uint(buf[i + 1]) ^ (f1 << 31));
+      buf[i] = __fadd_rn(a, b);
+      buf[i + 1] = __fsub_rn(a, b);
+    }
+#pragma unroll
+    for (int len = 2; len < P; len <<= 1) {
+#pragma unroll
+      for (int base = 0; base < P; base += 2 * len) {
+#pragma unroll
+        for (int j = base; j < base + len; ++j) {
+          const float lo = buf[j], hi = buf[j + len];
+          buf[j] = __fadd_rn(lo, hi);
+          buf[j + len] = __fsub_rn(lo, hi);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < P; ++i) buf[i] = __fmul_rn(__fmul_rn(buf[i], inv_sqrt_p), sqrt_p);
+
+    float s2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < P; ++i) s2 = __fadd_rn(s2, __fmul_rn(buf[i], buf[i]));
+    const float sigma = sqrtf(__fadd_rn(s2 / (float)P, 1e-12f));
+    const float clip = __fmul_rn(3.0f, sigma);
+
+    uint32_t w[Row<P, B>::words];
+#pragma unroll
+    for (int k = 0; k < Row<P, B>::words; ++k) w[k] = 0u;
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      float v = buf[i];
+      if (v > clip) v = clip;
+      if (v < -clip) v = -clip;
+      const uint32_t q = quantize<B>(v);
+      // Bit position of code i inside the little-endian word stream.
+      int byte, shift;
+      if constexpr (B == 4) {
+        byte = i / 2;
+        shift = (i % 2) ? 0 : 4;
+      } else if constexpr (B == 2) {
+        byte = i / 4;
+        shift = 6 - 2 * (i % 4);
+      } else {
+        // 3-bit: group g = i/8 is the 24-bit big-endian word s0<<21|...|s7.
+        const int g = i / 8, k = i % 8;
+        const int bit = 21 - 3 * k;  // position inside the 24-bit word
+        // byte 0 of the group holds bits 23..16, byte 1 bits 15..8, byte 2 7..0
+        const int lo_byte = 2 - bit / 8, lo_shift = bit % 8;
+        if (lo_shift + 3 <= 8) {
+          byte = 3 * g + lo_byte;
+          shift = lo_shift;
+        } else {
+          // the code straddles two bytes: low part here, high part in byte-1
+          const int b0 = 3 * g + lo_byte;
+          const int nlow = 8 - lo_shift;
+          w[b0 / 4] |= (q & ((1u << nlow) - 1u)) << (8 * (b0 % 4) + lo_shift);
+          const int b1 = b0 - 1;
+          w[b1 / 4] |= (q >> nlow) << (8 * (b1 % 4));
+          continue;
+        }
+      }
+      w[byte / 4] |= q << (8 * (byte % 4) + shift);
+    }
+    store_row<Row<P, B>::bytes>(codes, w, slot);
+    scales[slot] = norm;
+  }
+}
+
+// Same codec for padded dimensions above 128: identical float steps in the
+// same order, with the vector in per-lane scratch instead of VGPRs (wide heads
+// are rare; the unrolled register kernel would cost minutes of compile time).
+template <int B>
+__global__ __launch_bounds__(128) void append_kernel_wide(HeadDesc *const *descs, int n_ctx,
+                                                          int side, const float *__restrict__ src,
+                                                          int n_tok, int dim, int P,
+                                                          float inv_sqrt_p, float sqrt_p) {
+  const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= (long long)n_ctx * n_tok) return;
+  const int c = (int)(g / n_tok);
+  const int t = (int)(g - (long long)c * n_tok);
+  const HeadDesc *d = descs[c];
+  const RingState st = d->st;
+  const int cap = d->cap;
+  const float *x = src + ((size_t)c * n_tok + t) * dim;
+  const bool write_ring = cap > 0 && t >= n_tok - cap;
+  const int slot = cap > 0 ? (int)(((long long)st.head + t) % cap) : 0;
+  if (t < mirror_count(st, n_tok, cap, d->hyb)) {
+    float *m = (side == 0 ? d->raw_k : d->raw_v) + (size_t)(st.raw_count + t) * dim;
+    for (int i = 0; i < dim; ++i) m[i] = x[i];
+  }
+  if (!write_ring) return;
+  uint8_t *codes = side == 0 ? d->k_codes : d->v_codes;
+  float *scales = side == 0 ? d->k_scale : d->v_scale;
+  const int pb = packed_bytes(P, B);
+  uint8_t *row = codes + (size_t)slot * pb;
+  if constexpr (B == 16) {
+    float *r = reinterpret_cast<float *>(row);
+    for (int i = 0; i < P; ++i) r[i] = i < dim ? x[i] : 0.0f;
+    scales[slot] = 1.0f;
+    return;
+  } else {
+    float buf[kMaxPadded];
+    float s = 0.0f;
+    for (int i = 0; i < P; ++i) {
+      buf[i] = i < dim ? x[i] : 0.0f;
+      s = __fadd_rn(s, __fmul_rn(buf[i], buf[i]));
+    }
+    const float norm = sqrtf(__fadd_rn(s, 1e-12f));
+    const float inv = 1.0f / norm;
+    for (int i = 0; i < P; ++i) buf[i] = __fmul_rn(buf[i], inv);
+    for (int i = 0; i < P; i += 2) {
+      const uint32_t f0 = ((d->signs[i >> 5] >> (i & 31)) & 1u) ^ 1u;
+      const uint32_t f1 = ((d->signs[(i + 1) >> 5] >> ((i + 1) & 31)) & 1u) ^ 1u;
+      const float a = __uint_as_float(__float_as_uint(buf[i]) ^ (f0 << 31));
+      const float b = __uint_as_float(__float_as_uint(buf[i + 1]) ^ (f1 << 31));
+      buf[i] = __fadd_rn(a, b);
+      buf[i + 1] = __fsub_rn(a, b);
+    }
+    for (int len = 2; len < P; len <<= 1)
+      for (int base = 0; base < P; base += 2 * len)
+        for (int j = base; j < base + len; ++j) {
+          const float lo = buf[j], hi = buf[j + len];
+          buf[j] = __fadd_rn(lo, hi);
+          buf[j + len] = __fsub_rn(lo, hi);
+        }
+    float s2 = 0.0f;
+    for (int i = 0; i < P; ++i) {
+      buf[i] = __fmul_rn(__fmul_rn(buf[i], inv_sqrt_p), sqrt_p);
+      s2 = __fadd_rn(s2, __fmul_rn(buf[i], buf[i]));
+    }
+    const float sigma = sqrtf(__fadd_rn(s2 / (float)P, 1e-12f));
+    const float clip = __fmul_rn(3.0f, sigma);
+    for (int i = 0; i < pb; ++i) row[i] = 0;
+    for (int i = 0; i < P; ++i) {
+      float v = buf[i];
+      if (v > clip) v = clip;
+      if (v < -clip) v = -clip;
+      const uint32_t q = quantize<B>(v);
+      if constexpr (B == 4) {
+        row[i / 2] |= (uint8_t)(q << ((i % 2) ? 0 : 4));
+      } else if constexpr (B == 2) {
+        row[i / 4] |= (uint8_t)(q << (6 - 2 * (i % 4)));
+      } else {
+        const int g8 = i / 8, k = i % 8, bit = 21 - 3 * k;
+        const uint32_t w = q << bit;  // inside the 24-bit big-endian group
+        row[3 * g8] |= (uint8_t)(w >> 16);
+        row[3 * g8 + 1] |= (uint8_t)(w >> 8);
+        row[3 * g8 + 2] |= (uint8_t)w;
+      }
+    }
+    scales[slot] = norm;
+  }
+}
+
+__global__ void commit_kernel(HeadDesc *const *descs, int n_ctx, int n_tok) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= n_ctx) return;
+  HeadDesc *d = descs[c];
+  d->st = ring_after(d->st, n_tok, d->cap, d->hyb);
+}
+
+__global__ void reset_kernel(HeadDesc *const *descs, int n_ctx) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= n_ctx) return;
+  RingState z = {0, 0, 0, 0};
+  descs[c]->st = z;
+}
+
+hipError_t launch_wide(HeadDesc *const *descs, int n_ctx, int side, int bits, const float *src,
+                       int n_tok, int dim, int P, hipStream_t s) {
+  const float sp = sqrtf((float)P);
+  const float isp = 1.0f / sp;
+  const long long total = (long long)n_ctx * n_tok;
+  const dim3 grid((unsigned)((total + 127) / 128));
+  switch (bits) {
+    case 2: append_kernel_wide<2><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, P, isp, sp); break;
+    case 3: append_kernel_wide<3><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, P, isp, sp); break;
+    case 4: append_kernel_wide<4><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, P, isp, sp); break;
+    case 16: append_kernel_wide<16><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, P, isp, sp); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <int P>
+hipError_t launch_side(HeadDesc *const *descs, int n_ctx, int side, int bits, const float *src,
+                       int n_tok, int dim, hipStream_t s) {
+  const float sp = sqrtf((float)P);
+  const float isp = 1.0f / sp;
+  const long long total = (long long)n_ctx * n_tok;
+  const dim3 grid((unsigned)((total + 127) / 128));
+  switch (bits) {
+    case 2: append_kernel<P, 2><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp); break;
+    case 3: append_kernel<P, 3><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp); break;
+    case 4: append_kernel<P, 4><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp); break;
+    case 16: append_kernel<P, 16><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_append(HeadDesc *const *descs, int n_ctx, int dim, int padded, int k_bits,
+                         int v_bits, const float *keys, const float *vals, int n_tok,
+                         hipStream_t s) {
+  if (n_ctx <= 0 || n_tok <= 0) return hipSuccess;
+  hipError_t e = hipSuccess;
+  for (int side = 0; side < 2 && e == hipSuccess; ++side) {
+    const int bits = side == 0 ? k_bits : v_bits;
+    const float *src = side == 0 ? keys : vals;
+    switch (padded) {
+      case 1: e = launch_side<1>(descs, n_ctx, side, bits, src, n_tok, dim, s); break;
+      case 2: e = launch_side<2>(descs, n_ctx, side, bits, src, n_tok, dim, s); break;
+      case 4: e = launch_side<4>(descs, n_ctx, side, bits, src, n_tok, dim, s); break;
+      case 8: e = launch_side<8>(descs, n_ctx, side, bits, src, n_tok, dim, s); break;
+      case 16: e = launch_side<16>(descs, n_ctx, side, bits, src, n_tok, dim, s); break;
+      case 32: e = launch_side<32>(descs, n_ctx, side, bits, src, n_tok, dim, s); break;
+      case 64: e = launch_side<64>(descs, n_ctx, side, bits, src, n_tok, dim, s); break;
+      case 128: e = launch_side<128>(descs, n_ctx, side, bits, src, n_tok, dim, s); break;
+      case 256:
+      case 512:
+      case 1024: e = launch_wide(descs, n_ctx, side, bits, src, n_tok, dim, padded, s); break;
+      default: return hipErrorInvalidValue;
+    }
+  }
+  if (e != hipSuccess) return e;
+  commit_kernel<<<(n_ctx + 255) / 256, 256, 0, s>>>(descs, n_ctx, n_tok);
+  return hipGetLastError();
+}
+
+hipError_t launch_reset_state(HeadDesc *const *descs, int n_ctx, hipStream_t s) {
+  if (n_ctx <= 0) return hipSuccess;
+  reset_kernel<<<(n_ctx + 255) / 256, 256, 0, s>>>(descs, n_ctx);
+  return hipGetLastError();
+}
+
+}  // namespace aq

@@ -1,0 +1,722 @@
+// c_api.cpp -- the C ABI of include/adaptq.h on top of the gfx950 kernels.
+//
+// Restates the contracts of the reference's core/adaptq_c_api.cpp:15-281
+// (validation, per-head seeds, thread-local error strings, return codes) and
+// attention.cpp:324-366 (head setup, append bookkeeping).  Differences, all
+// deliberate:
+//   * state lives in device HBM; appends are staged on the host and quantised
+//     by one kernel launch per flush;
+//   * nothing throws across the ABI; allocation failure returns NULL with an
+//     ADAPTQ_ERR_ALLOC message (the reference lets bad_alloc escape,
+//     ring_buffer.cpp:71-76);
+//   * adaptq_mha_create fails as a whole if a head fails (the reference keeps
+//     NULL heads, c_api.cpp:159-163).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <vector>
+
+#include "../../include/adaptq.h"
+#include "device.hpp"
+#include "launch.hpp"
+
+namespace {
+
+thread_local char tl_error[256] = "";
+
+void set_error(const char *msg) { std::snprintf(tl_error, sizeof(tl_error), "%s", msg); }
+
+void set_errorf(const char *fn, const char *what) {
+  std::snprintf(tl_error, sizeof(tl_error), "%s: %s", fn, what);
+}
+
+void clear_error() { tl_error[0] = '\0'; }
+
+bool require_handle(const void *h, const char *fn) {
+  if (h) return true;
+  set_errorf(fn, "null handle");
+  return false;
+}
+
+bool require_pointer(const void *p, const char *fn, const char *param) {
+  if (p) return true;
+  char msg[256];
+  std::snprintf(msg, sizeof(msg), "%s: null %s", fn, param);
+  set_error(msg);
+  return false;
+}
+
+bool hip_fail(hipError_t e, const char *fn) {
+  if (e == hipSuccess) return false;
+  char msg[256];
+  std::snprintf(msg, sizeof(msg), "%s: HIP error: %s", fn, hipGetErrorString(e));
+  set_error(msg);
+  return true;
+}
+
+int next_pow2(int n) {
+  if (n <= 1) return 1;
+  if (n > (1 << 30)) return 1 << 30;
+  int p = 1;
+  while (p < n) p <<= 1;
+  return p;
+}
+
+bool valid_bits(int b) { return b == 16 || (b >= 2 && b <= 4); }
+
+// One library stream per device (default priority).
+std::mutex g_stream_mu;
+hipStream_t g_streams[64];
+
+hipStream_t lib_stream(int dev) {
+  std::lock_guard<std::mutex> g(g_stream_mu);
+  if (dev < 0 || dev >= 64) return nullptr;
+  if (!g_streams[dev]) {
+    hipStream_t s = nullptr;
+    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return nullptr;
+    g_streams[dev] = s;
+  }
+  return g_streams[dev];
+}
+
+struct DevBuf {
+  void *p = nullptr;
+  size_t bytes = 0;
+  hipError_t ensure(size_t need) {
+    if (need <= bytes) return hipSuccess;
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    bytes = 0;
+    size_t want = std::max(need, (size_t)4096);
+    hipError_t e = hipMalloc(&p, want);
+    if (e == hipSuccess) bytes = want;
+    return e;
+  }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    bytes = 0;
+  }
+};
+
+constexpr int kStageTokens = 1024;
+
+struct Ctx {
+  std::mutex mu;
+  int device = 0;
+  int dim = 0, padded = 0, k_bits = 0, v_bits = 0, cap = 0, hyb = 0, k_pb = 0, v_pb = 0;
+  float v_mass = 0.f;
+  aq::RingState st{0, 0, 0, 0};
+  void *slab = nullptr;
+  aq::HeadDesc *d_desc = nullptr;
+  aq::HeadDesc **d_desc_list = nullptr;  // one entry: d_desc
+  std::vector<float> stage_k, stage_v;
+  int staged = 0;
+  DevBuf d_stage, d_io, d_ws, d_items;
+  int items_uploaded = 0;
+};
+
+struct Mha {
+  std::vector<Ctx *> heads;
+  int n_heads = 0;
+};
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+void free_ctx(Ctx *c) {
+  if (!c) return;
+  int cur = 0;
+  (void)hipGetDevice(&cur);
+  (void)hipSetDevice(c->device);
+  if (c->slab) (void)hipFree(c->slab);
+  c->d_stage.release();
+  c->d_io.release();
+  c->d_ws.release();
+  c->d_items.release();
+  (void)hipSetDevice(cur);
+  delete c;
+}
+
+Ctx *create_ctx(int dim, int k_bits, int v_bits, int capacity, uint64_t seed, float v_mass,
+                int hyb, const char *fn) {
+  const int padded = next_pow2(dim);
+  if (padded > aq::kMaxPadded) {
+    set_errorf(fn, "head dimension too large (padded dimension > 1024)");
+    return nullptr;
+  }
+  Ctx *c = new (std::nothrow) Ctx();
+  if (!c) {
+    set_errorf(fn, "host allocation failed");
+    return nullptr;
+  }
+  if (hipGetDevice(&c->device) != hipSuccess) {
+    delete c;
+    set_errorf(fn, "no HIP device available");
+    return nullptr;
+  }
+  c->dim = dim;
+  c->padded = padded;
+  c->k_bits = k_bits;
+  c->v_bits = v_bits;
+  c->cap = capacity;
+  c->hyb = hyb;
+  c->v_mass = v_mass;
+  c->k_pb = aq::packed_bytes(padded, k_bits);
+  c->v_pb = aq::packed_bytes(padded, v_bits);
+
+  // Rademacher signs, restating core/fwht.cpp:21-27 (xorshift64 13/7/17,
+  // odd -> +1) for the padded length (quantizer.cpp:32-33).
+  uint32_t sign_words[aq::kMaxSignWords] = {};
+  {
+    uint64_t s = seed ? seed : 0xdeadbeefcafe1234ULL;
+    for (int i = 0; i < padded; ++i) {
+      s ^= s << 13;
+      s ^= s >> 7;
+      s ^= s << 17;
+      if (s & 1u) sign_words[i >> 5] |= 1u << (i & 31);
+    }
+  }
+
+  const size_t cap_sz = (size_t)(capacity > 0 ? capacity : 0);
+  size_t off = 0;
+  const size_t o_desc = off;
+  off += align256(sizeof(aq::HeadDesc));
+  const size_t o_list = off;
+  off += align256(sizeof(void *));
+  const size_t o_signs = off;
+  off += align256(sizeof(sign_words));
+  const size_t o_kc = off;
+  off += align256(cap_sz * c->k_pb);
+  const size_t o_vc = off;
+  off += align256(cap_sz * c->v_pb);
+  const size_t o_ks = off;
+  off += align256(cap_sz * 4);
+  const size_t o_vs = off;
+  off += align256(cap_sz * 4);
+  const size_t o_rk = off;
+  off += align256((size_t)hyb * dim * 4);
+  const size_t o_rv = off;
+  off += align256((size_t)hyb * dim * 4);
+
+  if (hipMalloc(&c->slab, off) != hipSuccess || !c->slab) {
+    (void)hipGetLastError();
+    c->slab = nullptr;
+    free_ctx(c);
+    set_errorf(fn, "device allocation failed");
+    return nullptr;
+  }
+  uint8_t *base = static_cast<uint8_t *>(c->slab);
+  aq::HeadDesc h{};
+  h.k_codes = base + o_kc;
+  h.v_codes = base + o_vc;
+  h.k_scale = reinterpret_cast<float *>(base + o_ks);
+  h.v_scale = reinterpret_cast<float *>(base + o_vs);
+  h.raw_k = reinterpret_cast<float *>(base + o_rk);
+  h.raw_v = reinterpret_cast<float *>(base + o_rv);
+  h.signs = reinterpret_cast<uint32_t *>(base + o_signs);
+  h.dim = dim;
+  h.padded = padded;
+  h.k_bits = k_bits;
+  h.v_bits = v_bits;
+  h.k_pb = c->k_pb;
+  h.v_pb = c->v_pb;
+  h.cap = capacity;
+  h.hyb = hyb;
+  h.v_mass = v_mass;
+  h.st = aq::RingState{0, 0, 0, 0};
+  c->d_desc = reinterpret_cast<aq::HeadDesc *>(base + o_desc);
+  c->d_desc_list = reinterpret_cast<aq::HeadDesc **>(base + o_list);
+
+  // Zeroed codes and scales of 1.0, as KVFlatBuffer::init leaves them
+  // (ring_buffer.cpp:77-83).
+  hipError_t e = hipMemset(c->slab, 0, off);
+  if (e == hipSuccess) e = hipMemcpy(base + o_desc, &h, sizeof(h), hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(base + o_list, &c->d_desc, sizeof(void *), hipMemcpyHostToDevice);
+  if (e == hipSuccess)
+    e = hipMemcpy(base + o_signs, sign_words, sizeof(sign_words), hipMemcpyHostToDevice);
+  if (e == hipSuccess && cap_sz > 0) {
+    std::vector<float> ones(cap_sz, 1.0f);
+    e = hipMemcpy(base + o_ks, ones.data(), cap_sz * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(base + o_vs, ones.data(), cap_sz * 4, hipMemcpyHostToDevice);
+  }
+  if (e != hipSuccess) {
+    hip_fail(e, fn);
+    free_ctx(c);
+    return nullptr;
+  }
+  return c;
+}
+
+struct DeviceGuard {
+  int prev = -1;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (prev != dev) (void)hipSetDevice(dev);
+  }
+  ~DeviceGuard() {
+    int cur = -1;
+    (void)hipGetDevice(&cur);
+    if (prev >= 0 && cur != prev) (void)hipSetDevice(prev);
+  }
+};
+
+// Quantise the staged tokens (caller holds c->mu).
+bool flush_locked(Ctx *c, const char *fn) {
+  if (c->staged == 0) return true;
+  DeviceGuard g(c->device);
+  hipStream_t s = lib_stream(c->device);
+  const size_t row = (size_t)c->dim * 4;
+  const size_t half = align256((size_t)c->staged * row);
+  if (hip_fail(c->d_stage.ensure(2 * half), fn)) return false;
+  float *dk = static_cast<float *>(c->d_stage.p);
+  float *dv = reinterpret_cast<float *>(static_cast<uint8_t *>(c->d_stage.p) + half);
+  hipError_t e = hipMemcpyAsync(dk, c->stage_k.data(), c->staged * row, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(dv, c->stage_v.data(), c->staged * row, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess)
+    e = aq::launch_append(c->d_desc_list, 1, c->dim, c->padded, c->k_bits, c->v_bits, dk, dv,
+                          c->staged, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (hip_fail(e, fn)) return false;
+  c->st = aq::ring_after(c->st, c->staged, c->cap, c->hyb);
+  c->staged = 0;
+  c->stage_k.clear();
+  c->stage_v.clear();
+  return true;
+}
+
+void append_locked(Ctx *c, const float *key, const float *val) {
+  c->stage_k.insert(c->stage_k.end(), key, key + c->dim);
+  c->stage_v.insert(c->stage_v.end(), val, val + c->dim);
+  ++c->staged;
+  if (c->staged >= kStageTokens) flush_locked(c, "adaptq_append");
+}
+
+enum class Mode { Dense, Hybrid, Sparse };
+
+Mode mode_of(const Ctx *c) {
+  const int n = c->st.size;
+  if (c->hyb > 0 && n <= c->hyb && c->st.raw_count == n) return Mode::Hybrid;
+  if (c->v_mass > 0.0f && c->k_bits != 16 && c->v_bits != 16) return Mode::Sparse;
+  return Mode::Dense;
+}
+
+// Synchronous decode of nq queries against one head (caller holds c->mu).
+int compute_locked(Ctx *c, const float *queries, int nq, float *outs, const char *fn) {
+  if (!flush_locked(c, fn)) return -1;
+  const int n = c->st.size;
+  if (n == 0) {
+    std::memset(outs, 0, sizeof(float) * (size_t)nq * c->dim);
+    return 0;
+  }
+  DeviceGuard g(c->device);
+  hipStream_t s = lib_stream(c->device);
+  const Mode mode = mode_of(c);
+  aq::DecodeShape sh{c->dim, c->padded, c->k_bits, c->v_bits, mode == Mode::Hybrid, n};
+  const size_t io = align256((size_t)nq * c->dim * 4);
+  if (hip_fail(c->d_io.ensure(2 * io), fn)) return -1;
+  if (nq > c->items_uploaded) {
+    if (hip_fail(c->d_items.ensure(sizeof(void *) * (size_t)nq), fn)) return -1;
+    std::vector<aq::HeadDesc *> items((size_t)nq, c->d_desc);
+    if (hip_fail(hipMemcpy(c->d_items.p, items.data(), sizeof(void *) * nq, hipMemcpyHostToDevice), fn))
+      return -1;
+    c->items_uploaded = nq;
+  }
+  const size_t wsf = mode == Mode::Sparse ? aq::sparse_workspace_floats(nq, sh)
+                                          : aq::decode_workspace_floats(nq, sh);
+  if (hip_fail(c->d_ws.ensure(wsf * 4), fn)) return -1;
+  float *dq = static_cast<float *>(c->d_io.p);
+  float *dout = reinterpret_cast<float *>(static_cast<uint8_t *>(c->d_io.p) + io);
+  auto **items = static_cast<aq::HeadDesc **>(c->d_items.p);
+  hipError_t e = hipMemcpyAsync(dq, queries, (size_t)nq * c->dim * 4, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) {
+    if (mode == Mode::Sparse)
+      e = aq::launch_decode_sparse(items, nq, sh, c->v_mass, dq, dout,
+                                   static_cast<float *>(c->d_ws.p), s);
+    else
+      e = aq::launch_decode(items, nq, sh, dq, dout, static_cast<float *>(c->d_ws.p), s);
+  }
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(outs, dout, (size_t)nq * c->dim * 4, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (hip_fail(e, fn)) return -1;
+  return n;
+}
+
+void reset_locked(Ctx *c) {
+  c->staged = 0;
+  c->stage_k.clear();
+  c->stage_v.clear();
+  c->st = aq::RingState{0, 0, 0, 0};
+  DeviceGuard g(c->device);
+  hipStream_t s = lib_stream(c->device);
+  hipError_t e = aq::launch_reset_state(c->d_desc_list, 1, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) hip_fail(e, "adaptq_reset");
+}
+
+struct Plan {
+  std::vector<Ctx *> ctxs;
+  int device = 0;
+  DevBuf d_list, d_ws;
+};
+
+}  // namespace
+
+extern "C" {
+
+const char *adaptq_last_error(void) { return tl_error; }
+
+adaptq_ctx_t adaptq_create(int dim, int k_bits, int v_bits, int capacity, uint64_t seed,
+                           float v_mass, int hybrid_thresh) {
+  if (dim <= 0 || !valid_bits(k_bits) || !valid_bits(v_bits) || capacity < 0 ||
+      hybrid_thresh < 0) {
+    set_error("adaptq_create: invalid dimensions or capacity");
+    return nullptr;
+  }
+  return create_ctx(dim, k_bits, v_bits, capacity, seed, v_mass, hybrid_thresh, "adaptq_create");
+}
+
+void adaptq_destroy(adaptq_ctx_t h) { free_ctx(static_cast<Ctx *>(h)); }
+
+void adaptq_append(adaptq_ctx_t h, const float *key, const float *val, int token_pos) {
+  (void)token_pos;
+  if (!require_handle(h, "adaptq_append") || !require_pointer(key, "adaptq_append", "key") ||
+      !require_pointer(val, "adaptq_append", "val"))
+    return;
+  Ctx *c = static_cast<Ctx *>(h);
+  std::lock_guard<std::mutex> g(c->mu);
+  append_locked(c, key, val);
+}
+
+int adaptq_compute(adaptq_ctx_t h, const float *query, float *out) {
+  if (!require_handle(h, "adaptq_compute") || !require_pointer(query, "adaptq_compute", "query") ||
+      !require_pointer(out, "adaptq_compute", "out"))
+    return -1;
+  Ctx *c = static_cast<Ctx *>(h);
+  std::lock_guard<std::mutex> g(c->mu);
+  return compute_locked(c, query, 1, out, "adaptq_compute");
+}
+
+int adaptq_compute_batch(adaptq_ctx_t h, const float *queries, int num_queries, float *outs) {
+  if (!require_handle(h, "adaptq_compute_batch")) return -1;
+  if (num_queries < 0) {
+    set_error("adaptq_compute_batch: negative num_queries");
+    return -1;
+  }
+  if (num_queries > 0 && (!require_pointer(queries, "adaptq_compute_batch", "queries") ||
+                          !require_pointer(outs, "adaptq_compute_batch", "outs")))
+    return -1;
+  Ctx *c = static_cast<Ctx *>(h);
+  std::lock_guard<std::mutex> g(c->mu);
+  if (num_queries == 0) {
+    if (!flush_locked(c, "adaptq_compute_batch")) return -1;
+    return c->st.size;
+  }
+  return compute_locked(c, queries, num_queries, outs, "adaptq_compute_batch");
+}
+
+void adaptq_reset(adaptq_ctx_t h) {
+  if (!require_handle(h, "adaptq_reset")) return;
+  Ctx *c = static_cast<Ctx *>(h);
+  {
+    std::lock_guard<std::mutex> g(c->mu);
+    reset_locked(c);
+  }
+  clear_error();
+}
+
+size_t adaptq_kv_bytes(adaptq_ctx_t h) {
+  if (!require_handle(h, "adaptq_kv_bytes")) return 0;
+  Ctx *c = static_cast<Ctx *>(h);
+  std::lock_guard<std::mutex> g(c->mu);
+  aq::RingState s = aq::ring_after(c->st, c->staged, c->cap, c->hyb);
+  return (size_t)s.size * (size_t)(c->k_pb + c->v_pb);
+}
+
+adaptq_mha_t adaptq_mha_create(int n_heads, int dim, int k_bits, int v_bits, int capacity,
+                               uint64_t base_seed, float v_mass, int hybrid_thresh) {
+  if (n_heads <= 0 || dim <= 0 || !valid_bits(k_bits) || !valid_bits(v_bits) || capacity < 0 ||
+      hybrid_thresh < 0) {
+    set_error("adaptq_mha_create: invalid parameters");
+    return nullptr;
+  }
+  Mha *m = new (std::nothrow) Mha();
+  if (!m) {
+    set_error("adaptq_mha_create: host allocation failed");
+    return nullptr;
+  }
+  m->n_heads = n_heads;
+  m->heads.reserve(n_heads);
+  for (int i = 0; i < n_heads; ++i) {
+    const uint64_t seed = base_seed ^ ((uint64_t)i * 0xDEADBEEFCAFEULL);
+    Ctx *c = create_ctx(dim, k_bits, v_bits, capacity, seed, v_mass, hybrid_thresh,
+                        "adaptq_mha_create");
+    if (!c) {
+      for (Ctx *x : m->heads) free_ctx(x);
+      delete m;
+      return nullptr;
+    }
+    m->heads.push_back(c);
+  }
+  return m;
+}
+
+void adaptq_mha_destroy(adaptq_mha_t h) {
+  if (!h) return;
+  Mha *m = static_cast<Mha *>(h);
+  for (Ctx *c : m->heads) free_ctx(c);
+  delete m;
+}
+
+void adaptq_mha_append(adaptq_mha_t h, int head_idx, const float *key, const float *val,
+                       int token_pos) {
+  if (!require_handle(h, "adaptq_mha_append")) return;
+  Mha *m = static_cast<Mha *>(h);
+  if (head_idx < 0 || head_idx >= m->n_heads) {
+    set_error("adaptq_mha_append: head_idx out of range");
+    return;
+  }
+  if (!require_pointer(key, "adaptq_mha_append", "key") ||
+      !require_pointer(val, "adaptq_mha_append", "val"))
+    return;
+  clear_error();
+  adaptq_append(m->heads[head_idx], key, val, token_pos);
+}
+
+int adaptq_mha_compute(adaptq_mha_t h, int head_idx, const float *query, float *out) {
+  if (!require_handle(h, "adaptq_mha_compute")) return -1;
+  Mha *m = static_cast<Mha *>(h);
+  if (head_idx < 0 || head_idx >= m->n_heads) {
+    set_error("adaptq_mha_compute: head_idx out of range");
+    return -1;
+  }
+  if (!require_pointer(query, "adaptq_mha_compute", "query") ||
+      !require_pointer(out, "adaptq_mha_compute", "out"))
+    return -1;
+  clear_error();
+  return adaptq_compute(m->heads[head_idx], query, out);
+}
+
+int adaptq_mha_compute_batch(adaptq_mha_t h, int head_idx, const float *queries,
+                             int num_queries, float *outs) {
+  if (!require_handle(h, "adaptq_mha_compute_batch")) return -1;
+  Mha *m = static_cast<Mha *>(h);
+  if (head_idx < 0 || head_idx >= m->n_heads) {
+    set_error("adaptq_mha_compute_batch: head_idx out of range");
+    return -1;
+  }
+  if (num_queries < 0) {
+    set_error("adaptq_mha_compute_batch: negative num_queries");
+    return -1;
+  }
+  if (num_queries > 0 && (!require_pointer(queries, "adaptq_mha_compute_batch", "queries") ||
+                          !require_pointer(outs, "adaptq_mha_compute_batch", "outs")))
+    return -1;
+  clear_error();
+  return adaptq_compute_batch(m->heads[head_idx], queries, num_queries, outs);
+}
+
+void adaptq_mha_reset(adaptq_mha_t h) {
+  if (!require_handle(h, "adaptq_mha_reset")) return;
+  Mha *m = static_cast<Mha *>(h);
+  for (Ctx *c : m->heads) adaptq_reset(c);
+}
+
+size_t adaptq_mha_total_kv_bytes(adaptq_mha_t h) {
+  if (!require_handle(h, "adaptq_mha_total_kv_bytes")) return 0;
+  Mha *m = static_cast<Mha *>(h);
+  size_t total = 0;
+  for (Ctx *c : m->heads) total += adaptq_kv_bytes(c);
+  return total;
+}
+
+unsigned int adaptq_features(void) {
+  return ADAPTQ_FEAT_HYBRID | ADAPTQ_FEAT_SPARSE_V | ADAPTQ_FEAT_HIP;
+}
+
+const char *adaptq_version(void) { return "3.2.0-hip-gfx950"; }
+
+// ---- extensions ----
+
+int adaptq_flush(adaptq_ctx_t h) {
+  if (!require_handle(h, "adaptq_flush")) return -1;
+  Ctx *c = static_cast<Ctx *>(h);
+  std::lock_guard<std::mutex> g(c->mu);
+  return flush_locked(c, "adaptq_flush") ? 0 : -1;
+}
+
+int adaptq_ring_info(adaptq_ctx_t h, int *head, int *size, int *capacity, int *padded_dim,
+                     int *k_packed_bytes, int *v_packed_bytes) {
+  if (!require_handle(h, "adaptq_ring_info")) return -1;
+  Ctx *c = static_cast<Ctx *>(h);
+  std::lock_guard<std::mutex> g(c->mu);
+  if (!flush_locked(c, "adaptq_ring_info")) return -1;
+  if (head) *head = c->st.head;
+  if (size) *size = c->st.size;
+  if (capacity) *capacity = c->cap;
+  if (padded_dim) *padded_dim = c->padded;
+  if (k_packed_bytes) *k_packed_bytes = c->k_pb;
+  if (v_packed_bytes) *v_packed_bytes = c->v_pb;
+  return 0;
+}
+
+int adaptq_read_slots(adaptq_ctx_t h, int first_slot, int count, uint8_t *k_codes,
+                      uint8_t *v_codes, float *k_scale, float *v_scale) {
+  if (!require_handle(h, "adaptq_read_slots")) return -1;
+  Ctx *c = static_cast<Ctx *>(h);
+  std::lock_guard<std::mutex> g(c->mu);
+  if (first_slot < 0 || count < 0 || (long long)first_slot + count > c->cap) {
+    set_error("adaptq_read_slots: slot range out of bounds");
+    return -1;
+  }
+  if (!flush_locked(c, "adaptq_read_slots")) return -1;
+  if (count == 0) return 0;
+  DeviceGuard g2(c->device);
+  hipStream_t s = lib_stream(c->device);
+  aq::HeadDesc hd;
+  hipError_t e = hipMemcpy(&hd, c->d_desc, sizeof(hd), hipMemcpyDeviceToHost);
+  if (e == hipSuccess && k_codes)
+    e = hipMemcpyAsync(k_codes, hd.k_codes + (size_t)first_slot * c->k_pb, (size_t)count * c->k_pb,
+                       hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess && v_codes)
+    e = hipMemcpyAsync(v_codes, hd.v_codes + (size_t)first_slot * c->v_pb, (size_t)count * c->v_pb,
+                       hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess && k_scale)
+    e = hipMemcpyAsync(k_scale, hd.k_scale + first_slot, (size_t)count * 4, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess && v_scale)
+    e = hipMemcpyAsync(v_scale, hd.v_scale + first_slot, (size_t)count * 4, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (hip_fail(e, "adaptq_read_slots")) return -1;
+  return 0;
+}
+
+adaptq_ctx_t adaptq_mha_head(adaptq_mha_t h, int head_idx) {
+  if (!require_handle(h, "adaptq_mha_head")) return nullptr;
+  Mha *m = static_cast<Mha *>(h);
+  if (head_idx < 0 || head_idx >= m->n_heads) {
+    set_error("adaptq_mha_head: head_idx out of range");
+    return nullptr;
+  }
+  return m->heads[head_idx];
+}
+
+adaptq_plan_t adaptq_plan_create(const adaptq_ctx_t *ctxs, int n_ctx) {
+  const char *fn = "adaptq_plan_create";
+  if (!require_pointer(ctxs, fn, "ctxs")) return nullptr;
+  if (n_ctx <= 0) {
+    set_error("adaptq_plan_create: n_ctx must be positive");
+    return nullptr;
+  }
+  Plan *p = new (std::nothrow) Plan();
+  if (!p) {
+    set_error("adaptq_plan_create: host allocation failed");
+    return nullptr;
+  }
+  std::vector<aq::HeadDesc *> list((size_t)n_ctx);
+  for (int i = 0; i < n_ctx; ++i) {
+    Ctx *c = static_cast<Ctx *>(ctxs[i]);
+    if (!c) {
+      delete p;
+      set_error("adaptq_plan_create: null context");
+      return nullptr;
+    }
+    const Ctx *c0 = static_cast<Ctx *>(ctxs[0]);
+    if (c->dim != c0->dim || c->k_bits != c0->k_bits || c->v_bits != c0->v_bits ||
+        c->cap != c0->cap || c->hyb != c0->hyb || c->v_mass != c0->v_mass ||
+        c->device != c0->device) {
+      delete p;
+      set_error("adaptq_plan_create: contexts differ in shape, bits, capacity, mode or device");
+      return nullptr;
+    }
+    p->ctxs.push_back(c);
+    list[i] = c->d_desc;
+  }
+  p->device = p->ctxs[0]->device;
+  DeviceGuard g(p->device);
+  if (hip_fail(p->d_list.ensure(sizeof(void *) * (size_t)n_ctx), fn) ||
+      hip_fail(hipMemcpy(p->d_list.p, list.data(), sizeof(void *) * n_ctx, hipMemcpyHostToDevice), fn)) {
+    p->d_list.release();
+    delete p;
+    return nullptr;
+  }
+  return p;
+}
+
+void adaptq_plan_destroy(adaptq_plan_t h) {
+  if (!h) return;
+  Plan *p = static_cast<Plan *>(h);
+  DeviceGuard g(p->device);
+  p->d_list.release();
+  p->d_ws.release();
+  delete p;
+}
+
+int adaptq_plan_append_device(adaptq_plan_t h, const float *d_keys, const float *d_vals,
+                              int n_tokens, int first_pos, void *stream) {
+  (void)first_pos;
+  const char *fn = "adaptq_plan_append_device";
+  if (!require_handle(h, fn) || !require_pointer(d_keys, fn, "d_keys") ||
+      !require_pointer(d_vals, fn, "d_vals"))
+    return -1;
+  if (n_tokens < 0) {
+    set_error("adaptq_plan_append_device: negative n_tokens");
+    return -1;
+  }
+  Plan *p = static_cast<Plan *>(h);
+  if (n_tokens == 0) return 0;
+  for (Ctx *c : p->ctxs) {
+    std::lock_guard<std::mutex> g(c->mu);
+    if (!flush_locked(c, fn)) return -1;
+  }
+  DeviceGuard g(p->device);
+  hipStream_t s = stream ? static_cast<hipStream_t>(stream) : lib_stream(p->device);
+  const Ctx *c0 = p->ctxs[0];
+  hipError_t e = aq::launch_append(static_cast<aq::HeadDesc **>(p->d_list.p), (int)p->ctxs.size(),
+                                   c0->dim, c0->padded, c0->k_bits, c0->v_bits, d_keys, d_vals,
+                                   n_tokens, s);
+  if (hip_fail(e, fn)) return -1;
+  for (Ctx *c : p->ctxs) {
+    std::lock_guard<std::mutex> g2(c->mu);
+    c->st = aq::ring_after(c->st, n_tokens, c->cap, c->hyb);
+  }
+  return 0;
+}
+
+int adaptq_plan_compute_device(adaptq_plan_t h, const float *d_queries, float *d_outs,
+                               void *stream) {
+  const char *fn = "adaptq_plan_compute_device";
+  if (!require_handle(h, fn) || !require_pointer(d_queries, fn, "d_queries") ||
+      !require_pointer(d_outs, fn, "d_outs"))
+    return -1;
+  Plan *p = static_cast<Plan *>(h);
+  int max_n = 0;
+  for (Ctx *c : p->ctxs) {
+    std::lock_guard<std::mutex> g(c->mu);
+    if (!flush_locked(c, fn)) return -1;
+    if (c->st.size > 0 && mode_of(c) != Mode::Dense) {
+      set_error(
+          "adaptq_plan_compute_device: a context takes the sparse-V or hybrid branch; "
+          "use adaptq_compute for it");
+      return -1;
+    }
+    max_n = std::max(max_n, c->st.size);
+  }
+  const Ctx *c0 = p->ctxs[0];
+  const int n_items = (int)p->ctxs.size();
+  aq::DecodeShape sh{c0->dim, c0->padded, c0->k_bits, c0->v_bits, false, max_n};
+  DeviceGuard g(p->device);
+  if (hip_fail(p->d_ws.ensure(aq::decode_workspace_floats(n_items, sh) * 4), fn)) return -1;
+  hipStream_t s = stream ? static_cast<hipStream_t>(stream) : lib_stream(p->device);
+  hipError_t e = aq::launch_decode(static_cast<aq::HeadDesc **>(p->d_list.p), n_items, sh,
+                                   d_queries, d_outs, static_cast<float *>(p->d_ws.p), s);
+  if (hip_fail(e, fn)) return -1;
+  return 0;
+}
+
+}  // extern "C"

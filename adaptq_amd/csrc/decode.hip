@@ -1,0 +1,728 @@
+// decode.hip -- attention over the packed ring for gfx950 (dense softmax).
+//
+// What is computed, per (head, query), restating attention.cpp:480-660 with
+// v_mass <= 0:
+//   quantised K:  qr = H (D . q)  (the reference's rotation, fwht.cpp:33-66,
+//                 scaled back by sqrt(p)*||q||, attention.cpp:537-550, is
+//                 exactly the unnormalised Hadamard transform of D.q),
+//                 logit_t = (sum_i qr_i CB_K[c_ti]) / (sqrt(dim) p) * kscale_t
+//   fp32 K (16):  logit_t = (q . k_t) / sqrt(dim)            (:565-580)
+//   weights:      softmax over the ring
+//   quantised V:  acc = sum_t p_t vscale_t / sqrt(p) CB_V[c_t]  (rotated domain)
+//                 out = (H acc / sqrt(p)) . D, first dim entries   (fwht.cpp:106-134)
+//   fp32 V (16):  out = sum_t p_t v_t
+// Hybrid branch (:491-523) = fp32 K and V read from the raw mirror.
+//
+// Work split ("flash decoding"): grid = (splits, items).  A block of 4 waves
+// takes one contiguous token range of one item; each wave streams 64-token
+// tiles with an online softmax; a block writes (max, sum, acc[p]) and the
+// finalize kernel merges splits and applies the inverse FWHT.
+//
+// LUT kernel (padded 64 or 128): one lane per token.
+//   K: byte lookup table in LDS, LUT[j][b] = the contribution of code byte j
+//      with value b (2 codes at 4 bits, 4 at 2 bits, a 6-bit code pair at 3
+//      bits), so a token costs one LDS read per code byte.
+//   V: per-lane accumulators acc[p] in VGPRs, fed from a codebook-only table
+//      (byte -> 4 floats at 2 bits, byte -> 2 floats at 4 bits, 6-bit pair ->
+//      2 floats at 3 bits); reduced across lanes once per block.
+// Generic kernel (any padded up to 1024): one block-wide reduction per token
+// group; used for shapes the LUT kernel does not cover.
+#include "launch.hpp"
+
+namespace aq {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kTile = 64;
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+template <int B>
+__device__ __forceinline__ float cbv(int i) {
+  return cb<B>(i);
+}
+
+// Bytes of one ring row.
+template <int P, int B>
+struct RowBytes {
+  static constexpr int value = B == 16 ? 4 * P : (P * B) / 8;
+};
+
+// Load NB bytes (NB % 8 == 0) of row `t` into 32-bit words.
+template <int NB>
+__device__ __forceinline__ void load_row(const uint8_t *base, long long t, uint32_t (&w)[NB / 4]) {
+  const uint8_t *p = base + (size_t)t * NB;
+  if constexpr (NB % 16 == 0) {
+#pragma unroll
+    for (int i = 0; i < NB / 16; ++i) {
+      const uint4 v = reinterpret_cast<const uint4 *>(p)[i];
+      w[4 * i] = v.x;
+      w[4 * i + 1] = v.y;
+      w[4 * i + 2] = v.z;
+      w[4 * i + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NB / 8; ++i) {
+      const uint2 v = reinterpret_cast<const uint2 *>(p)[i];
+      w[2 * i] = v.x;
+      w[2 * i + 1] = v.y;
+    }
+  }
+}
+
+__device__ __forceinline__ uint32_t byte_of(const uint32_t *w, int j) {
+  return (w[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+}
+
+// 3-bit rows: code pair m (0..3) of group g as a 6-bit value s_{2m}<<3|s_{2m+1}.
+__device__ __forceinline__ uint32_t pair3(const uint32_t *w, int g, int m) {
+  const uint32_t w24 = (byte_of(w, 3 * g) << 16) | (byte_of(w, 3 * g + 1) << 8) | byte_of(w, 3 * g + 2);
+  return (w24 >> (18 - 6 * m)) & 63u;
+}
+
+template <int P, int KB>
+struct KLut {
+  // entries of the K lookup table
+  static constexpr int size = KB == 4 ? (P / 2) * 256 : KB == 2 ? (P / 4) * 256 : KB == 3 ? (P / 2) * 64 : 1;
+};
+template <int VB>
+struct VLut {
+  static constexpr int size = VB == 2 ? 256 * 4 : VB == 4 ? 256 * 2 : VB == 3 ? 64 * 2 : 4;
+};
+
+// Rotate the query into shared memory.  Quantised K: qr = H (D . q) (butterfly
+// stages in place); fp32 K: qr = q.  Padded entries are zero.
+template <int P>
+__device__ void load_query(float *s_q, const float *q, int dim, bool rotate, const uint32_t *signs) {
+  for (int i = threadIdx.x; i < P; i += blockDim.x) {
+    float v = i < dim ? q[i] : 0.0f;
+    if (rotate && !((signs[i >> 5] >> (i & 31)) & 1u)) v = -v;
+    s_q[i] = v;
+  }
+  __syncthreads();
+  if (!rotate) return;
+  for (int len = 1; len < P; len <<= 1) {
+    for (int k = threadIdx.x; k < P / 2; k += blockDim.x) {
+      const int j = (k / len) * 2 * len + (k % len);
+      const float lo = s_q[j], hi = s_q[j + len];
+      s_q[j] = lo + hi;
+      s_q[j + len] = lo - hi;
+    }
+    __syncthreads();
+  }
+}
+
+template <int P, int KB>
+__device__ void build_klut(float *lut, const float *qr) {
+  if constexpr (KB == 4) {
+    for (int e = threadIdx.x; e < (P / 2) * 256; e += blockDim.x) {
+      const int j = e >> 8, b = e & 255;
+      lut[e] = qr[2 * j] * cbv<4>(b >> 4) + qr[2 * j + 1] * cbv<4>(b & 15);
+    }
+  } else if constexpr (KB == 2) {
+    for (int e = threadIdx.x; e < (P / 4) * 256; e += blockDim.x) {
+      const int j = e >> 8, b = e & 255;
+      lut[e] = (qr[4 * j] * cbv<2>(b >> 6) + qr[4 * j + 1] * cbv<2>((b >> 4) & 3)) +
+               (qr[4 * j + 2] * cbv<2>((b >> 2) & 3) + qr[4 * j + 3] * cbv<2>(b & 3));
+    }
+  } else if constexpr (KB == 3) {
+    for (int e = threadIdx.x; e < (P / 2) * 64; e += blockDim.x) {
+      const int j = e >> 6, b = e & 63;
+      lut[e] = qr[2 * j] * cbv<3>(b >> 3) + qr[2 * j + 1] * cbv<3>(b & 7);
+    }
+  }
+}
+
+template <int VB>
+__device__ void build_vlut(float *lut) {
+  if constexpr (VB == 2) {
+    for (int b = threadIdx.x; b < 256; b += blockDim.x) {
+      lut[4 * b] = cbv<2>(b >> 6);
+      lut[4 * b + 1] = cbv<2>((b >> 4) & 3);
+      lut[4 * b + 2] = cbv<2>((b >> 2) & 3);
+      lut[4 * b + 3] = cbv<2>(b & 3);
+    }
+  } else if constexpr (VB == 4) {
+    for (int b = threadIdx.x; b < 256; b += blockDim.x) {
+      lut[2 * b] = cbv<4>(b >> 4);
+      lut[2 * b + 1] = cbv<4>(b & 15);
+    }
+  } else if constexpr (VB == 3) {
+    for (int b = threadIdx.x; b < 64; b += blockDim.x) {
+      lut[2 * b] = cbv<3>(b >> 3);
+      lut[2 * b + 1] = cbv<3>(b & 7);
+    }
+  }
+}
+
+// Sum over the lanes of a wave of v[0..P) (P >= 64): butterfly reduce-scatter;
+// on return lane L holds the totals of entries [L*P/64, (L+1)*P/64) in
+// v[0..P/64).
+// The halves are chosen with a bit mask rather than a select so the compiler
+// cannot turn the choice into a lane-dependent array index (which would move
+// v[] to scratch memory).
+template <int P>
+__device__ __forceinline__ void wave_reduce_scatter(float (&v)[P], int lane) {
+#pragma unroll
+  for (int step = 0; step < 6; ++step) {
+    const int m = 32 >> step;
+    const int half = P >> (step + 1);
+    const uint32_t up = (lane & m) ? 0xFFFFFFFFu : 0u;
+#pragma unroll
+    for (int j = 0; j < half; ++j) {
+      const uint32_t a = __float_as_uint(v[j]), b = __float_as_uint(v[j + half]);
+      const float send = __uint_as_float((a & up) | (b & ~up));
+      const float keep = __uint_as_float((b & up) | (a & ~up));
+      v[j] = keep + __shfl_xor(send, m, 64);
+    }
+  }
+}
+
+struct ItemView {
+  const uint8_t *k_rows;
+  const uint8_t *v_rows;
+  const float *k_scale;
+  const float *v_scale;
+  int n;
+};
+
+template <bool RAW>
+__device__ __forceinline__ ItemView item_view(const HeadDesc *d) {
+  ItemView r;
+  if constexpr (RAW) {
+    r.k_rows = reinterpret_cast<const uint8_t *>(d->raw_k);
+    r.v_rows = reinterpret_cast<const uint8_t *>(d->raw_v);
+  } else {
+    r.k_rows = d->k_codes;
+    r.v_rows = d->v_codes;
+  }
+  r.k_scale = d->k_scale;
+  r.v_scale = d->v_scale;
+  r.n = d->st.size;
+  return r;
+}
+
+// Writes the block's partial (max, sum, acc[P]) for (item, split).
+template <int P>
+__device__ void write_partial(float *part, float m, float l, const float *acc_lds) {
+  if (threadIdx.x == 0) {
+    part[0] = m;
+    part[1] = l;
+  }
+  for (int i = threadIdx.x; i < P; i += blockDim.x) part[4 + i] = acc_lds[i];
+}
+
+// Normalise acc (in LDS, P entries) by 1/L, undo the rotation (inverse FWHT
+// and signs, fwht.cpp:106-134) when V is quantised, and write dim outputs.
+template <bool INVERSE_FWHT>
+__device__ void finish_item(float *s_acc, int P, int dim, float L, const uint32_t *signs,
+                            float *out) {
+  const float invL = 1.0f / L;
+  for (int i = threadIdx.x; i < P; i += blockDim.x) s_acc[i] *= invL;
+  __syncthreads();
+  if (INVERSE_FWHT) {
+    for (int len = 1; len < P; len <<= 1) {
+      for (int k = threadIdx.x; k < P / 2; k += blockDim.x) {
+        const int j = (k / len) * 2 * len + (k % len);
+        const float lo = s_acc[j], hi = s_acc[j + len];
+        s_acc[j] = lo + hi;
+        s_acc[j + len] = lo - hi;
+      }
+      __syncthreads();
+    }
+    const float scale = 1.0f / sqrtf((float)P);
+    for (int i = threadIdx.x; i < dim; i += blockDim.x) {
+      const float v = s_acc[i] * scale;
+      out[i] = ((signs[i >> 5] >> (i & 31)) & 1u) ? v : -v;
+    }
+  } else {
+    for (int i = threadIdx.x; i < dim; i += blockDim.x) out[i] = s_acc[i];
+  }
+}
+
+// With n_splits == 1 the block owns its item and writes the final output
+// (outs) directly; otherwise it writes a partial for finalize_kernel.
+template <int P, int KB, int VB, bool RAW>
+__global__ __launch_bounds__(kThreads, 2) void decode_lut_kernel(
+    HeadDesc *const *item_desc, const float *__restrict__ queries, int chunk, int n_splits,
+    float *__restrict__ partials, float *__restrict__ outs) {
+  constexpr bool KQ = KB != 16;
+  constexpr bool VQ = VB != 16;
+  constexpr int KNB = RAW ? 0 : RowBytes<P, KB>::value;
+  constexpr int VNB = RAW ? 0 : RowBytes<P, VB>::value;
+  __shared__ float s_q[P];
+  __shared__ float s_klut[KLut<P, KB>::size];
+  __shared__ __align__(16) float s_vlut[VLut<VB>::size];
+  __shared__ float s_red[kWaves][P];
+  __shared__ float s_ml[kWaves][2];
+
+  const int item = blockIdx.y, split = blockIdx.x;
+  const HeadDesc *d = item_desc[item];
+  const ItemView iv = item_view<RAW>(d);
+  const int dim = d->dim;
+  const int n = iv.n;
+  const int t_begin = split * chunk;
+  const int t_end = min(n, t_begin + chunk);
+  float *part = partials + ((size_t)item * n_splits + split) * (P + 4);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (t_begin >= t_end) {
+    if (n_splits == 1) {
+      for (int i = threadIdx.x; i < dim; i += blockDim.x) outs[(size_t)item * dim + i] = 0.0f;
+      return;
+    }
+    for (int i = threadIdx.x; i < P; i += blockDim.x) part[4 + i] = 0.0f;
+    if (threadIdx.x == 0) {
+      part[0] = -INFINITY;
+      part[1] = 0.0f;
+    }
+    return;
+  }
+
+  load_query<P>(s_q, queries + (size_t)item * dim, dim, KQ, d->signs);
+  if constexpr (KQ) build_klut<P, KB>(s_klut, s_q);
+  if constexpr (VQ) build_vlut<VB>(s_vlut);
+  __syncthreads();
+
+  const float attn_s = KQ ? 1.0f / (sqrtf((float)dim) * (float)P) : 1.0f / sqrtf((float)dim);
+  const float isp = VQ ? 1.0f / sqrtf((float)P) : 1.0f;
+  // Raw rows hold dim floats; this kernel sees them only when dim == P.
+  const int stride_f = P;
+
+  float acc[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) acc[i] = 0.0f;
+  float m_run = -INFINITY, l_run = 0.0f;
+
+  for (int base = t_begin + wave * kTile; base < t_end; base += kWaves * kTile) {
+    const int t = base + lane;
+    const bool valid = t < t_end;
+    const int tt = valid ? t : t_end - 1;
+
+    // ---- logits ----
+    float dot = 0.0f;
+    if constexpr (KQ) {
+      uint32_t w[KNB / 4];
+      load_row<KNB>(iv.k_rows, tt, w);
+      float part4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if constexpr (KB == 3) {
+#pragma unroll
+        for (int g = 0; g < P / 8; ++g)
+#pragma unroll
+          for (int m = 0; m < 4; ++m) part4[m] += s_klut[(4 * g + m) * 64 + pair3(w, g, m)];
+      } else {
+#pragma unroll
+        for (int j = 0; j < KNB; ++j) part4[j & 3] += s_klut[j * 256 + byte_of(w, j)];
+      }
+      dot = (part4[0] + part4[1]) + (part4[2] + part4[3]);
+      dot = dot * attn_s * iv.k_scale[tt];
+    } else {
+      const float *kr = reinterpret_cast<const float *>(iv.k_rows) + (size_t)tt * stride_f;
+      float part4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int i = 0; i < P; i += 4) {
+        const float4 k4 = *reinterpret_cast<const float4 *>(kr + i);
+        part4[0] = fmaf(s_q[i], k4.x, part4[0]);
+        part4[1] = fmaf(s_q[i + 1], k4.y, part4[1]);
+        part4[2] = fmaf(s_q[i + 2], k4.z, part4[2]);
+        part4[3] = fmaf(s_q[i + 3], k4.w, part4[3]);
+      }
+      dot = ((part4[0] + part4[1]) + (part4[2] + part4[3])) * attn_s;
+    }
+    const float logit = valid ? dot : -INFINITY;
+
+    // ---- online softmax (wave-uniform running max) ----
+    const float tmax = wave_max(logit);
+    if (tmax > m_run) {
+      const float alpha = m_run == -INFINITY ? 0.0f : expf(m_run - tmax);
+#pragma unroll
+      for (int i = 0; i < P; ++i) acc[i] *= alpha;
+      l_run *= alpha;
+      m_run = tmax;
+    }
+    if (!valid) continue;
+    const float e = expf(logit - m_run);
+    l_run += e;
+
+    // ---- V accumulate ----
+    if constexpr (VQ) {
+      const float wgt = e * iv.v_scale[tt] * isp;
+      uint32_t w[VNB / 4];
+      load_row<VNB>(iv.v_rows, tt, w);
+      if constexpr (VB == 2) {
+#pragma unroll
+        for (int j = 0; j < VNB; ++j) {
+          const float4 c = reinterpret_cast<const float4 *>(s_vlut)[byte_of(w, j)];
+          acc[4 * j] = fmaf(c.x, wgt, acc[4 * j]);
+          acc[4 * j + 1] = fmaf(c.y, wgt, acc[4 * j + 1]);
+          acc[4 * j + 2] = fmaf(c.z, wgt, acc[4 * j + 2]);
+          acc[4 * j + 3] = fmaf(c.w, wgt, acc[4 * j + 3]);
+        }
+      } else if constexpr (VB == 4) {
+#pragma unroll
+        for (int j = 0; j < VNB; ++j) {
+          const float2 c = reinterpret_cast<const float2 *>(s_vlut)[byte_of(w, j)];
+          acc[2 * j] = fmaf(c.x, wgt, acc[2 * j]);
+          acc[2 * j + 1] = fmaf(c.y, wgt, acc[2 * j + 1]);
+        }
+      } else {
+#pragma unroll
+        for (int g = 0; g < P / 8; ++g)
+#pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            const float2 c = reinterpret_cast<const float2 *>(s_vlut)[pair3(w, g, m)];
+            acc[8 * g + 2 * m] = fmaf(c.x, wgt, acc[8 * g + 2 * m]);
+            acc[8 * g + 2 * m + 1] = fmaf(c.y, wgt, acc[8 * g + 2 * m + 1]);
+          }
+      }
+    } else {
+      const float *vr = reinterpret_cast<const float *>(iv.v_rows) + (size_t)tt * stride_f;
+#pragma unroll
+      for (int i = 0; i < P; i += 4) {
+        const float4 v4 = *reinterpret_cast<const float4 *>(vr + i);
+        acc[i] = fmaf(v4.x, e, acc[i]);
+        acc[i + 1] = fmaf(v4.y, e, acc[i + 1]);
+        acc[i + 2] = fmaf(v4.z, e, acc[i + 2]);
+        acc[i + 3] = fmaf(v4.w, e, acc[i + 3]);
+      }
+    }
+  }
+
+  // ---- block merge: waves -> one (m, l, acc) ----
+  const float l_w = wave_sum(l_run);
+  wave_reduce_scatter<P>(acc, lane);
+#pragma unroll
+  for (int k = 0; k < P / 64; ++k) s_red[wave][lane * (P / 64) + k] = acc[k];
+  if (lane == 0) {
+    s_ml[wave][0] = m_run;
+    s_ml[wave][1] = l_w;
+  }
+  __syncthreads();
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_ml[w][0]);
+  float f[kWaves], L = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    f[w] = s_ml[w][0] == -INFINITY ? 0.0f : expf(s_ml[w][0] - M);
+    L += f[w] * s_ml[w][1];
+  }
+  if (n_splits == 1) {
+    // s_q is free now: merge the waves into it and finish the item here.
+    for (int i = threadIdx.x; i < P; i += blockDim.x) {
+      float a = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) a += f[w] * s_red[w][i];
+      s_q[i] = a;
+    }
+    __syncthreads();
+    finish_item<VQ && !RAW>(s_q, P, dim, L, d->signs, outs + (size_t)item * dim);
+    return;
+  }
+  for (int i = threadIdx.x; i < P; i += blockDim.x) {
+    float a = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) a += f[w] * s_red[w][i];
+    part[4 + i] = a;
+  }
+  if (threadIdx.x == 0) {
+    part[0] = M;
+    part[1] = L;
+  }
+}
+
+// Code c of a packed row (generic unpack; restates quantizer.cpp:161-209).
+template <int B>
+__device__ __forceinline__ int code_at(const uint8_t *row, int i) {
+  if constexpr (B == 4) {
+    const uint32_t b = row[i >> 1];
+    return (i & 1) ? (b & 15) : (b >> 4);
+  } else if constexpr (B == 2) {
+    return (row[i >> 2] >> (6 - 2 * (i & 3))) & 3;
+  } else {
+    const uint8_t *p = row + 3 * (i >> 3);
+    const uint32_t w24 = ((uint32_t)p[0] << 16) | ((uint32_t)p[1] << 8) | p[2];
+    return (w24 >> (21 - 3 * (i & 7))) & 7;
+  }
+}
+
+// Generic kernel: any padded up to 1024.  Thread j owns dims j, j+256, ...;
+// tokens are processed in groups of 8 with one block reduction per group.
+template <int KB, int VB, bool RAW>
+__global__ __launch_bounds__(kThreads) void decode_generic_kernel(
+    HeadDesc *const *item_desc, const float *__restrict__ queries, int chunk, int n_splits,
+    float *__restrict__ partials) {
+  constexpr bool KQ = KB != 16;
+  constexpr bool VQ = VB != 16;
+  constexpr int G = 8;
+  __shared__ float s_q[kMaxPadded];
+  __shared__ float s_part[kWaves][G];
+  const int item = blockIdx.y, split = blockIdx.x;
+  const HeadDesc *d = item_desc[item];
+  const ItemView iv = item_view<RAW>(d);
+  const int dim = d->dim, P = d->padded;
+  const int n = iv.n;
+  const int t_begin = split * chunk;
+  const int t_end = min(n, t_begin + chunk);
+  float *part = partials + ((size_t)item * n_splits + split) * (P + 4);
+  if (t_begin >= t_end) {
+    for (int i = threadIdx.x; i < P; i += blockDim.x) part[4 + i] = 0.0f;
+    if (threadIdx.x == 0) {
+      part[0] = -INFINITY;
+      part[1] = 0.0f;
+    }
+    return;
+  }
+  const float *q = queries + (size_t)item * dim;
+  for (int i = threadIdx.x; i < P; i += blockDim.x) {
+    float v = i < dim ? q[i] : 0.0f;
+    if (KQ && !((d->signs[i >> 5] >> (i & 31)) & 1u)) v = -v;
+    s_q[i] = v;
+  }
+  __syncthreads();
+  if (KQ) {
+    for (int len = 1; len < P; len <<= 1) {
+      for (int k = threadIdx.x; k < P / 2; k += blockDim.x) {
+        const int j = (k / len) * 2 * len + (k % len);
+        const float lo = s_q[j], hi = s_q[j + len];
+        s_q[j] = lo + hi;
+        s_q[j + len] = lo - hi;
+      }
+      __syncthreads();
+    }
+  }
+  const float attn_s = KQ ? 1.0f / (sqrtf((float)dim) * (float)P) : 1.0f / sqrtf((float)dim);
+  const float isp = VQ ? 1.0f / sqrtf((float)P) : 1.0f;
+  const int kstride = RAW ? dim * 4 : packed_bytes(P, KB);
+  const int vstride = RAW ? dim * 4 : packed_bytes(P, VB);
+  const int own = RAW ? dim : P;  // dims that carry data
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+
+  float acc[kMaxPadded / kThreads];
+#pragma unroll
+  for (int r = 0; r < kMaxPadded / kThreads; ++r) acc[r] = 0.0f;
+  float m_run = -INFINITY, l_run = 0.0f;
+
+  for (int t0 = t_begin; t0 < t_end; t0 += G) {
+    float pd[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      pd[g] = 0.0f;
+      const int t = t0 + g;
+      if (t >= t_end) continue;
+      const uint8_t *row = iv.k_rows + (size_t)t * kstride;
+      for (int i = threadIdx.x; i < own; i += kThreads) {
+        float kv;
+        if constexpr (KQ) kv = cbv<KB>(code_at<KB>(row, i));
+        else kv = reinterpret_cast<const float *>(row)[i];
+        pd[g] = fmaf(s_q[i], kv, pd[g]);
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float s = wave_sum(pd[g]);
+      if (lane == 0) s_part[wave][g] = s;
+    }
+    __syncthreads();
+    float lg[G];
+    float gmax = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float s = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) s += s_part[w][g];
+      const int t = t0 + g;
+      lg[g] = t < t_end ? (KQ ? s * attn_s * iv.k_scale[t] : s * attn_s) : -INFINITY;
+      gmax = fmaxf(gmax, lg[g]);
+    }
+    __syncthreads();
+    if (gmax > m_run) {
+      const float alpha = m_run == -INFINITY ? 0.0f : expf(m_run - gmax);
+#pragma unroll
+      for (int r = 0; r < kMaxPadded / kThreads; ++r) acc[r] *= alpha;
+      l_run *= alpha;
+      m_run = gmax;
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int t = t0 + g;
+      if (t >= t_end) continue;
+      const float e = expf(lg[g] - m_run);
+      l_run += e;
+      const float wgt = VQ ? e * iv.v_scale[t] * isp : e;
+      const uint8_t *row = iv.v_rows + (size_t)t * vstride;
+#pragma unroll
+      for (int r = 0; r < kMaxPadded / kThreads; ++r) {
+        const int i = threadIdx.x + r * kThreads;
+        if (i >= own) break;
+        float vv;
+        if constexpr (VQ) vv = cbv<VB>(code_at<VB>(row, i));
+        else vv = reinterpret_cast<const float *>(row)[i];
+        acc[r] = fmaf(vv, wgt, acc[r]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kMaxPadded / kThreads; ++r) {
+    const int i = threadIdx.x + r * kThreads;
+    if (i < P) part[4 + i] = i < own ? acc[r] : 0.0f;
+  }
+  if (threadIdx.x == 0) {
+    part[0] = m_run;
+    part[1] = l_run;
+  }
+}
+
+// Merge the splits of each item, normalise, undo the rotation.
+template <bool INVERSE_FWHT>
+__global__ __launch_bounds__(kThreads) void finalize_kernel(HeadDesc *const *item_desc, int P,
+                                                            int n_splits,
+                                                            const float *__restrict__ partials,
+                                                            float *__restrict__ outs) {
+  __shared__ float s_acc[kMaxPadded];
+  __shared__ float s_f[256];
+  const int item = blockIdx.x;
+  const HeadDesc *d = item_desc[item];
+  const int dim = d->dim;
+  float *out = outs + (size_t)item * dim;
+  if (d->st.size == 0) {
+    for (int i = threadIdx.x; i < dim; i += blockDim.x) out[i] = 0.0f;
+    return;
+  }
+  const float *part = partials + (size_t)item * n_splits * (P + 4);
+  float M = -INFINITY;
+  for (int s = 0; s < n_splits; ++s) M = fmaxf(M, part[(size_t)s * (P + 4)]);
+  float L = 0.0f;
+  for (int s = 0; s < n_splits; ++s) {
+    const float ms = part[(size_t)s * (P + 4)];
+    const float f = ms == -INFINITY ? 0.0f : expf(ms - M);
+    if (threadIdx.x == 0 && s < 256) s_f[s] = f;
+    L += f * part[(size_t)s * (P + 4) + 1];
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < P; i += blockDim.x) {
+    float a = 0.0f;
+    for (int s = 0; s < n_splits; ++s) {
+      const float f = s < 256 ? s_f[s]
+                              : (part[(size_t)s * (P + 4)] == -INFINITY ? 0.0f : expf(part[(size_t)s * (P + 4)] - M));
+      a += f * part[(size_t)s * (P + 4) + 4 + i];
+    }
+    s_acc[i] = a;
+  }
+  __syncthreads();
+  finish_item<INVERSE_FWHT>(s_acc, P, dim, L, d->signs, out);
+}
+
+struct SplitPlan {
+  int splits, chunk;
+};
+
+SplitPlan plan_splits(int n_items, int max_n) {
+  SplitPlan sp;
+  const int target_blocks = 1024;
+  int by_work = (max_n + 255) / 256;
+  if (by_work < 1) by_work = 1;
+  int want = (target_blocks + n_items - 1) / n_items;
+  sp.splits = want < by_work ? want : by_work;
+  if (sp.splits < 1) sp.splits = 1;
+  int chunk = (max_n + sp.splits - 1) / sp.splits;
+  chunk = ((chunk + kTile - 1) / kTile) * kTile;
+  if (chunk < kTile) chunk = kTile;
+  sp.chunk = chunk;
+  sp.splits = (max_n + chunk - 1) / chunk;
+  if (sp.splits < 1) sp.splits = 1;
+  return sp;
+}
+
+template <int P, bool RAW>
+hipError_t dispatch_lut(const DecodeShape &sh, dim3 grid, HeadDesc *const *descs, const float *q,
+                        int chunk, int splits, float *part, float *out, hipStream_t s) {
+#define AQ_LUT(KB_, VB_)                                                                         \
+  if (sh.k_bits == KB_ && sh.v_bits == VB_) {                                                     \
+    decode_lut_kernel<P, KB_, VB_, RAW><<<grid, kThreads, 0, s>>>(descs, q, chunk, splits, part, out); \
+    return hipGetLastError();                                                                     \
+  }
+  if constexpr (RAW) {
+    AQ_LUT(16, 16)
+  } else {
+    AQ_LUT(4, 2) AQ_LUT(4, 3) AQ_LUT(4, 4) AQ_LUT(4, 16)
+    AQ_LUT(3, 2) AQ_LUT(3, 3) AQ_LUT(3, 4) AQ_LUT(3, 16)
+    AQ_LUT(2, 2) AQ_LUT(2, 3) AQ_LUT(2, 4) AQ_LUT(2, 16)
+    AQ_LUT(16, 2) AQ_LUT(16, 3) AQ_LUT(16, 4) AQ_LUT(16, 16)
+  }
+#undef AQ_LUT
+  return hipErrorInvalidValue;
+}
+
+template <bool RAW>
+hipError_t dispatch_generic(const DecodeShape &sh, dim3 grid, HeadDesc *const *descs,
+                            const float *q, int chunk, int splits, float *part, hipStream_t s) {
+#define AQ_GEN(KB_, VB_)                                                                           \
+  if (sh.k_bits == KB_ && sh.v_bits == VB_) {                                                       \
+    decode_generic_kernel<KB_, VB_, RAW><<<grid, kThreads, 0, s>>>(descs, q, chunk, splits, part); \
+    return hipGetLastError();                                                                       \
+  }
+  if constexpr (RAW) {
+    AQ_GEN(16, 16)
+  } else {
+    AQ_GEN(4, 2) AQ_GEN(4, 3) AQ_GEN(4, 4) AQ_GEN(4, 16)
+    AQ_GEN(3, 2) AQ_GEN(3, 3) AQ_GEN(3, 4) AQ_GEN(3, 16)
+    AQ_GEN(2, 2) AQ_GEN(2, 3) AQ_GEN(2, 4) AQ_GEN(2, 16)
+    AQ_GEN(16, 2) AQ_GEN(16, 3) AQ_GEN(16, 4) AQ_GEN(16, 16)
+  }
+#undef AQ_GEN
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+size_t decode_workspace_floats(int n_items, const DecodeShape &sh) {
+  const SplitPlan sp = plan_splits(n_items, sh.max_n > 0 ? sh.max_n : 1);
+  return (size_t)n_items * sp.splits * (sh.padded + 4);
+}
+
+hipError_t launch_decode(HeadDesc *const *descs, int n_items, const DecodeShape &sh,
+                         const float *d_q, float *d_out, float *d_ws, hipStream_t s) {
+  if (n_items <= 0) return hipSuccess;
+  const int max_n = sh.max_n > 0 ? sh.max_n : 1;
+  const SplitPlan sp = plan_splits(n_items, max_n);
+  const dim3 grid(sp.splits, n_items);
+  const bool raw = sh.raw;
+  // Raw rows hold dim floats; the LUT kernel handles them when dim == padded.
+  const bool lut_ok = (sh.padded == 64 || sh.padded == 128) && (!raw || sh.dim == sh.padded);
+  hipError_t e;
+  if (lut_ok) {
+    if (sh.padded == 64)
+      e = raw ? dispatch_lut<64, true>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, d_out, s)
+              : dispatch_lut<64, false>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, d_out, s);
+    else
+      e = raw ? dispatch_lut<128, true>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, d_out, s)
+              : dispatch_lut<128, false>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, d_out, s);
+    if (e != hipSuccess || sp.splits == 1) return e;  // one split: the kernel finished the items
+  } else {
+    e = raw ? dispatch_generic<true>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, s)
+            : dispatch_generic<false>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, s);
+  }
+  if (e != hipSuccess) return e;
+  const bool fwht = !raw && sh.v_bits != 16;
+  if (fwht)
+    finalize_kernel<true><<<n_items, kThreads, 0, s>>>(descs, sh.padded, sp.splits, d_ws, d_out);
+  else
+    finalize_kernel<false><<<n_items, kThreads, 0, s>>>(descs, sh.padded, sp.splits, d_ws, d_out);
+  return hipGetLastError();
+}
+
+}  // namespace aq

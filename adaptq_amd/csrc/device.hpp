@@ -1,0 +1,108 @@
+// device.hpp -- data layout shared by the host C ABI and the gfx950 kernels.
+//
+// One attention head ("context") owns, in device HBM:
+//   k_codes [cap][k_pb] u8   packed K codes, reference byte layout
+//   v_codes [cap][v_pb] u8   packed V codes       (cache/ring_buffer.cpp:47-84)
+//   k_scale [cap] f32, v_scale [cap] f32          L2 norms (1.0 for bits=16)
+//   raw_k/raw_v [hyb][dim] f32                    hybrid mirror (attention.cpp:356-365)
+//   signs   [padded/32] u32                       Rademacher D as a bit mask
+//   desc    HeadDesc                              pointers + config + ring state
+// With bits = 16 a "code row" is padded fp32 (k_pb = 4 * padded).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace aq {
+
+constexpr int kMaxPadded = 1024;
+constexpr int kMaxSignWords = kMaxPadded / 32;
+
+// Mutable ring state.  The host keeps its own copy for API return values; the
+// device copy is what kernels read, advanced by commit kernels in stream order.
+struct RingState {
+  int head;       // next slot to write
+  int size;       // valid tokens
+  int raw_count;  // tokens in the hybrid mirror
+  int pad_;
+};
+
+struct HeadDesc {
+  uint8_t *k_codes;
+  uint8_t *v_codes;
+  float *k_scale;
+  float *v_scale;
+  float *raw_k;
+  float *raw_v;
+  uint32_t *signs;  // bit i set <=> D[i] = +1
+  int dim, padded, k_bits, v_bits, k_pb, v_pb, cap, hyb;
+  float v_mass;
+  int pad_[3];
+  RingState st;
+};
+
+__host__ __device__ inline int packed_bytes(int padded, int bits) {
+  return bits == 16 ? padded * 4 : (padded * bits + 7) / 8;
+}
+
+// State after appending n tokens starting from s, restating
+// cache/ring_buffer.cpp:105-119 (insert) and attention.cpp:354-365 (mirror):
+// the mirror takes tokens while the ring has not evicted and holds fewer than
+// hyb vectors, and is emptied for good by the first eviction.
+__host__ __device__ inline RingState ring_after(RingState s, int n, int cap, int hyb) {
+  RingState r = s;
+  if (n <= 0) return r;
+  if (cap > 0) {
+    r.head = (int)(((long long)s.head + n) % cap);
+    long long sz = (long long)s.size + n;
+    r.size = sz > cap ? cap : (int)sz;
+  }
+  if (hyb > 0) {
+    bool evicts = (long long)s.size + n > cap;
+    if (evicts) {
+      r.raw_count = 0;
+    } else {
+      int room = hyb - s.raw_count;
+      int m = n < room ? n : room;
+      r.raw_count = s.raw_count + (m > 0 ? m : 0);
+    }
+  }
+  return r;
+}
+
+// Number of leading tokens of an n-token append that enter the mirror
+// (0 when the batch evicts, since the mirror then ends empty).
+__host__ __device__ inline int mirror_count(RingState s, int n, int cap, int hyb) {
+  if (hyb <= 0 || (long long)s.size + n > cap) return 0;
+  int room = hyb - s.raw_count;
+  int m = n < room ? n : room;
+  return m > 0 ? m : 0;
+}
+
+// Lloyd-Max N(0,1) codebooks (core/codebook.cpp:32-62).  These literal
+// tables are the quantisation format, so they equal the reference's.
+struct CB {
+  static constexpr float b2[4] = {-1.5104f, -0.4528f, 0.4528f, 1.5104f};
+  static constexpr float b3[8] = {-2.1529f, -1.3439f, -0.7560f, -0.2451f,
+                                  0.2451f,  0.7560f,  1.3439f,  2.1529f};
+  static constexpr float b4[16] = {-2.4008f, -1.8944f, -1.5105f, -1.2016f,
+                                   -0.9138f, -0.6402f, -0.3795f, -0.1258f,
+                                   0.1258f,  0.3795f,  0.6402f,  0.9138f,
+                                   1.2016f,  1.5105f,  1.8944f,  2.4008f};
+};
+
+template <int B>
+__host__ __device__ constexpr float cb(int i) {
+  return B == 2 ? CB::b2[i] : B == 3 ? CB::b3[i] : CB::b4[i];
+}
+
+// Decision threshold k (between centroids k and k+1): the float expression
+// (c[k] + c[k+1]) * 0.5f, exactly 0 at the centre (codebook.cpp:67-100).
+// Evaluated at compile time with IEEE round-to-nearest, as the reference's
+// static initialisers are.
+template <int B>
+__host__ __device__ constexpr float thr(int k) {
+  return k == (1 << B) / 2 - 1 ? 0.0f : (cb<B>(k) + cb<B>(k + 1)) * 0.5f;
+}
+
+}  // namespace aq

@@ -1,0 +1,44 @@
+// launch.hpp -- host-side launchers of the gfx950 kernels (append.hip,
+// decode.hip).  All are asynchronous on the given stream and return the HIP
+// launch status.
+#pragma once
+
+#include "device.hpp"
+
+namespace aq {
+
+// Quantise and insert n_tok tokens into each of n_ctx heads.
+// keys, vals: device [n_ctx][n_tok][dim] fp32.  All heads share padded,
+// k_bits, v_bits and dim.  Advances every head's device ring state.
+hipError_t launch_append(HeadDesc *const *d_descs, int n_ctx, int dim, int padded,
+                         int k_bits, int v_bits, const float *keys, const float *vals,
+                         int n_tok, hipStream_t stream);
+
+// Zero a head's device ring state (reset).
+hipError_t launch_reset_state(HeadDesc *const *d_descs, int n_ctx, hipStream_t stream);
+
+struct DecodeShape {
+  int dim, padded, k_bits, v_bits;
+  bool raw;   // hybrid branch: exact fp32 attention over the raw mirror
+  int max_n;  // largest ring size among the items (host view)
+};
+
+// Floats of workspace the decode of n_items items needs.
+size_t decode_workspace_floats(int n_items, const DecodeShape &shape);
+
+// One decode per item: item i attends with query d_queries[i*dim..] over the
+// ring of d_item_desc[i] and writes d_outs[i*dim..].  Dense softmax over all
+// cached tokens (the v_mass <= 0 branch); items with an empty ring get zeros.
+hipError_t launch_decode(HeadDesc *const *d_item_desc, int n_items, const DecodeShape &shape,
+                         const float *d_queries, float *d_outs, float *d_workspace,
+                         hipStream_t stream);
+
+// Sparse-V decode (v_mass > 0 on quantised K and V), restating
+// attention.cpp:448-473.  d_workspace must hold sparse_workspace_floats().
+size_t sparse_workspace_floats(int n_items, const DecodeShape &shape);
+hipError_t launch_decode_sparse(HeadDesc *const *d_item_desc, int n_items,
+                                const DecodeShape &shape, float v_mass,
+                                const float *d_queries, float *d_outs, float *d_workspace,
+                                hipStream_t stream);
+
+}  // namespace aq

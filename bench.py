@@ -1,0 +1,245 @@
+"""Headline benchmark: batched K4/V2 decode over the packed KV cache.
+
+Workload: 64 sequences x 32 layers x 8 KV heads =
+16,384 heads, head dim 128, 8,192 cached tokens each, K4/V2, v_mass = 0 and
+hybrid_thresh = 0 (pure packed-KV decode).  K/V are N(0,1) fp32 with a
+log-normal(0, 0.5) scale per head, generated on the GPU and appended through
+the library's batched device append; one decode step = one query per head,
+all heads in a single launch (adaptq_plan_compute_device).
+
+Printed JSON line: throughput in token*heads/s over the timed steps, the
+roofline of the decode kernel (algorithmic bytes / launch duration measured
+with HIP events on the launch stream), append throughput, and the reference's
+own CPU path (oracle/_ref, AVX2) timed on this host on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import threading
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+HBM_PEAK_GBS = 8000.0
+
+CFG5 = dict(n_seq=64, n_layer=32, heads=8, dim=128, ctx=8192, k_bits=4, v_bits=2)
+
+
+def pb(p, bits):
+    return p * 4 if bits == 16 else p * bits // 8
+
+
+def decode_bytes_per_token(p, kb, vb):
+    """Algorithmic HBM bytes one decode reads per (token, head): packed K and V
+    codes plus the two fp32 scales."""
+    return pb(p, kb) + pb(p, vb) + 8
+
+
+def append_bytes_per_token(dim, p, kb, vb):
+    """fp32 K and V in, packed codes and scales out."""
+    return 8 * dim + pb(p, kb) + pb(p, vb) + 8
+
+
+def cpu_baseline(cfg, seconds=12.0, heads=8, seed=0):
+    """The reference's own decode (oracle/_ref: core/*.cpp, attention.cpp built
+    from /root/reference) on this host: `heads` heads of the bench shape, each
+    filled with cfg['ctx'] tokens, then compute() repeated for ~seconds, first
+    on one thread (the reference's execution model), then on one thread per
+    head.  Returns the multi-thread figure with the single-thread one attached."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from bind import Ref, REF_SO, fptr  # test infrastructure: the checker/baseline only
+    if not os.path.exists(REF_SO):
+        return None
+    r = Ref()
+    L = r.lib
+    dim, n = cfg["dim"], cfg["ctx"]
+    rng = np.random.default_rng(seed)
+    hs = []
+    for h in range(heads):
+        c = L.adaptq_create(dim, cfg["k_bits"], cfg["v_bits"], n, 1000 + h, 0.0, 0)
+        kv = rng.standard_normal((n, 2, dim)).astype(np.float32)
+        for t in range(n):
+            L.adaptq_append(c, fptr(kv[t, 0]), fptr(kv[t, 1]), t)
+        hs.append(c)
+    q = rng.standard_normal((heads, dim)).astype(np.float32)
+    out = np.zeros((heads, dim), np.float32)
+
+    def run(idx, budget, counts):
+        t0 = time.perf_counter()
+        k = 0
+        while time.perf_counter() - t0 < budget:
+            L.adaptq_compute(hs[idx], fptr(q[idx]), fptr(out[idx]))
+            k += 1
+        counts[idx] = (k, time.perf_counter() - t0)
+
+    counts = {}
+    run(0, seconds / 3, counts)
+    single = counts[0][0] * n / counts[0][1]
+    counts = {}
+    threads = [threading.Thread(target=run, args=(i, 2 * seconds / 3, counts)) for i in range(heads)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    multi = sum(k * n / dt for k, dt in counts.values())
+    for c in hs:
+        L.adaptq_destroy(c)
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": multi, "unit": "token*heads/s", "cores": heads, "kind": "reference",
+        "sample": f"{heads} heads x {n} tokens, d{dim} K{cfg['k_bits']}/V{cfg['v_bits']}, "
+                  f"v_mass=0, hybrid=0; compute() repeated ~{seconds:.0f}s "
+                  f"(1/3 on 1 thread, 2/3 on {heads} threads); CPU: {model}",
+        "single_thread_value": single,
+        "gb_per_s": multi * decode_bytes_per_token(dim, cfg["k_bits"], cfg["v_bits"]) / 1e9,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: every box in this setup has one GPU and the "
+              "path shards by (sequence, layer, head) with no communication; run --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch  # loads torch's HIP runtime first; libadaptq binds to the same one
+
+    sys.path.insert(0, ROOT)
+    from adaptq_amd import _lib
+    L = _lib.lib
+    import ctypes as C
+
+    cfg = CFG5
+    dim, n, kb, vb = cfg["dim"], cfg["ctx"], cfg["k_bits"], cfg["v_bits"]
+    p = dim
+    n_eng = cfg["n_seq"] * cfg["n_layer"]
+    H = n_eng * cfg["heads"]
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    sptr = C.c_void_p(stream.cuda_stream)
+
+    # engines: one MHA per (sequence, layer), seed = sequence*32 + layer
+    t0 = time.time()
+    mhas, ctxs = [], []
+    for e in range(n_eng):
+        m = L.adaptq_mha_create(cfg["heads"], dim, kb, vb, n, e, 0.0, 0)
+        assert m, _lib.last_error()
+        mhas.append(m)
+        for h in range(cfg["heads"]):
+            ctxs.append(L.adaptq_mha_head(m, h))
+    arr = (C.c_void_p * H)(*ctxs)
+    plan = L.adaptq_plan_create(arr, H)
+    assert plan, _lib.last_error()
+    t_create = time.time() - t0
+
+    # bulk append in chunks of heads (synthetic data generated on the GPU)
+    g = torch.Generator(device=dev)
+    g.manual_seed(42)
+    chunk = 256
+    scales = torch.exp(0.5 * torch.randn(H, generator=g, device=dev))
+    append_ms = 0.0
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for c0 in range(0, H, chunk):
+        sub = (C.c_void_p * chunk)(*ctxs[c0:c0 + chunk])
+        sp = L.adaptq_plan_create(sub, chunk)
+        k = torch.randn(chunk, n, dim, generator=g, device=dev) * scales[c0:c0 + chunk, None, None]
+        v = torch.randn(chunk, n, dim, generator=g, device=dev) * scales[c0:c0 + chunk, None, None]
+        ev0.record(stream)
+        rc = L.adaptq_plan_append_device(sp, C.c_void_p(k.data_ptr()), C.c_void_p(v.data_ptr()),
+                                         n, 0, sptr)
+        ev1.record(stream)
+        assert rc == 0, _lib.last_error()
+        torch.cuda.synchronize()
+        append_ms += ev0.elapsed_time(ev1)
+        L.adaptq_plan_destroy(sp)
+        del k, v
+    append_tokens = H * n
+
+    q = torch.randn(H, dim, generator=g, device=dev)
+    out = torch.empty(H, dim, device=dev)
+    qp, op = C.c_void_p(q.data_ptr()), C.c_void_p(out.data_ptr())
+    for _ in range(args.warmup):
+        assert L.adaptq_plan_compute_device(plan, qp, op, sptr) == 0, _lib.last_error()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    for a, b in evs:
+        a.record(stream)
+        L.adaptq_plan_compute_device(plan, qp, op, sptr)
+        b.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    kern_ms = [a.elapsed_time(b) for a, b in evs]
+    ms = float(np.mean(kern_ms))
+    ms_per_step = wall * 1e3 / args.steps
+
+    tokens = H * n
+    bytes_launch = tokens * decode_bytes_per_token(p, kb, vb)
+    achieved = bytes_launch / (ms * 1e-3) / 1e9
+    value = tokens / (ms_per_step * 1e-3)
+    append_bytes = append_tokens * append_bytes_per_token(dim, p, kb, vb)
+
+    cpu = None if args.no_cpu else cpu_baseline(cfg, args.cpu_seconds)
+
+    line = {
+        "metric": "decode attn tokens*heads/s over packed KV + achieved HBM GB/s (% of peak)",
+        "value": value,
+        "unit": "token*heads/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8 codes / f32",
+        "data": "synthetic: N(0,1) fp32 K/V x per-head lognormal(0,0.5) scale, generated on GPU",
+        "config": {
+            "workload": "BASELINE configs[4]: 64 seq x 32 layers x 8 heads = 16384 heads, d128, "
+                        "ctx 8192, K4/V2, v_mass=0, hybrid=0, one batched decode launch",
+            "heads": H, "ctx": n, "dim": dim, "k_bits": kb, "v_bits": vb,
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+            "kernel": "decode_lut_kernel<128,4,2>", "bytes_per_launch": bytes_launch,
+            "kernel_ms": ms,
+        },
+        "append": {
+            "token_heads_per_s": append_tokens / (append_ms * 1e-3),
+            "gb_per_s": append_bytes / (append_ms * 1e-3) / 1e9,
+            "frac_hbm": append_bytes / (append_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "ms_total": append_ms,
+        },
+        "cpu_baseline": cpu,
+        "setup_s": {"create": t_create},
+    }
+    print(json.dumps(line))
+    L.adaptq_plan_destroy(plan)
+    for m in mhas:
+        L.adaptq_mha_destroy(m)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,176 @@
+/*
+ * adaptq.h -- C ABI of the MI355X (gfx950 HIP) AdapTQ KV-cache hot path.
+ *
+ * Part 1 is a drop-in for the reference's include/adaptq.h:17-126: the same
+ * 17 symbols with the same signatures, argument meaning, return codes and
+ * error strings.  Behind them, the ring buffer lives in device HBM, appends
+ * are quantised by a HIP kernel and attention is computed by HIP kernels.
+ *
+ * Part 2 lists extensions that have no counterpart in the reference; each
+ * says which callers it is for.
+ *
+ * Threading: each handle is independent (reference adaptq.h:12).  Calls on
+ * one handle are serialised by a per-handle lock.  The last-error string is
+ * thread-local.  No function throws.
+ */
+#pragma once
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#include <stddef.h>
+#include <stdint.h>
+
+/* ---- Error codes (reference include/adaptq.h:17-23) ---- */
+typedef enum {
+  ADAPTQ_OK = 0,
+  ADAPTQ_ERR_ALLOC = 1,         /* host or device allocation failed        */
+  ADAPTQ_ERR_INVALID_ARG = 2,   /* NULL handle, out-of-range bits/dim      */
+  ADAPTQ_ERR_OUT_OF_BOUNDS = 3, /* head_idx >= n_heads                     */
+  ADAPTQ_ERR_UNSUPPORTED = 4    /* requested mode not available            */
+} adaptq_error_t;
+
+/* Message of the last error on this thread, "" if none
+ * (reference include/adaptq.h:30, core/adaptq_c_api.cpp:15-21). */
+const char *adaptq_last_error(void);
+
+typedef void *adaptq_ctx_t; /* one head: ring buffer + codec state */
+typedef void *adaptq_mha_t; /* n_heads contexts                     */
+
+/* ================= Part 1: the reference's C ABI ================= */
+
+/* Replaces reference adaptq_create (core/adaptq_c_api.cpp:63-74).
+ * dim > 0 with next_pow2(dim) <= 1024; k_bits, v_bits in {2,3,4,16}
+ * (16 = fp32 passthrough); capacity >= 0; hybrid_thresh >= 0.  The context
+ * lives on the HIP device current at the call.  Returns NULL and sets the
+ * last error on invalid arguments or failed allocation. */
+adaptq_ctx_t adaptq_create(int dim, int k_bits, int v_bits, int capacity,
+                           uint64_t seed, float v_mass, int hybrid_thresh);
+
+/* Replaces reference adaptq_destroy (c_api.cpp:76-80).  NULL is a no-op. */
+void adaptq_destroy(adaptq_ctx_t ctx);
+
+/* Replaces reference adaptq_append (c_api.cpp:82-94).  Copies key and val
+ * (dim floats each) before returning; quantisation runs on the device when
+ * the staged tokens are flushed (by compute, kv_bytes, reset, adaptq_flush or
+ * a full staging area).  token_pos is accepted and unused, as in the
+ * reference. */
+void adaptq_append(adaptq_ctx_t ctx, const float *key, const float *val,
+                   int token_pos);
+
+/* Replaces reference adaptq_compute (c_api.cpp:96-107).  Synchronous: out
+ * (dim floats, host memory) is filled on return.  Returns the number of
+ * cached tokens, 0 when empty (out zeroed), -1 on error. */
+int adaptq_compute(adaptq_ctx_t ctx, const float *query, float *out);
+
+/* Replaces reference adaptq_compute_batch (c_api.cpp:109-126): num_queries
+ * queries against the same cache in one launch.  Returns the number of
+ * cached tokens, 0 when empty (outs zeroed), -1 on error; num_queries == 0
+ * accepts NULL buffers. */
+int adaptq_compute_batch(adaptq_ctx_t ctx, const float *queries,
+                         int num_queries, float *outs);
+
+/* Replaces reference adaptq_reset (c_api.cpp:128-137): empties the ring and
+ * the hybrid mirror, keeps the configuration, clears the last error. */
+void adaptq_reset(adaptq_ctx_t ctx);
+
+/* Replaces reference adaptq_kv_bytes (c_api.cpp:139-143):
+ * size * (k_packed_bytes + v_packed_bytes); scales are not counted. */
+size_t adaptq_kv_bytes(adaptq_ctx_t ctx);
+
+/* Replaces reference adaptq_mha_create (c_api.cpp:149-165).  Head i uses
+ * seed base_seed ^ (i * 0xDEADBEEFCAFE).  Unlike the reference, a head that
+ * fails to allocate fails the whole call (NULL + last error). */
+adaptq_mha_t adaptq_mha_create(int n_heads, int dim, int k_bits, int v_bits,
+                               int capacity, uint64_t base_seed, float v_mass,
+                               int hybrid_thresh);
+
+/* Replaces reference adaptq_mha_destroy (c_api.cpp:167-175). */
+void adaptq_mha_destroy(adaptq_mha_t mha);
+
+/* Replaces reference adaptq_mha_append (c_api.cpp:177-195). */
+void adaptq_mha_append(adaptq_mha_t mha, int head_idx, const float *key,
+                       const float *val, int token_pos);
+
+/* Replaces reference adaptq_mha_compute (c_api.cpp:197-215). */
+int adaptq_mha_compute(adaptq_mha_t mha, int head_idx, const float *query,
+                       float *out);
+
+/* Replaces reference adaptq_mha_compute_batch (c_api.cpp:217-241). */
+int adaptq_mha_compute_batch(adaptq_mha_t mha, int head_idx,
+                             const float *queries, int num_queries,
+                             float *outs);
+
+/* Replaces reference adaptq_mha_reset (c_api.cpp:243-250). */
+void adaptq_mha_reset(adaptq_mha_t mha);
+
+/* Replaces reference adaptq_mha_total_kv_bytes (c_api.cpp:252-261). */
+size_t adaptq_mha_total_kv_bytes(adaptq_mha_t mha);
+
+/* ---- Feature flags (reference include/adaptq.h:118-120) ---- */
+#define ADAPTQ_FEAT_AVX2 (1u << 0)     /* never set by this build          */
+#define ADAPTQ_FEAT_HYBRID (1u << 1)
+#define ADAPTQ_FEAT_SPARSE_V (1u << 2)
+#define ADAPTQ_FEAT_HIP (1u << 3)      /* extension: HIP device path       */
+
+/* Replaces reference adaptq_features (c_api.cpp:267-273). */
+unsigned int adaptq_features(void);
+
+/* Replaces reference adaptq_version (c_api.cpp:275-281), e.g.
+ * "3.2.0-hip-gfx950". */
+const char *adaptq_version(void);
+
+/* ================= Part 2: extensions ================= */
+
+/* Extension, no counterpart in the reference.  For callers that need the
+ * device state settled (timing, snapshots): quantises every staged token of
+ * ctx now.  Returns 0, or -1 with the last error set. */
+int adaptq_flush(adaptq_ctx_t ctx);
+
+/* Extension, no counterpart in the reference.  For parity checks and ring
+ * snapshots: reports the ring geometry and state. Any pointer may be NULL. */
+int adaptq_ring_info(adaptq_ctx_t ctx, int *head, int *size, int *capacity,
+                     int *padded_dim, int *k_packed_bytes,
+                     int *v_packed_bytes);
+
+/* Extension, no counterpart in the reference.  For parity checks and ring
+ * snapshots: copies `count` physical slots starting at first_slot to host
+ * memory, codes in the reference's byte layout (k_packed_bytes per slot),
+ * scales as stored.  Any output pointer may be NULL. Returns 0 or -1. */
+int adaptq_read_slots(adaptq_ctx_t ctx, int first_slot, int count,
+                      uint8_t *k_codes, uint8_t *v_codes, float *k_scale,
+                      float *v_scale);
+
+/* Extension, no counterpart in the reference.  For callers that batch over
+ * heads: the context of head head_idx of an MHA (NULL if out of range). */
+adaptq_ctx_t adaptq_mha_head(adaptq_mha_t mha, int head_idx);
+
+/* ---- Batched device-pointer path ----
+ * Extension, no counterpart in the reference.  For callers whose data is
+ * already in device memory (torch-ROCm tensors, serving loops) and for the
+ * "all engines in one launch" decode: a plan binds n_ctx contexts that share
+ * dim, k_bits, v_bits, capacity, v_mass and hybrid_thresh. */
+typedef void *adaptq_plan_t;
+
+adaptq_plan_t adaptq_plan_create(const adaptq_ctx_t *ctxs, int n_ctx);
+void adaptq_plan_destroy(adaptq_plan_t plan);
+
+/* Append n_tokens tokens to every context of the plan in one launch.
+ * d_keys, d_vals: device memory, layout [n_ctx][n_tokens][dim] fp32.
+ * Asynchronous on `stream` (a hipStream_t; NULL = the library's stream).
+ * Staged host appends of those contexts are flushed first. Returns 0/-1. */
+int adaptq_plan_append_device(adaptq_plan_t plan, const float *d_keys,
+                              const float *d_vals, int n_tokens,
+                              int first_pos, void *stream);
+
+/* One decode step for every context of the plan in one launch.
+ * d_queries [n_ctx][dim] -> d_outs [n_ctx][dim], device memory, async on
+ * `stream`.  Same results as adaptq_compute per context; contexts with an
+ * empty ring get zeros.  Returns 0/-1 (ADAPTQ_ERR_UNSUPPORTED when a context
+ * would take the sparse-V or hybrid branch: use adaptq_compute for those). */
+int adaptq_plan_compute_device(adaptq_plan_t plan, const float *d_queries,
+                               float *d_outs, void *stream);
+
+#ifdef __cplusplus
+}
+#endif

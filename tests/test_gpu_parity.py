@@ -1,0 +1,170 @@
+"""GPU parity against the oracle (oracle/oracle.c) on seeded inputs.
+
+Bar: packed codes, scales and ring state bit-exact; attention outputs within
+1e-4 norm-wise relative error (max|y - r| / max|r|), as BASELINE.json's
+north star states.
+"""
+import numpy as np
+import pytest
+
+from gpu_head import GpuHead, rel_err, same_bits
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def _inputs(rng, n, dim, family):
+    k = rng.standard_normal((n, dim)).astype(np.float32)
+    v = rng.standard_normal((n, dim)).astype(np.float32)
+    if family == "student_t":
+        k = (rng.standard_t(4, (n, dim)) / np.sqrt(2)).astype(np.float32)
+        v = (rng.standard_t(4, (n, dim)) / np.sqrt(2)).astype(np.float32)
+    elif family == "outliers":
+        k[:, [3, 17 % dim]] *= 20
+        v[:, [3, 17 % dim]] *= 20
+    elif family == "tiny":
+        k *= np.float32(1e-20)
+        v *= np.float32(1e-7)
+    elif family == "huge":
+        k *= np.float32(1e18)
+        v *= np.float32(-3e17)
+    return k, v
+
+
+def _fill(heads, k, v):
+    for t in range(k.shape[0]):
+        for h in heads:
+            h.append(k[t], v[t], t)
+
+
+def _ring_equal(g, o):
+    gi, oi = g.info(), o.info()
+    assert (gi["head"], gi["size"]) == (oi["head"], oi["size"])
+    n = oi["cap"]
+    if n == 0:
+        return
+    a = g.read_slots(0, oi["size"])
+    b = o.read_slots(0, oi["size"])
+    for x, y, what in zip(a, b, ["k codes", "v codes", "k scale", "v scale"]):
+        assert same_bits(x, y), f"{what} differ in {int((x != y).any(axis=-1).sum()) if x.ndim > 1 else int((x.view(np.uint32) != y.view(np.uint32)).sum())} slots"
+
+
+@pytest.mark.parametrize("dim,kb,vb", [
+    (64, 4, 2), (128, 4, 2), (64, 3, 2), (128, 3, 3), (64, 2, 2), (128, 2, 4),
+    (64, 16, 2), (128, 4, 16), (96, 4, 2), (32, 3, 4), (256, 4, 2), (48, 2, 3),
+])
+@pytest.mark.parametrize("family", ["normal", "student_t", "outliers", "tiny", "huge"])
+def test_append_bit_exact(oracle, dim, kb, vb, family):
+    print(f"append parity dim={dim} k{kb}v{vb} {family}", flush=True)
+    rng = np.random.default_rng(dim * 1000 + kb * 10 + vb)
+    cap, n = 96, 150  # wraps the ring
+    seed = int(rng.integers(0, 2**63))
+    k, v = _inputs(rng, n, dim, family)
+    g = GpuHead(dim, kb, vb, cap, seed)
+    o = oracle.head(dim, kb, vb, cap, seed)
+    _fill([g, o], k, v)
+    _ring_equal(g, o)
+
+
+def test_append_special_values(oracle):
+    dim, cap = 64, 32
+    rows = [np.zeros(dim, np.float32), np.full(dim, np.nan, np.float32),
+            np.full(dim, 1e38, np.float32), np.full(dim, -1e38, np.float32),
+            np.full(dim, 1e-38, np.float32), np.full(dim, -0.0, np.float32),
+            np.full(dim, np.inf, np.float32)]
+    x = np.zeros(dim, np.float32)
+    x[5] = 1e-38
+    rows.append(x)
+    x = np.zeros(dim, np.float32)
+    x[0] = 1e7
+    rows.append(x)
+    for kb, vb in [(4, 2), (3, 3), (2, 4)]:
+        print(f"special values k{kb}v{vb}", flush=True)
+        g = GpuHead(dim, kb, vb, cap, 42)
+        o = oracle.head(dim, kb, vb, cap, 42)
+        for i, r in enumerate(rows):
+            for h in (g, o):
+                h.append(r, r[::-1].copy(), i)
+        _ring_equal(g, o)
+
+
+DECODE_CASES = [
+    # dim, kb, vb, cap, n
+    (64, 4, 2, 2048, 2048),
+    (128, 4, 2, 1024, 1500),
+    (128, 4, 4, 512, 700),
+    (64, 3, 2, 1280, 1100),
+    (128, 2, 3, 300, 300),
+    (64, 16, 2, 512, 512),
+    (64, 16, 16, 256, 200),
+    (128, 4, 16, 256, 256),
+    (96, 4, 2, 256, 300),
+    (256, 3, 2, 200, 260),
+    (32, 2, 2, 100, 77),
+]
+
+
+@pytest.mark.parametrize("dim,kb,vb,cap,n", DECODE_CASES)
+def test_decode_dense(oracle, dim, kb, vb, cap, n):
+    print(f"decode dense dim={dim} k{kb}v{vb} cap={cap} n={n}", flush=True)
+    rng = np.random.default_rng(n + dim)
+    seed = 42 + dim
+    k, v = _inputs(rng, n, dim, "normal")
+    g = GpuHead(dim, kb, vb, cap, seed)
+    o = oracle.head(dim, kb, vb, cap, seed)
+    _fill([g, o], k, v)
+    for _ in range(3):
+        q = rng.standard_normal(dim).astype(np.float32)
+        y, ny = g.compute(q)
+        r, nr = o.compute(q)
+        assert ny == nr
+        assert rel_err(y, r) <= TOL, rel_err(y, r)
+
+
+@pytest.mark.parametrize("dim,kb,vb,hyb,n", [
+    (64, 4, 2, 512, 512), (128, 4, 4, 64, 40), (96, 3, 2, 128, 100), (64, 16, 2, 16, 10),
+])
+def test_decode_hybrid(oracle, dim, kb, vb, hyb, n):
+    print(f"decode hybrid dim={dim} k{kb}v{vb} hyb={hyb} n={n}", flush=True)
+    rng = np.random.default_rng(7 * n + dim)
+    k, v = _inputs(rng, n, dim, "normal")
+    g = GpuHead(dim, kb, vb, 1024, 9, 0.95, hyb)
+    o = oracle.head(dim, kb, vb, 1024, 9, 0.95, hyb)
+    _fill([g, o], k, v)
+    q = rng.standard_normal(dim).astype(np.float32)
+    y, _ = g.compute(q)
+    r, _ = o.compute(q)
+    assert rel_err(y, r) <= TOL
+
+
+@pytest.mark.parametrize("dim,kb,vb,cap,n,vm", [
+    (64, 4, 2, 2048, 2048, 0.95), (128, 4, 4, 512, 700, 0.95), (64, 3, 2, 600, 513, 0.7),
+    (128, 2, 3, 9000, 9000, 0.95), (64, 4, 2, 100, 7, 0.5),
+])
+def test_decode_sparse_v(oracle, dim, kb, vb, cap, n, vm):
+    print(f"decode sparse dim={dim} k{kb}v{vb} n={n} v_mass={vm}", flush=True)
+    rng = np.random.default_rng(3 * n + dim)
+    k, v = _inputs(rng, n, dim, "normal")
+    g = GpuHead(dim, kb, vb, cap, 5, vm, 0)
+    o = oracle.head(dim, kb, vb, cap, 5, vm, 0)
+    _fill([g, o], k, v)
+    for _ in range(2):
+        q = (3 * rng.standard_normal(dim)).astype(np.float32)
+        y, _ = g.compute(q)
+        r, _ = o.compute(q)
+        assert rel_err(y, r) <= TOL
+
+
+def test_compute_batch(oracle):
+    dim, kb, vb, cap, n = 128, 4, 4, 4096, 5000
+    rng = np.random.default_rng(11)
+    k, v = _inputs(rng, n, dim, "normal")
+    g = GpuHead(dim, kb, vb, cap, 7)
+    o = oracle.head(dim, kb, vb, cap, 7)
+    _fill([g, o], k, v)
+    qs = rng.standard_normal((16, dim)).astype(np.float32)
+    y, ny = g.compute_batch(qs)
+    r, nr = o.compute_batch(qs)
+    assert ny == nr == cap
+    assert rel_err(y, r) <= TOL
