@@ -675,7 +675,7 @@ int adaptq_plan_append_device(adaptq_plan_t h, const float *d_keys, const float 
     if (!flush_locked(c, fn)) return -1;
   }
   DeviceGuard g(p->device);
-  hipStream_t s = stream ? static_cast<hipStream_t>(stream) : lib_stream(p->device);
+  hipStream_t s = static_cast<hipStream_t>(stream);  // NULL = the HIP null stream
   const Ctx *c0 = p->ctxs[0];
   hipError_t e = aq::launch_append(static_cast<aq::HeadDesc **>(p->d_list.p), (int)p->ctxs.size(),
                                    c0->dim, c0->padded, c0->k_bits, c0->v_bits, d_keys, d_vals,
@@ -712,7 +712,7 @@ int adaptq_plan_compute_device(adaptq_plan_t h, const float *d_queries, float *d
   aq::DecodeShape sh{c0->dim, c0->padded, c0->k_bits, c0->v_bits, false, max_n};
   DeviceGuard g(p->device);
   if (hip_fail(p->d_ws.ensure(aq::decode_workspace_floats(n_items, sh) * 4), fn)) return -1;
-  hipStream_t s = stream ? static_cast<hipStream_t>(stream) : lib_stream(p->device);
+  hipStream_t s = static_cast<hipStream_t>(stream);  // NULL = the HIP null stream
   hipError_t e = aq::launch_decode(static_cast<aq::HeadDesc **>(p->d_list.p), n_items, sh,
                                    d_queries, d_outs, static_cast<float *>(p->d_ws.p), s);
   if (hip_fail(e, fn)) return -1;

@@ -694,9 +694,11 @@ size_t decode_workspace_floats(int n_items, const DecodeShape &sh) {
   return (size_t)n_items * sp.splits * (sh.padded + 4);
 }
 
-hipError_t launch_decode(HeadDesc *const *descs, int n_items, const DecodeShape &sh,
+hipError_t launch_decode(HeadDesc *const *descs, int n_items, const DecodeShape &shape,
                          const float *d_q, float *d_out, float *d_ws, hipStream_t s) {
   if (n_items <= 0) return hipSuccess;
+  DecodeShape sh = shape;
+  if (sh.raw) sh.k_bits = sh.v_bits = 16;  // the mirror holds fp32 keys and values
   const int max_n = sh.max_n > 0 ? sh.max_n : 1;
   const SplitPlan sp = plan_splits(n_items, max_n);
   const dim3 grid(sp.splits, n_items);

@@ -157,7 +157,7 @@ void adaptq_plan_destroy(adaptq_plan_t plan);
 
 /* Append n_tokens tokens to every context of the plan in one launch.
  * d_keys, d_vals: device memory, layout [n_ctx][n_tokens][dim] fp32.
- * Asynchronous on `stream` (a hipStream_t; NULL = the library's stream).
+ * Asynchronous on `stream` (a hipStream_t; NULL = the HIP null stream).
  * Staged host appends of those contexts are flushed first. Returns 0/-1. */
 int adaptq_plan_append_device(adaptq_plan_t plan, const float *d_keys,
                               const float *d_vals, int n_tokens,

@@ -87,3 +87,45 @@ def same_bits(a, b):
     a = np.ascontiguousarray(a)
     b = np.ascontiguousarray(b)
     return a.shape == b.shape and a.tobytes() == b.tobytes()
+
+
+class DeviceBuffer:
+    """Device memory through the HIP runtime libadaptq.so is linked against."""
+
+    _hip = None
+
+    @classmethod
+    def hip(cls):
+        if cls._hip is None:
+            h = C.CDLL("libamdhip64.so.7")
+            h.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+            h.hipFree.argtypes = [C.c_void_p]
+            h.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+            h.hipDeviceSynchronize.argtypes = []
+            cls._hip = h
+        return cls._hip
+
+    def __init__(self, nbytes):
+        self.nbytes = nbytes
+        self.ptr = C.c_void_p()
+        rc = self.hip().hipMalloc(C.byref(self.ptr), nbytes)
+        assert rc == 0, rc
+
+    def upload(self, a):
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes
+        assert self.hip().hipMemcpy(self.ptr, a.ctypes.data, a.nbytes, 1) == 0  # H2D
+
+    def download(self, shape, dtype=np.float32):
+        out = np.empty(shape, dtype)
+        assert self.hip().hipMemcpy(out.ctypes.data, self.ptr, out.nbytes, 2) == 0  # D2H
+        return out
+
+    def __del__(self):
+        if getattr(self, "ptr", None) and self.ptr.value:
+            self.hip().hipFree(self.ptr)
+            self.ptr = None
+
+
+def sync():
+    assert DeviceBuffer.hip().hipDeviceSynchronize() == 0

@@ -1,0 +1,79 @@
+"""Batched device-pointer path (adaptq_plan_*): one append launch and one
+decode launch for many heads must give the same ring bytes as per-token host
+appends and the same outputs as the oracle."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from adaptq_amd import _lib
+from gpu_head import DeviceBuffer, GpuHead, err, rel_err, same_bits, sync
+
+pytestmark = pytest.mark.gpu
+L = _lib.lib
+
+
+@pytest.mark.parametrize("dim,kb,vb,cap,n", [(128, 4, 2, 300, 350), (64, 3, 2, 512, 200),
+                                             (64, 16, 2, 128, 128), (128, 4, 4, 64, 64)])
+def test_plan_append_and_compute(oracle, dim, kb, vb, cap, n):
+    print(f"plan dim={dim} k{kb}v{vb} cap={cap} n={n}", flush=True)
+    H = 6
+    rng = np.random.default_rng(dim + n)
+    heads = [GpuHead(dim, kb, vb, cap, 100 + i) for i in range(H)]
+    refs = [oracle.head(dim, kb, vb, cap, 100 + i) for i in range(H)]
+    # a few host appends first, so the plan starts from a non-empty ring
+    pre = rng.standard_normal((H, 5, 2, dim)).astype(np.float32)
+    for i in range(H):
+        for t in range(5):
+            heads[i].append(pre[i, t, 0], pre[i, t, 1], t)
+            refs[i].append(pre[i, t, 0], pre[i, t, 1], t)
+    k = rng.standard_normal((H, n, dim)).astype(np.float32)
+    v = rng.standard_normal((H, n, dim)).astype(np.float32)
+    dk, dv = DeviceBuffer(k.nbytes), DeviceBuffer(v.nbytes)
+    dk.upload(k)
+    dv.upload(v)
+    arr = (C.c_void_p * H)(*[h.h for h in heads])
+    plan = L.adaptq_plan_create(arr, H)
+    assert plan, err()
+    assert L.adaptq_plan_append_device(plan, dk.ptr, dv.ptr, n, 0, None) == 0, err()
+    sync()
+    for i in range(H):
+        for t in range(n):
+            refs[i].append(k[i, t], v[i, t], t)
+    for g, o in zip(heads, refs):
+        gi, oi = g.info(), o.info()
+        assert (gi["head"], gi["size"]) == (oi["head"], oi["size"])
+        for x, y in zip(g.read_slots(0, oi["size"]), o.read_slots(0, oi["size"])):
+            assert same_bits(x, y)
+    q = rng.standard_normal((H, dim)).astype(np.float32)
+    dq, do = DeviceBuffer(q.nbytes), DeviceBuffer(q.nbytes)
+    dq.upload(q)
+    assert L.adaptq_plan_compute_device(plan, dq.ptr, do.ptr, None) == 0, err()
+    sync()
+    y = do.download((H, dim))
+    r = np.stack([o.compute(q[i])[0] for i, o in enumerate(refs)])
+    assert rel_err(y, r) <= 1e-4
+    L.adaptq_plan_destroy(plan)
+
+
+def test_plan_rejects_mixed_shapes():
+    a = GpuHead(64, 4, 2, 16, 1)
+    b = GpuHead(128, 4, 2, 16, 1)
+    arr = (C.c_void_p * 2)(a.h, b.h)
+    assert not L.adaptq_plan_create(arr, 2)
+    assert "differ" in err()
+
+
+def test_plan_empty_rings_give_zeros():
+    H, dim = 3, 64
+    heads = [GpuHead(dim, 4, 2, 32, i) for i in range(H)]
+    arr = (C.c_void_p * H)(*[h.h for h in heads])
+    plan = L.adaptq_plan_create(arr, H)
+    q = np.ones((H, dim), np.float32)
+    dq, do = DeviceBuffer(q.nbytes), DeviceBuffer(q.nbytes)
+    dq.upload(q)
+    do.upload(np.full((H, dim), 7.0, np.float32))
+    assert L.adaptq_plan_compute_device(plan, dq.ptr, do.ptr, None) == 0, err()
+    sync()
+    assert np.all(do.download((H, dim)) == 0)
+    L.adaptq_plan_destroy(plan)
