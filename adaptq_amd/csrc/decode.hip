@@ -100,7 +100,7 @@ struct KLut {
 };
 template <int VB>
 struct VLut {
-  static constexpr int size = VB == 2 ? 256 * 4 : VB == 4 ? 256 * 2 : VB == 3 ? 64 * 2 : 4;
+  static constexpr int size = VB == 2 ? 32 : VB == 4 ? 16 : VB == 3 ? 8 : 4;
 };
 
 // Rotate the query into shared memory.  Quantised K: qr = H (D . q) (butterfly
@@ -146,25 +146,20 @@ __device__ void build_klut(float *lut, const float *qr) {
   }
 }
 
+// Codebook tables for V, sized so that distinct entries never share an LDS
+// bank: 2-bit: nibble (codes 2k, 2k+1) -> float2; 4-bit: nibble -> float;
+// 3-bit: code -> float.
 template <int VB>
 __device__ void build_vlut(float *lut) {
   if constexpr (VB == 2) {
-    for (int b = threadIdx.x; b < 256; b += blockDim.x) {
-      lut[4 * b] = cbv<2>(b >> 6);
-      lut[4 * b + 1] = cbv<2>((b >> 4) & 3);
-      lut[4 * b + 2] = cbv<2>((b >> 2) & 3);
-      lut[4 * b + 3] = cbv<2>(b & 3);
+    for (int b = threadIdx.x; b < 16; b += blockDim.x) {
+      lut[2 * b] = cbv<2>(b >> 2);
+      lut[2 * b + 1] = cbv<2>(b & 3);
     }
   } else if constexpr (VB == 4) {
-    for (int b = threadIdx.x; b < 256; b += blockDim.x) {
-      lut[2 * b] = cbv<4>(b >> 4);
-      lut[2 * b + 1] = cbv<4>(b & 15);
-    }
+    for (int b = threadIdx.x; b < 16; b += blockDim.x) lut[b] = cbv<4>(b);
   } else if constexpr (VB == 3) {
-    for (int b = threadIdx.x; b < 64; b += blockDim.x) {
-      lut[2 * b] = cbv<3>(b >> 3);
-      lut[2 * b + 1] = cbv<3>(b & 7);
-    }
+    for (int b = threadIdx.x; b < 8; b += blockDim.x) lut[b] = cbv<3>(b);
   }
 }
 
@@ -253,16 +248,78 @@ __device__ void finish_item(float *s_acc, int P, int dim, float L, const uint32_
   }
 }
 
+#define AQ_AS1 __attribute__((address_space(1)))
+#define AQ_AS4 __attribute__((address_space(4)))
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Wave-wide reductions with DPP inside 16-lane rows and readlane across rows
+// (no LDS traffic; the result is wave-uniform).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, true));
+}
+
+template <bool MAX>
+__device__ __forceinline__ float wave_reduce(float v) {
+  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+  v = op(v, dpp<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = op(v, dpp<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = op(v, dpp<0x124>(v));  // row_ror:4
+  v = op(v, dpp<0x128>(v));  // row_ror:8
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return op(op(r0, r1), op(r2, r3));
+}
+
+// Load NB bytes of row t through the global address space into words.
+template <int NB>
+__device__ __forceinline__ void load_row_g(const uint8_t *base, long long t, uint32_t (&w)[NB / 4]) {
+  const AQ_AS1 uint8_t *p = (const AQ_AS1 uint8_t *)base + (size_t)t * NB;
+  if constexpr (NB % 16 == 0) {
+#pragma unroll
+    for (int i = 0; i < NB / 16; ++i) {
+      const u32x4 v = reinterpret_cast<const AQ_AS1 u32x4 *>(p)[i];
+      w[4 * i] = v.x;
+      w[4 * i + 1] = v.y;
+      w[4 * i + 2] = v.z;
+      w[4 * i + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NB / 8; ++i) {
+      const u32x2 v = reinterpret_cast<const AQ_AS1 u32x2 *>(p)[i];
+      w[2 * i] = v.x;
+      w[2 * i + 1] = v.y;
+    }
+  }
+}
+
 // With n_splits == 1 the block owns its item and writes the final output
 // (outs) directly; otherwise it writes a partial for finalize_kernel.
+//
+// One lane per token.  K: byte lookup table (LDS), one read per code byte.
+// V: per-lane accumulators acc[P] fed from codebook tables small enough that
+// distinct entries sit in distinct LDS banks (no bank conflicts):
+//   2-bit: nibble (2 codes) -> float2, 16 entries
+//   4-bit: nibble (1 code)  -> float, 16 entries
+//   3-bit: code             -> float, 8 entries
+// The next tile's K row and scales are loaded while the current tile is
+// reduced.
 template <int P, int KB, int VB, bool RAW>
 __global__ __launch_bounds__(kThreads, 2) void decode_lut_kernel(
     HeadDesc *const *item_desc, const float *__restrict__ queries, int chunk, int n_splits,
     float *__restrict__ partials, float *__restrict__ outs) {
   constexpr bool KQ = KB != 16;
   constexpr bool VQ = VB != 16;
-  constexpr int KNB = RAW ? 0 : RowBytes<P, KB>::value;
-  constexpr int VNB = RAW ? 0 : RowBytes<P, VB>::value;
+  constexpr int KNB = RAW ? 4 * P : RowBytes<P, KB>::value;
+  constexpr int VNB = RAW ? 4 * P : RowBytes<P, VB>::value;
+  constexpr int KW = KQ ? KNB / 4 : 1;
   __shared__ float s_q[P];
   __shared__ float s_klut[KLut<P, KB>::size];
   __shared__ __align__(16) float s_vlut[VLut<VB>::size];
@@ -270,15 +327,18 @@ __global__ __launch_bounds__(kThreads, 2) void decode_lut_kernel(
   __shared__ float s_ml[kWaves][2];
 
   const int item = blockIdx.y, split = blockIdx.x;
-  const HeadDesc *d = item_desc[item];
-  const ItemView iv = item_view<RAW>(d);
+  // Descriptor fields are read through the constant address space so they
+  // load as scalars (a generic-pointer load is assumed divergent).
+  const AQ_AS4 HeadDesc *d =
+      (const AQ_AS4 HeadDesc *)((const AQ_AS4 uint64_t *)item_desc)[item];
   const int dim = d->dim;
-  const int n = iv.n;
+  const int n = d->st.size;
   const int t_begin = split * chunk;
   const int t_end = min(n, t_begin + chunk);
   float *part = partials + ((size_t)item * n_splits + split) * (P + 4);
-
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t *signs = (const uint32_t *)d->signs;
   if (t_begin >= t_end) {
     if (n_splits == 1) {
       for (int i = threadIdx.x; i < dim; i += blockDim.x) outs[(size_t)item * dim + i] = 0.0f;
@@ -292,60 +352,81 @@ __global__ __launch_bounds__(kThreads, 2) void decode_lut_kernel(
     return;
   }
 
-  load_query<P>(s_q, queries + (size_t)item * dim, dim, KQ, d->signs);
+  load_query<P>(s_q, queries + (size_t)item * dim, dim, KQ, signs);
   if constexpr (KQ) build_klut<P, KB>(s_klut, s_q);
   if constexpr (VQ) build_vlut<VB>(s_vlut);
   __syncthreads();
 
   const float attn_s = KQ ? 1.0f / (sqrtf((float)dim) * (float)P) : 1.0f / sqrtf((float)dim);
   const float isp = VQ ? 1.0f / sqrtf((float)P) : 1.0f;
-  // Raw rows hold dim floats; this kernel sees them only when dim == P.
-  const int stride_f = P;
+  const uint8_t *k_rows = RAW ? (const uint8_t *)d->raw_k : (const uint8_t *)d->k_codes;
+  const uint8_t *v_rows = RAW ? (const uint8_t *)d->raw_v : (const uint8_t *)d->v_codes;
+  const AQ_AS1 float *k_scale = (const AQ_AS1 float *)d->k_scale;
+  const AQ_AS1 float *v_scale = (const AQ_AS1 float *)d->v_scale;
 
   float acc[P];
 #pragma unroll
   for (int i = 0; i < P; ++i) acc[i] = 0.0f;
   float m_run = -INFINITY, l_run = 0.0f;
 
-  for (int base = t_begin + wave * kTile; base < t_end; base += kWaves * kTile) {
+  int base = t_begin + wave * kTile;
+  uint32_t kw[KW];
+  float ks = 1.0f, vs = 1.0f;
+  auto fetch = [&](int b) {
+    const int t = min(b + lane, t_end - 1);
+    if constexpr (KQ) load_row_g<KNB>(k_rows, t, kw);
+    if constexpr (!RAW) {
+      ks = k_scale[t];
+      vs = v_scale[t];
+    }
+  };
+  if (base < t_end) fetch(base);
+
+  for (; base < t_end; base += kWaves * kTile) {
     const int t = base + lane;
     const bool valid = t < t_end;
     const int tt = valid ? t : t_end - 1;
+    uint32_t kc[KW];
+#pragma unroll
+    for (int i = 0; i < KW; ++i) kc[i] = kw[i];
+    const float ksc = ks, vsc = vs;
+    if (base + kWaves * kTile < t_end) fetch(base + kWaves * kTile);
 
-    // ---- logits ----
-    float dot = 0.0f;
+    // V row load issued before the K reduction so its latency overlaps it.
+    uint32_t vw[VQ ? VNB / 4 : 1];
+    if constexpr (VQ) load_row_g<VNB>(v_rows, tt, vw);
+
+    // ---- logit ----
+    float dot;
     if constexpr (KQ) {
-      uint32_t w[KNB / 4];
-      load_row<KNB>(iv.k_rows, tt, w);
-      float part4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      float p4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
       if constexpr (KB == 3) {
 #pragma unroll
         for (int g = 0; g < P / 8; ++g)
 #pragma unroll
-          for (int m = 0; m < 4; ++m) part4[m] += s_klut[(4 * g + m) * 64 + pair3(w, g, m)];
+          for (int m = 0; m < 4; ++m) p4[m] += s_klut[(4 * g + m) * 64 + pair3(kc, g, m)];
       } else {
 #pragma unroll
-        for (int j = 0; j < KNB; ++j) part4[j & 3] += s_klut[j * 256 + byte_of(w, j)];
+        for (int j = 0; j < KNB; ++j) p4[j & 3] += s_klut[j * 256 + byte_of(kc, j)];
       }
-      dot = (part4[0] + part4[1]) + (part4[2] + part4[3]);
-      dot = dot * attn_s * iv.k_scale[tt];
+      dot = ((p4[0] + p4[1]) + (p4[2] + p4[3])) * attn_s * ksc;
     } else {
-      const float *kr = reinterpret_cast<const float *>(iv.k_rows) + (size_t)tt * stride_f;
-      float part4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      const AQ_AS1 float *kr = (const AQ_AS1 float *)k_rows + (size_t)tt * P;
+      float p4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int i = 0; i < P; i += 4) {
-        const float4 k4 = *reinterpret_cast<const float4 *>(kr + i);
-        part4[0] = fmaf(s_q[i], k4.x, part4[0]);
-        part4[1] = fmaf(s_q[i + 1], k4.y, part4[1]);
-        part4[2] = fmaf(s_q[i + 2], k4.z, part4[2]);
-        part4[3] = fmaf(s_q[i + 3], k4.w, part4[3]);
+        const f32x4 k4 = *reinterpret_cast<const AQ_AS1 f32x4 *>(kr + i);
+        p4[0] = fmaf(s_q[i], k4.x, p4[0]);
+        p4[1] = fmaf(s_q[i + 1], k4.y, p4[1]);
+        p4[2] = fmaf(s_q[i + 2], k4.z, p4[2]);
+        p4[3] = fmaf(s_q[i + 3], k4.w, p4[3]);
       }
-      dot = ((part4[0] + part4[1]) + (part4[2] + part4[3])) * attn_s;
+      dot = ((p4[0] + p4[1]) + (p4[2] + p4[3])) * attn_s;
     }
     const float logit = valid ? dot : -INFINITY;
 
     // ---- online softmax (wave-uniform running max) ----
-    const float tmax = wave_max(logit);
+    const float tmax = wave_reduce<true>(logit);
     if (tmax > m_run) {
       const float alpha = m_run == -INFINITY ? 0.0f : expf(m_run - tmax);
 #pragma unroll
@@ -353,46 +434,46 @@ __global__ __launch_bounds__(kThreads, 2) void decode_lut_kernel(
       l_run *= alpha;
       m_run = tmax;
     }
-    if (!valid) continue;
-    const float e = expf(logit - m_run);
+    const float e = valid ? expf(logit - m_run) : 0.0f;
     l_run += e;
+    if (!valid) continue;
 
     // ---- V accumulate ----
     if constexpr (VQ) {
-      const float wgt = e * iv.v_scale[tt] * isp;
-      uint32_t w[VNB / 4];
-      load_row<VNB>(iv.v_rows, tt, w);
+      const float wgt = e * vsc * isp;
       if constexpr (VB == 2) {
+        const f32x2 *t2 = reinterpret_cast<const f32x2 *>(s_vlut);
 #pragma unroll
         for (int j = 0; j < VNB; ++j) {
-          const float4 c = reinterpret_cast<const float4 *>(s_vlut)[byte_of(w, j)];
-          acc[4 * j] = fmaf(c.x, wgt, acc[4 * j]);
-          acc[4 * j + 1] = fmaf(c.y, wgt, acc[4 * j + 1]);
-          acc[4 * j + 2] = fmaf(c.z, wgt, acc[4 * j + 2]);
-          acc[4 * j + 3] = fmaf(c.w, wgt, acc[4 * j + 3]);
+          const uint32_t bj = byte_of(vw, j);
+          const f32x2 hi = t2[bj >> 4], lo = t2[bj & 15];
+          acc[4 * j] = fmaf(hi.x, wgt, acc[4 * j]);
+          acc[4 * j + 1] = fmaf(hi.y, wgt, acc[4 * j + 1]);
+          acc[4 * j + 2] = fmaf(lo.x, wgt, acc[4 * j + 2]);
+          acc[4 * j + 3] = fmaf(lo.y, wgt, acc[4 * j + 3]);
         }
       } else if constexpr (VB == 4) {
 #pragma unroll
         for (int j = 0; j < VNB; ++j) {
-          const float2 c = reinterpret_cast<const float2 *>(s_vlut)[byte_of(w, j)];
-          acc[2 * j] = fmaf(c.x, wgt, acc[2 * j]);
-          acc[2 * j + 1] = fmaf(c.y, wgt, acc[2 * j + 1]);
+          const uint32_t bj = byte_of(vw, j);
+          acc[2 * j] = fmaf(s_vlut[bj >> 4], wgt, acc[2 * j]);
+          acc[2 * j + 1] = fmaf(s_vlut[bj & 15], wgt, acc[2 * j + 1]);
         }
       } else {
 #pragma unroll
-        for (int g = 0; g < P / 8; ++g)
+        for (int g = 0; g < P / 8; ++g) {
+          const uint32_t w24 = (byte_of(vw, 3 * g) << 16) | (byte_of(vw, 3 * g + 1) << 8) |
+                               byte_of(vw, 3 * g + 2);
 #pragma unroll
-          for (int m = 0; m < 4; ++m) {
-            const float2 c = reinterpret_cast<const float2 *>(s_vlut)[pair3(w, g, m)];
-            acc[8 * g + 2 * m] = fmaf(c.x, wgt, acc[8 * g + 2 * m]);
-            acc[8 * g + 2 * m + 1] = fmaf(c.y, wgt, acc[8 * g + 2 * m + 1]);
-          }
+          for (int k = 0; k < 8; ++k)
+            acc[8 * g + k] = fmaf(s_vlut[(w24 >> (21 - 3 * k)) & 7u], wgt, acc[8 * g + k]);
+        }
       }
     } else {
-      const float *vr = reinterpret_cast<const float *>(iv.v_rows) + (size_t)tt * stride_f;
+      const AQ_AS1 float *vr = (const AQ_AS1 float *)v_rows + (size_t)tt * P;
 #pragma unroll
       for (int i = 0; i < P; i += 4) {
-        const float4 v4 = *reinterpret_cast<const float4 *>(vr + i);
+        const f32x4 v4 = *reinterpret_cast<const AQ_AS1 f32x4 *>(vr + i);
         acc[i] = fmaf(v4.x, e, acc[i]);
         acc[i + 1] = fmaf(v4.y, e, acc[i + 1]);
         acc[i + 2] = fmaf(v4.z, e, acc[i + 2]);
@@ -402,7 +483,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_lut_kernel(
   }
 
   // ---- block merge: waves -> one (m, l, acc) ----
-  const float l_w = wave_sum(l_run);
+  const float l_w = wave_reduce<false>(l_run);
   wave_reduce_scatter<P>(acc, lane);
 #pragma unroll
   for (int k = 0; k < P / 64; ++k) s_red[wave][lane * (P / 64) + k] = acc[k];
@@ -429,7 +510,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_lut_kernel(
       s_q[i] = a;
     }
     __syncthreads();
-    finish_item<VQ && !RAW>(s_q, P, dim, L, d->signs, outs + (size_t)item * dim);
+    finish_item<VQ && !RAW>(s_q, P, dim, L, signs, outs + (size_t)item * dim);
     return;
   }
   for (int i = threadIdx.x; i < P; i += blockDim.x) {
@@ -630,10 +711,10 @@ struct SplitPlan {
   int splits, chunk;
 };
 
-SplitPlan plan_splits(int n_items, int max_n) {
+SplitPlan plan_splits(int n_items, int max_n, int min_chunk = 256) {
   SplitPlan sp;
   const int target_blocks = 1024;
-  int by_work = (max_n + 255) / 256;
+  int by_work = (max_n + min_chunk - 1) / min_chunk;
   if (by_work < 1) by_work = 1;
   int want = (target_blocks + n_items - 1) / n_items;
   sp.splits = want < by_work ? want : by_work;
@@ -700,10 +781,9 @@ hipError_t launch_decode(HeadDesc *const *descs, int n_items, const DecodeShape 
   DecodeShape sh = shape;
   if (sh.raw) sh.k_bits = sh.v_bits = 16;  // the mirror holds fp32 keys and values
   const int max_n = sh.max_n > 0 ? sh.max_n : 1;
+  const bool raw = sh.raw;
   const SplitPlan sp = plan_splits(n_items, max_n);
   const dim3 grid(sp.splits, n_items);
-  const bool raw = sh.raw;
-  // Raw rows hold dim floats; the LUT kernel handles them when dim == padded.
   const bool lut_ok = (sh.padded == 64 || sh.padded == 128) && (!raw || sh.dim == sh.padded);
   hipError_t e;
   if (lut_ok) {

@@ -113,6 +113,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 1 GiB device copy 5 times (scales rocprof "
+                         "FETCH_SIZE/WRITE_SIZE readings to bytes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: every box in this setup has one GPU and the "
@@ -122,6 +125,15 @@ def main():
 
     import numpy as np
     import torch  # loads torch's HIP runtime first; libadaptq binds to the same one
+
+    if args.copy_calibration:
+        x = torch.ones(1 << 28, device="cuda:0")  # 1 GiB of fp32
+        y = torch.empty_like(x)
+        for _ in range(5):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": x.numel() * 4, "launches": 5}))
+        return
 
     sys.path.insert(0, ROOT)
     from adaptq_amd import _lib
