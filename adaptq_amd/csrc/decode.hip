@@ -300,19 +300,85 @@ __device__ __forceinline__ void load_row_g(const uint8_t *base, long long t, uin
   }
 }
 
+// Bytes of LDS reserved in front of the K lookup table for the V codebook
+// table, so that both are addressed with the 16-bit immediate offset of
+// ds_read (the K table of padded 128 fills 64 KB by itself).
+constexpr int kVlutBytes = 256;
+
+// LUT kernel geometry: 8 waves per block share one K table; a wave streams
+// 64-token tiles.
+constexpr int kLutWaves = 8;
+constexpr int kLutThreads = 64 * kLutWaves;
+
+// Half-row V accumulation for one token: acc[0..P/2) += wgt * CB_V[codes]
+// over the P/2 dimensions held in vw (P/2 * VB / 8 bytes).  Table addresses
+// come from pre-shifted code words so each nibble or code costs one masked
+// byte select (SDWA) and one LDS read.
+template <int P, int VB>
+__device__ __forceinline__ void vhalf_accumulate(float (&acc)[P / 2], const uint32_t *vw,
+                                                 float wgt, const uint8_t *lds) {
+  constexpr int HB = (P / 2) * VB / 8;  // bytes in a half row
+  if constexpr (VB == 2) {
+    // nibble n of byte j -> float2 at n*8: codes (dims) 4j,4j+1 | 4j+2,4j+3
+#pragma unroll
+    for (int q = 0; q < HB / 4; ++q) {
+      const uint32_t xh = vw[q] >> 1, xl = vw[q] << 3;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int j = 4 * q + k;
+        const uint32_t ah = (xh >> (8 * k)) & 0x78u, al = (xl >> (8 * k)) & 0x78u;
+        const f32x2 hi = *reinterpret_cast<const f32x2 *>(lds + ah);
+        const f32x2 lo = *reinterpret_cast<const f32x2 *>(lds + al);
+        acc[4 * j] = fmaf(hi.x, wgt, acc[4 * j]);
+        acc[4 * j + 1] = fmaf(hi.y, wgt, acc[4 * j + 1]);
+        acc[4 * j + 2] = fmaf(lo.x, wgt, acc[4 * j + 2]);
+        acc[4 * j + 3] = fmaf(lo.y, wgt, acc[4 * j + 3]);
+      }
+    }
+  } else if constexpr (VB == 4) {
+    // nibble -> float at n*4: dims 2j (high nibble), 2j+1 (low nibble)
+#pragma unroll
+    for (int q = 0; q < HB / 4; ++q) {
+      const uint32_t xh = vw[q] >> 2, xl = vw[q] << 2;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int j = 4 * q + k;
+        const uint32_t ah = (xh >> (8 * k)) & 0x3Cu, al = (xl >> (8 * k)) & 0x3Cu;
+        acc[2 * j] = fmaf(*reinterpret_cast<const float *>(lds + ah), wgt, acc[2 * j]);
+        acc[2 * j + 1] = fmaf(*reinterpret_cast<const float *>(lds + al), wgt, acc[2 * j + 1]);
+      }
+    }
+  } else {
+    // 3-bit: 8 codes per 24-bit big-endian group -> float at c*4
+#pragma unroll
+    for (int g = 0; g < P / 16; ++g) {
+      const uint32_t w24 = (byte_of(vw, 3 * g) << 16) | (byte_of(vw, 3 * g + 1) << 8) |
+                           byte_of(vw, 3 * g + 2);
+      const uint32_t w26 = w24 << 2;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t a = (w26 >> (21 - 3 * k)) & 0x1Cu;
+        acc[8 * g + k] = fmaf(*reinterpret_cast<const float *>(lds + a), wgt, acc[8 * g + k]);
+      }
+    }
+  }
+}
+
 // With n_splits == 1 the block owns its item and writes the final output
 // (outs) directly; otherwise it writes a partial for finalize_kernel.
 //
-// One lane per token.  K: byte lookup table (LDS), one read per code byte.
-// V: per-lane accumulators acc[P] fed from codebook tables small enough that
-// distinct entries sit in distinct LDS banks (no bank conflicts):
+// One lane per token for K: a byte lookup table in LDS gives one read per
+// code byte.  For V, lanes L and L+32 pair up: after a v_permlane32_swap the
+// lower lane holds the first half of the V rows of tokens L and L+32 and the
+// upper lane the second halves, so each lane keeps P/2 accumulators (half
+// the registers of one-token-per-lane accumulation, hence twice the
+// occupancy) and does the same number of FMAs.  V codebook tables are small
+// enough that distinct entries sit in distinct LDS banks:
 //   2-bit: nibble (2 codes) -> float2, 16 entries
 //   4-bit: nibble (1 code)  -> float, 16 entries
 //   3-bit: code             -> float, 8 entries
-// The next tile's K row and scales are loaded while the current tile is
-// reduced.
 template <int P, int KB, int VB, bool RAW>
-__global__ __launch_bounds__(kThreads, 2) void decode_lut_kernel(
+__global__ __launch_bounds__(kLutThreads, 2) void decode_lut_kernel(
     HeadDesc *const *item_desc, const float *__restrict__ queries, int chunk, int n_splits,
     float *__restrict__ partials, float *__restrict__ outs) {
   constexpr bool KQ = KB != 16;
@@ -320,11 +386,15 @@ __global__ __launch_bounds__(kThreads, 2) void decode_lut_kernel(
   constexpr int KNB = RAW ? 4 * P : RowBytes<P, KB>::value;
   constexpr int VNB = RAW ? 4 * P : RowBytes<P, VB>::value;
   constexpr int KW = KQ ? KNB / 4 : 1;
+  constexpr int VW = VQ ? VNB / 4 : 1;
+  constexpr int H = P / 2;
+  // LDS: [V table | K table | query | per-wave partials]
+  __shared__ __align__(16) uint8_t s_mem[kVlutBytes + 4 * KLut<P, KB>::size];
   __shared__ float s_q[P];
-  __shared__ float s_klut[KLut<P, KB>::size];
-  __shared__ __align__(16) float s_vlut[VLut<VB>::size];
-  __shared__ float s_red[kWaves][P];
-  __shared__ float s_ml[kWaves][2];
+  __shared__ float s_red[kLutWaves][P];
+  __shared__ float s_ml[kLutWaves][2];
+  float *s_vlut = reinterpret_cast<float *>(s_mem);
+  float *s_klut = reinterpret_cast<float *>(s_mem + kVlutBytes);
 
   const int item = blockIdx.y, split = blockIdx.x;
   // Descriptor fields are read through the constant address space so they
@@ -337,6 +407,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_lut_kernel(
   const int t_end = min(n, t_begin + chunk);
   float *part = partials + ((size_t)item * n_splits + split) * (P + 4);
   const int lane = threadIdx.x & 63;
+  const bool upper = lane >= 32;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t *signs = (const uint32_t *)d->signs;
   if (t_begin >= t_end) {
@@ -364,39 +435,23 @@ __global__ __launch_bounds__(kThreads, 2) void decode_lut_kernel(
   const AQ_AS1 float *k_scale = (const AQ_AS1 float *)d->k_scale;
   const AQ_AS1 float *v_scale = (const AQ_AS1 float *)d->v_scale;
 
-  float acc[P];
+  float acc[H];
 #pragma unroll
-  for (int i = 0; i < P; ++i) acc[i] = 0.0f;
+  for (int i = 0; i < H; ++i) acc[i] = 0.0f;
   float m_run = -INFINITY, l_run = 0.0f;
 
-  int base = t_begin + wave * kTile;
-  uint32_t kw[KW];
-  float ks = 1.0f, vs = 1.0f;
-  auto fetch = [&](int b) {
-    const int t = min(b + lane, t_end - 1);
-    if constexpr (KQ) load_row_g<KNB>(k_rows, t, kw);
-    if constexpr (!RAW) {
-      ks = k_scale[t];
-      vs = v_scale[t];
-    }
-  };
-  if (base < t_end) fetch(base);
-
-  for (; base < t_end; base += kWaves * kTile) {
+  for (int base = t_begin + wave * kTile; base < t_end; base += kLutWaves * kTile) {
     const int t = base + lane;
     const bool valid = t < t_end;
     const int tt = valid ? t : t_end - 1;
     uint32_t kc[KW];
-#pragma unroll
-    for (int i = 0; i < KW; ++i) kc[i] = kw[i];
-    const float ksc = ks, vsc = vs;
-    if (base + kWaves * kTile < t_end) fetch(base + kWaves * kTile);
-
-    // V row load issued before the K reduction so its latency overlaps it.
-    uint32_t vw[VQ ? VNB / 4 : 1];
+    if constexpr (KQ) load_row_g<KNB>(k_rows, tt, kc);
+    uint32_t vw[VW];
     if constexpr (VQ) load_row_g<VNB>(v_rows, tt, vw);
+    const float ksc = RAW ? 1.0f : k_scale[tt];
+    const float vsc = RAW ? 1.0f : v_scale[tt];
 
-    // ---- logit ----
+    // ---- logit of token t ----
     float dot;
     if constexpr (KQ) {
       float p4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -411,7 +466,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_lut_kernel(
       }
       dot = ((p4[0] + p4[1]) + (p4[2] + p4[3])) * attn_s * ksc;
     } else {
-      const AQ_AS1 float *kr = (const AQ_AS1 float *)k_rows + (size_t)tt * P;
+      const AQ_AS1 float *kr = (const AQ_AS1 float *)k_rows + (size_t)tt * (RAW ? dim : P);
       float p4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int i = 0; i < P; i += 4) {
@@ -430,63 +485,73 @@ __global__ __launch_bounds__(kThreads, 2) void decode_lut_kernel(
     if (tmax > m_run) {
       const float alpha = m_run == -INFINITY ? 0.0f : expf(m_run - tmax);
 #pragma unroll
-      for (int i = 0; i < P; ++i) acc[i] *= alpha;
+      for (int i = 0; i < H; ++i) acc[i] *= alpha;
       l_run *= alpha;
       m_run = tmax;
     }
     const float e = valid ? expf(logit - m_run) : 0.0f;
     l_run += e;
-    if (!valid) continue;
+    const float wgt = VQ ? e * vsc * isp : e;
 
-    // ---- V accumulate ----
+    // ---- V: exchange half rows with the partner lane, accumulate ----
+    // (w0, x0): token L (lower lanes) / token L-32 (upper lanes);
+    // (w1, x1): token L+32 (lower) / token L (upper).
+    const auto wsw = __builtin_amdgcn_permlane32_swap(__float_as_uint(wgt), __float_as_uint(wgt),
+                                                      false, false);
+    const float w0 = upper ? __uint_as_float(wsw[0]) : wgt;
+    const float w1 = upper ? wgt : __uint_as_float(wsw[1]);
     if constexpr (VQ) {
-      const float wgt = e * vsc * isp;
-      if constexpr (VB == 2) {
-        const f32x2 *t2 = reinterpret_cast<const f32x2 *>(s_vlut);
+      uint32_t x0[VW / 2], x1[VW / 2];
 #pragma unroll
-        for (int j = 0; j < VNB; ++j) {
-          const uint32_t bj = byte_of(vw, j);
-          const f32x2 hi = t2[bj >> 4], lo = t2[bj & 15];
-          acc[4 * j] = fmaf(hi.x, wgt, acc[4 * j]);
-          acc[4 * j + 1] = fmaf(hi.y, wgt, acc[4 * j + 1]);
-          acc[4 * j + 2] = fmaf(lo.x, wgt, acc[4 * j + 2]);
-          acc[4 * j + 3] = fmaf(lo.y, wgt, acc[4 * j + 3]);
-        }
-      } else if constexpr (VB == 4) {
-#pragma unroll
-        for (int j = 0; j < VNB; ++j) {
-          const uint32_t bj = byte_of(vw, j);
-          acc[2 * j] = fmaf(s_vlut[bj >> 4], wgt, acc[2 * j]);
-          acc[2 * j + 1] = fmaf(s_vlut[bj & 15], wgt, acc[2 * j + 1]);
-        }
-      } else {
-#pragma unroll
-        for (int g = 0; g < P / 8; ++g) {
-          const uint32_t w24 = (byte_of(vw, 3 * g) << 16) | (byte_of(vw, 3 * g + 1) << 8) |
-                               byte_of(vw, 3 * g + 2);
-#pragma unroll
-          for (int k = 0; k < 8; ++k)
-            acc[8 * g + k] = fmaf(s_vlut[(w24 >> (21 - 3 * k)) & 7u], wgt, acc[8 * g + k]);
-        }
+      for (int i = 0; i < VW / 2; ++i) {
+        const auto r = __builtin_amdgcn_permlane32_swap(vw[i], vw[VW / 2 + i], false, false);
+        x0[i] = r[0];
+        x1[i] = r[1];
       }
+      // invalid tokens carry weight 0 and valid (clamped) codes
+      vhalf_accumulate<P, VB>(acc, x0, w0, s_mem);
+      vhalf_accumulate<P, VB>(acc, x1, w1, s_mem);
     } else {
-      const AQ_AS1 float *vr = (const AQ_AS1 float *)v_rows + (size_t)tt * P;
+      const AQ_AS1 float *vr = (const AQ_AS1 float *)v_rows;
+      const int stride = RAW ? dim : P;
+      const int tok0 = min((upper ? base + lane - 32 : base + lane), t_end - 1);
+      const int tok1 = min((upper ? base + lane : base + lane + 32), t_end - 1);
+      const int off = upper ? H : 0;
 #pragma unroll
-      for (int i = 0; i < P; i += 4) {
-        const f32x4 v4 = *reinterpret_cast<const AQ_AS1 f32x4 *>(vr + i);
-        acc[i] = fmaf(v4.x, e, acc[i]);
-        acc[i + 1] = fmaf(v4.y, e, acc[i + 1]);
-        acc[i + 2] = fmaf(v4.z, e, acc[i + 2]);
-        acc[i + 3] = fmaf(v4.w, e, acc[i + 3]);
+      for (int i = 0; i < H; i += 4) {
+        const f32x4 a4 = *reinterpret_cast<const AQ_AS1 f32x4 *>(vr + (size_t)tok0 * stride + off + i);
+        const f32x4 b4 = *reinterpret_cast<const AQ_AS1 f32x4 *>(vr + (size_t)tok1 * stride + off + i);
+        acc[i] = fmaf(b4.x, w1, fmaf(a4.x, w0, acc[i]));
+        acc[i + 1] = fmaf(b4.y, w1, fmaf(a4.y, w0, acc[i + 1]));
+        acc[i + 2] = fmaf(b4.z, w1, fmaf(a4.z, w0, acc[i + 2]));
+        acc[i + 3] = fmaf(b4.w, w1, fmaf(a4.w, w0, acc[i + 3]));
       }
     }
   }
 
   // ---- block merge: waves -> one (m, l, acc) ----
+  // l_run: every token's e is held by its own lane once.
   const float l_w = wave_reduce<false>(l_run);
-  wave_reduce_scatter<P>(acc, lane);
+  // reduce acc[H] over the 32 lanes of each half-wave: lane L ends with the
+  // totals of dimensions 2(L%32), 2(L%32)+1 (+H for the upper half)
 #pragma unroll
-  for (int k = 0; k < P / 64; ++k) s_red[wave][lane * (P / 64) + k] = acc[k];
+  for (int step = 0; step < 5; ++step) {
+    const int m = 16 >> step;
+    const int half = H >> (step + 1);
+    const uint32_t up = (lane & m) ? 0xFFFFFFFFu : 0u;
+#pragma unroll
+    for (int j = 0; j < half; ++j) {
+      const uint32_t a = __float_as_uint(acc[j]), bb = __float_as_uint(acc[j + half]);
+      const float send = __uint_as_float((a & up) | (bb & ~up));
+      const float keep = __uint_as_float((bb & up) | (a & ~up));
+      acc[j] = keep + __shfl_xor(send, m, 64);
+    }
+  }
+  {
+    const int d0 = (upper ? H : 0) + (H / 32) * (lane & 31);
+#pragma unroll
+    for (int k = 0; k < H / 32; ++k) s_red[wave][d0 + k] = acc[k];
+  }
   if (lane == 0) {
     s_ml[wave][0] = m_run;
     s_ml[wave][1] = l_w;
@@ -494,10 +559,10 @@ __global__ __launch_bounds__(kThreads, 2) void decode_lut_kernel(
   __syncthreads();
   float M = -INFINITY;
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_ml[w][0]);
-  float f[kWaves], L = 0.0f;
+  for (int w = 0; w < kLutWaves; ++w) M = fmaxf(M, s_ml[w][0]);
+  float f[kLutWaves], L = 0.0f;
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
+  for (int w = 0; w < kLutWaves; ++w) {
     f[w] = s_ml[w][0] == -INFINITY ? 0.0f : expf(s_ml[w][0] - M);
     L += f[w] * s_ml[w][1];
   }
@@ -506,7 +571,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_lut_kernel(
     for (int i = threadIdx.x; i < P; i += blockDim.x) {
       float a = 0.0f;
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) a += f[w] * s_red[w][i];
+      for (int w = 0; w < kLutWaves; ++w) a += f[w] * s_red[w][i];
       s_q[i] = a;
     }
     __syncthreads();
@@ -516,7 +581,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_lut_kernel(
   for (int i = threadIdx.x; i < P; i += blockDim.x) {
     float a = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) a += f[w] * s_red[w][i];
+    for (int w = 0; w < kLutWaves; ++w) a += f[w] * s_red[w][i];
     part[4 + i] = a;
   }
   if (threadIdx.x == 0) {
@@ -733,7 +798,7 @@ hipError_t dispatch_lut(const DecodeShape &sh, dim3 grid, HeadDesc *const *descs
                         int chunk, int splits, float *part, float *out, hipStream_t s) {
 #define AQ_LUT(KB_, VB_)                                                                         \
   if (sh.k_bits == KB_ && sh.v_bits == VB_) {                                                     \
-    decode_lut_kernel<P, KB_, VB_, RAW><<<grid, kThreads, 0, s>>>(descs, q, chunk, splits, part, out); \
+    decode_lut_kernel<P, KB_, VB_, RAW><<<grid, kLutThreads, 0, s>>>(descs, q, chunk, splits, part, out); \
     return hipGetLastError();                                                                     \
   }
   if constexpr (RAW) {
@@ -768,10 +833,21 @@ hipError_t dispatch_generic(const DecodeShape &sh, dim3 grid, HeadDesc *const *d
   return hipErrorInvalidValue;
 }
 
+// The LUT kernel serves padded 64/128 (raw mirrors only when unpadded);
+// everything else takes the generic kernel.
+bool lut_eligible(const DecodeShape &sh) {
+  return (sh.padded == 64 || sh.padded == 128) && (!sh.raw || sh.dim == sh.padded);
+}
+
+SplitPlan decode_plan(int n_items, const DecodeShape &sh) {
+  const int max_n = sh.max_n > 0 ? sh.max_n : 1;
+  return plan_splits(n_items, max_n, lut_eligible(sh) ? kLutWaves * kTile : 256);
+}
+
 }  // namespace
 
 size_t decode_workspace_floats(int n_items, const DecodeShape &sh) {
-  const SplitPlan sp = plan_splits(n_items, sh.max_n > 0 ? sh.max_n : 1);
+  const SplitPlan sp = decode_plan(n_items, sh);
   return (size_t)n_items * sp.splits * (sh.padded + 4);
 }
 
@@ -780,11 +856,10 @@ hipError_t launch_decode(HeadDesc *const *descs, int n_items, const DecodeShape 
   if (n_items <= 0) return hipSuccess;
   DecodeShape sh = shape;
   if (sh.raw) sh.k_bits = sh.v_bits = 16;  // the mirror holds fp32 keys and values
-  const int max_n = sh.max_n > 0 ? sh.max_n : 1;
   const bool raw = sh.raw;
-  const SplitPlan sp = plan_splits(n_items, max_n);
+  const bool lut_ok = lut_eligible(sh);
+  const SplitPlan sp = decode_plan(n_items, sh);
   const dim3 grid(sp.splits, n_items);
-  const bool lut_ok = (sh.padded == 64 || sh.padded == 128) && (!raw || sh.dim == sh.padded);
   hipError_t e;
   if (lut_ok) {
     if (sh.padded == 64)
