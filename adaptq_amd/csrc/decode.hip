@@ -300,6 +300,34 @@ __device__ __forceinline__ void load_row_g(const uint8_t *base, long long t, uin
   }
 }
 
+// byte K of x, ANDed with m, in one instruction (SDWA source select).  The
+// compiler splits (x >> 8K) & m into a shift or bit-field extract plus an
+// AND, because SDWA takes no literal operands.
+template <int K>
+__device__ __forceinline__ uint32_t and_byte(uint32_t x, uint32_t m) {
+  uint32_t r;
+  if constexpr (K == 0)
+    asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0 src1_sel:DWORD"
+        : "=v"(r) : "v"(x), "v"(m));
+  else if constexpr (K == 1)
+    asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1 src1_sel:DWORD"
+        : "=v"(r) : "v"(x), "v"(m));
+  else if constexpr (K == 2)
+    asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2 src1_sel:DWORD"
+        : "=v"(r) : "v"(x), "v"(m));
+  else
+    asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3 src1_sel:DWORD"
+        : "=v"(r) : "v"(x), "v"(m));
+  return r;
+}
+
+template <int K>
+__device__ __forceinline__ void vq_addr(uint32_t xh, uint32_t xl, uint32_t m, uint32_t &ah,
+                                        uint32_t &al) {
+  ah = and_byte<K>(xh, m);
+  al = and_byte<K>(xl, m);
+}
+
 // Bytes of LDS reserved in front of the K lookup table for the V codebook
 // table, so that both are addressed with the 16-bit immediate offset of
 // ds_read (the K table of padded 128 fills 64 KB by itself).
@@ -310,25 +338,30 @@ constexpr int kVlutBytes = 256;
 constexpr int kLutWaves = 8;
 constexpr int kLutThreads = 64 * kLutWaves;
 
-// Half-row V accumulation for one token: acc[0..P/2) += wgt * CB_V[codes]
-// over the P/2 dimensions held in vw (P/2 * VB / 8 bytes).  Table addresses
-// come from pre-shifted code words so each nibble or code costs one masked
-// byte select (SDWA) and one LDS read.
-template <int P, int VB>
-__device__ __forceinline__ void vhalf_accumulate(float (&acc)[P / 2], const uint32_t *vw,
-                                                 float wgt, const uint8_t *lds) {
-  constexpr int HB = (P / 2) * VB / 8;  // bytes in a half row
+// V accumulation of one row segment of one token: acc[0..D) += wgt *
+// CB_V[codes] over the D dimensions held in vw (D * VB / 8 bytes, a whole
+// number of 32-bit words).  Table addresses come from pre-shifted code words
+// so each nibble or code costs one masked byte select (SDWA) and one LDS
+// read.
+template <int D, int VB>
+__device__ __forceinline__ void vseg_accumulate(float (&acc)[D], const uint32_t *vw, float wgt,
+                                                const uint8_t *lds, uint32_t mask) {
+  constexpr int HB = D * VB / 8;  // bytes in the segment
   if constexpr (VB == 2) {
     // nibble n of byte j -> float2 at n*8: codes (dims) 4j,4j+1 | 4j+2,4j+3
 #pragma unroll
     for (int q = 0; q < HB / 4; ++q) {
       const uint32_t xh = vw[q] >> 1, xl = vw[q] << 3;
+      uint32_t ahs[4], als[4];
+      vq_addr<0>(xh, xl, mask, ahs[0], als[0]);
+      vq_addr<1>(xh, xl, mask, ahs[1], als[1]);
+      vq_addr<2>(xh, xl, mask, ahs[2], als[2]);
+      vq_addr<3>(xh, xl, mask, ahs[3], als[3]);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int j = 4 * q + k;
-        const uint32_t ah = (xh >> (8 * k)) & 0x78u, al = (xl >> (8 * k)) & 0x78u;
-        const f32x2 hi = *reinterpret_cast<const f32x2 *>(lds + ah);
-        const f32x2 lo = *reinterpret_cast<const f32x2 *>(lds + al);
+        const f32x2 hi = *reinterpret_cast<const f32x2 *>(lds + ahs[k]);
+        const f32x2 lo = *reinterpret_cast<const f32x2 *>(lds + als[k]);
         acc[4 * j] = fmaf(hi.x, wgt, acc[4 * j]);
         acc[4 * j + 1] = fmaf(hi.y, wgt, acc[4 * j + 1]);
         acc[4 * j + 2] = fmaf(lo.x, wgt, acc[4 * j + 2]);
@@ -340,18 +373,22 @@ __device__ __forceinline__ void vhalf_accumulate(float (&acc)[P / 2], const uint
 #pragma unroll
     for (int q = 0; q < HB / 4; ++q) {
       const uint32_t xh = vw[q] >> 2, xl = vw[q] << 2;
+      uint32_t ahs[4], als[4];
+      vq_addr<0>(xh, xl, mask, ahs[0], als[0]);
+      vq_addr<1>(xh, xl, mask, ahs[1], als[1]);
+      vq_addr<2>(xh, xl, mask, ahs[2], als[2]);
+      vq_addr<3>(xh, xl, mask, ahs[3], als[3]);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int j = 4 * q + k;
-        const uint32_t ah = (xh >> (8 * k)) & 0x3Cu, al = (xl >> (8 * k)) & 0x3Cu;
-        acc[2 * j] = fmaf(*reinterpret_cast<const float *>(lds + ah), wgt, acc[2 * j]);
-        acc[2 * j + 1] = fmaf(*reinterpret_cast<const float *>(lds + al), wgt, acc[2 * j + 1]);
+        acc[2 * j] = fmaf(*reinterpret_cast<const float *>(lds + ahs[k]), wgt, acc[2 * j]);
+        acc[2 * j + 1] = fmaf(*reinterpret_cast<const float *>(lds + als[k]), wgt, acc[2 * j + 1]);
       }
     }
   } else {
     // 3-bit: 8 codes per 24-bit big-endian group -> float at c*4
 #pragma unroll
-    for (int g = 0; g < P / 16; ++g) {
+    for (int g = 0; g < D / 8; ++g) {
       const uint32_t w24 = (byte_of(vw, 3 * g) << 16) | (byte_of(vw, 3 * g + 1) << 8) |
                            byte_of(vw, 3 * g + 2);
       const uint32_t w26 = w24 << 2;
@@ -364,16 +401,62 @@ __device__ __forceinline__ void vhalf_accumulate(float (&acc)[P / 2], const uint
   }
 }
 
+// V rows are split into SPLIT segments of P/SPLIT dimensions: quarters when
+// a quarter row is a whole number of 16-byte units, halves otherwise
+// (3-bit codes at padded 64).
+template <int P, int VB>
+struct VSplit {
+  static constexpr int row_bytes = VB == 16 ? 4 * P : P * VB / 8;
+  static constexpr int value = (row_bytes % 16 == 0) ? 4 : 2;
+};
+
+// Segment transpose across lanes.  Lane l = G*r + c (G = 64/SPLIT lanes per
+// row group r, column c) holds segment q of its own row in
+// x[q*SW .. q*SW+SW); afterwards it holds segment r of the row of lane
+// G*s + c in x[s*SW ..], s < SPLIT.  permlane32_swap exchanges lanes 32-63 of
+// its first operand with lanes 0-31 of its second; permlane16_swap exchanges
+// the odd 16-lane rows of its first operand with the even rows of its second.
+template <int SPLIT, int SW>
+__device__ __forceinline__ void transpose_segments(uint32_t *x) {
+  if constexpr (SPLIT == 2) {
+#pragma unroll
+    for (int i = 0; i < SW; ++i) {
+      const auto r = __builtin_amdgcn_permlane32_swap(x[i], x[SW + i], false, false);
+      x[i] = r[0];
+      x[SW + i] = r[1];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < SW; ++i) {
+      const auto r0 = __builtin_amdgcn_permlane32_swap(x[i], x[2 * SW + i], false, false);
+      const auto r1 = __builtin_amdgcn_permlane32_swap(x[SW + i], x[3 * SW + i], false, false);
+      x[i] = r0[0];
+      x[2 * SW + i] = r0[1];
+      x[SW + i] = r1[0];
+      x[3 * SW + i] = r1[1];
+    }
+#pragma unroll
+    for (int i = 0; i < SW; ++i) {
+      const auto r0 = __builtin_amdgcn_permlane16_swap(x[i], x[SW + i], false, false);
+      const auto r1 = __builtin_amdgcn_permlane16_swap(x[2 * SW + i], x[3 * SW + i], false, false);
+      x[i] = r0[0];
+      x[SW + i] = r0[1];
+      x[2 * SW + i] = r1[0];
+      x[3 * SW + i] = r1[1];
+    }
+  }
+}
+
 // With n_splits == 1 the block owns its item and writes the final output
 // (outs) directly; otherwise it writes a partial for finalize_kernel.
 //
 // One lane per token for K: a byte lookup table in LDS gives one read per
-// code byte.  For V, lanes L and L+32 pair up: after a v_permlane32_swap the
-// lower lane holds the first half of the V rows of tokens L and L+32 and the
-// upper lane the second halves, so each lane keeps P/2 accumulators (half
-// the registers of one-token-per-lane accumulation, hence twice the
-// occupancy) and does the same number of FMAs.  V codebook tables are small
-// enough that distinct entries sit in distinct LDS banks:
+// code byte.  For V, the SPLIT lanes of a column exchange row segments
+// (transpose_segments) so that each lane accumulates one segment of
+// P/SPLIT dimensions for SPLIT tokens: the same FMAs as one token per lane,
+// with 1/SPLIT of the accumulator registers (hence the occupancy).  V
+// codebook tables are small enough that distinct entries sit in distinct LDS
+// banks:
 //   2-bit: nibble (2 codes) -> float2, 16 entries
 //   4-bit: nibble (1 code)  -> float, 16 entries
 //   3-bit: code             -> float, 8 entries
@@ -387,7 +470,10 @@ __global__ __launch_bounds__(kLutThreads, 2) void decode_lut_kernel(
   constexpr int VNB = RAW ? 4 * P : RowBytes<P, VB>::value;
   constexpr int KW = KQ ? KNB / 4 : 1;
   constexpr int VW = VQ ? VNB / 4 : 1;
-  constexpr int H = P / 2;
+  constexpr int SPLIT = VSplit<P, VB>::value;
+  constexpr int G = 64 / SPLIT;  // lanes per row group
+  constexpr int D = P / SPLIT;   // dimensions per lane
+  constexpr int SW = VQ ? VW / SPLIT : 1;
   // LDS: [V table | K table | query | per-wave partials]
   __shared__ __align__(16) uint8_t s_mem[kVlutBytes + 4 * KLut<P, KB>::size];
   __shared__ float s_q[P];
@@ -407,7 +493,7 @@ __global__ __launch_bounds__(kLutThreads, 2) void decode_lut_kernel(
   const int t_end = min(n, t_begin + chunk);
   float *part = partials + ((size_t)item * n_splits + split) * (P + 4);
   const int lane = threadIdx.x & 63;
-  const bool upper = lane >= 32;
+  const int grow = lane / G, gcol = lane % G;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t *signs = (const uint32_t *)d->signs;
   if (t_begin >= t_end) {
@@ -423,6 +509,28 @@ __global__ __launch_bounds__(kLutThreads, 2) void decode_lut_kernel(
     return;
   }
 
+  const uint8_t *k_rows = RAW ? (const uint8_t *)d->raw_k : (const uint8_t *)d->k_codes;
+  const uint8_t *v_rows = RAW ? (const uint8_t *)d->raw_v : (const uint8_t *)d->v_codes;
+  const AQ_AS1 float *k_scale = (const AQ_AS1 float *)d->k_scale;
+  const AQ_AS1 float *v_scale = (const AQ_AS1 float *)d->v_scale;
+
+  // Software pipeline: the first tile is requested before the tables are
+  // built; afterwards the K row of the next tile is requested as soon as
+  // this tile's logits are done and the V row as soon as its segments have
+  // been exchanged, so each load has a compute phase to hide behind without
+  // extra registers.
+  constexpr int kStride = kLutWaves * kTile;
+  int base = t_begin + wave * kTile;
+  uint32_t kc[KW], vw[VW];
+  float ksc = 1.0f, vsc = 1.0f;
+  {
+    const int tt = min(base + lane, t_end - 1);  // t_begin < t_end here
+    if constexpr (KQ) load_row_g<KNB>(k_rows, tt, kc);
+    if constexpr (VQ) load_row_g<VNB>(v_rows, tt, vw);
+    if constexpr (KQ) ksc = k_scale[tt];
+    if constexpr (VQ) vsc = v_scale[tt];
+  }
+
   load_query<P>(s_q, queries + (size_t)item * dim, dim, KQ, signs);
   if constexpr (KQ) build_klut<P, KB>(s_klut, s_q);
   if constexpr (VQ) build_vlut<VB>(s_vlut);
@@ -430,43 +538,31 @@ __global__ __launch_bounds__(kLutThreads, 2) void decode_lut_kernel(
 
   const float attn_s = KQ ? 1.0f / (sqrtf((float)dim) * (float)P) : 1.0f / sqrtf((float)dim);
   const float isp = VQ ? 1.0f / sqrtf((float)P) : 1.0f;
-  const uint8_t *k_rows = RAW ? (const uint8_t *)d->raw_k : (const uint8_t *)d->k_codes;
-  const uint8_t *v_rows = RAW ? (const uint8_t *)d->raw_v : (const uint8_t *)d->v_codes;
-  const AQ_AS1 float *k_scale = (const AQ_AS1 float *)d->k_scale;
-  const AQ_AS1 float *v_scale = (const AQ_AS1 float *)d->v_scale;
+  const uint32_t vmask = VB == 2 ? 0x78u : 0x3Cu;
 
-  float acc[H];
-#pragma unroll
-  for (int i = 0; i < H; ++i) acc[i] = 0.0f;
-  float m_run = -INFINITY, l_run = 0.0f;
-
-  for (int base = t_begin + wave * kTile; base < t_end; base += kLutWaves * kTile) {
-    const int t = base + lane;
-    const bool valid = t < t_end;
-    const int tt = valid ? t : t_end - 1;
-    uint32_t kc[KW];
-    if constexpr (KQ) load_row_g<KNB>(k_rows, tt, kc);
-    uint32_t vw[VW];
-    if constexpr (VQ) load_row_g<VNB>(v_rows, tt, vw);
-    const float ksc = RAW ? 1.0f : k_scale[tt];
-    const float vsc = RAW ? 1.0f : v_scale[tt];
-
-    // ---- logit of token t ----
+  // Logit of the token of this lane in the tile at tile_base (K row kc).
+  auto tile_logit = [&](const uint32_t *kcw, float kscale, int tile_base) -> float {
+    const int tt = tile_base + lane;
     float dot;
     if constexpr (KQ) {
-      float p4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      float p4[4];
       if constexpr (KB == 3) {
 #pragma unroll
-        for (int g = 0; g < P / 8; ++g)
+        for (int m = 0; m < 4; ++m) p4[m] = s_klut[m * 64 + pair3(kcw, 0, m)];
 #pragma unroll
-          for (int m = 0; m < 4; ++m) p4[m] += s_klut[(4 * g + m) * 64 + pair3(kc, g, m)];
+        for (int g = 1; g < P / 8; ++g)
+#pragma unroll
+          for (int m = 0; m < 4; ++m) p4[m] += s_klut[(4 * g + m) * 64 + pair3(kcw, g, m)];
       } else {
 #pragma unroll
-        for (int j = 0; j < KNB; ++j) p4[j & 3] += s_klut[j * 256 + byte_of(kc, j)];
+        for (int j = 0; j < 4; ++j) p4[j] = s_klut[j * 256 + byte_of(kcw, j)];
+#pragma unroll
+        for (int j = 4; j < KNB; ++j) p4[j & 3] += s_klut[j * 256 + byte_of(kcw, j)];
       }
-      dot = ((p4[0] + p4[1]) + (p4[2] + p4[3])) * attn_s * ksc;
+      dot = ((p4[0] + p4[1]) + (p4[2] + p4[3])) * attn_s * kscale;
     } else {
-      const AQ_AS1 float *kr = (const AQ_AS1 float *)k_rows + (size_t)tt * (RAW ? dim : P);
+      const AQ_AS1 float *kr =
+          (const AQ_AS1 float *)k_rows + (size_t)min(tt, t_end - 1) * (RAW ? dim : P);
       float p4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int i = 0; i < P; i += 4) {
@@ -478,14 +574,30 @@ __global__ __launch_bounds__(kLutThreads, 2) void decode_lut_kernel(
       }
       dot = ((p4[0] + p4[1]) + (p4[2] + p4[3])) * attn_s;
     }
-    const float logit = valid ? dot : -INFINITY;
+    return tt < t_end ? dot : -INFINITY;
+  };
+
+  float acc[D];
+#pragma unroll
+  for (int i = 0; i < D; ++i) acc[i] = 0.0f;
+  float m_run = -INFINITY, l_run = 0.0f;
+
+  // The loop body holds the V phase of tile i and the K phase of tile i+1.
+  float logit = tile_logit(kc, ksc, base);
+  if constexpr (KQ) {
+    const int tn = min(base + kStride + lane, t_end - 1);
+    load_row_g<KNB>(k_rows, tn, kc);
+    ksc = k_scale[tn];
+  }
+  for (; base < t_end; base += kStride) {
+    const bool valid = base + lane < t_end;
 
     // ---- online softmax (wave-uniform running max) ----
     const float tmax = wave_reduce<true>(logit);
     if (tmax > m_run) {
       const float alpha = m_run == -INFINITY ? 0.0f : expf(m_run - tmax);
 #pragma unroll
-      for (int i = 0; i < H; ++i) acc[i] *= alpha;
+      for (int i = 0; i < D; ++i) acc[i] *= alpha;
       l_run *= alpha;
       m_run = tmax;
     }
@@ -493,51 +605,65 @@ __global__ __launch_bounds__(kLutThreads, 2) void decode_lut_kernel(
     l_run += e;
     const float wgt = VQ ? e * vsc * isp : e;
 
-    // ---- V: exchange half rows with the partner lane, accumulate ----
-    // (w0, x0): token L (lower lanes) / token L-32 (upper lanes);
-    // (w1, x1): token L+32 (lower) / token L (upper).
-    const auto wsw = __builtin_amdgcn_permlane32_swap(__float_as_uint(wgt), __float_as_uint(wgt),
-                                                      false, false);
-    const float w0 = upper ? __uint_as_float(wsw[0]) : wgt;
-    const float w1 = upper ? wgt : __uint_as_float(wsw[1]);
-    if constexpr (VQ) {
-      uint32_t x0[VW / 2], x1[VW / 2];
+    // ---- V: exchange row segments within each column ----
+    // After the transposes, wv[s] and segment s of x belong to the token of
+    // lane G*s + gcol; x holds segment grow of its row.  Invalid tokens
+    // carry weight 0 and valid (clamped) codes.
+    uint32_t wv[SPLIT];
 #pragma unroll
-      for (int i = 0; i < VW / 2; ++i) {
-        const auto r = __builtin_amdgcn_permlane32_swap(vw[i], vw[VW / 2 + i], false, false);
-        x0[i] = r[0];
-        x1[i] = r[1];
-      }
-      // invalid tokens carry weight 0 and valid (clamped) codes
-      vhalf_accumulate<P, VB>(acc, x0, w0, s_mem);
-      vhalf_accumulate<P, VB>(acc, x1, w1, s_mem);
+    for (int s2 = 0; s2 < SPLIT; ++s2) wv[s2] = __float_as_uint(wgt);
+    transpose_segments<SPLIT, 1>(wv);
+    uint32_t x[VW];
+    if constexpr (VQ) {
+#pragma unroll
+      for (int i = 0; i < VW; ++i) x[i] = vw[i];
+      transpose_segments<SPLIT, SW>(x);
+      // past the end every lane reads the last row (one line)
+      const int tn = min(base + kStride + lane, t_end - 1);
+      load_row_g<VNB>(v_rows, tn, vw);
+      vsc = v_scale[tn];
+    }
+
+    // ---- V phase of this tile, then the K phase of the next ----
+    if constexpr (VQ) {
+#pragma unroll
+      for (int s2 = 0; s2 < SPLIT; ++s2)
+        vseg_accumulate<D, VB>(acc, x + s2 * SW, __uint_as_float(wv[s2]), s_mem, vmask);
     } else {
       const AQ_AS1 float *vr = (const AQ_AS1 float *)v_rows;
       const int stride = RAW ? dim : P;
-      const int tok0 = min((upper ? base + lane - 32 : base + lane), t_end - 1);
-      const int tok1 = min((upper ? base + lane : base + lane + 32), t_end - 1);
-      const int off = upper ? H : 0;
 #pragma unroll
-      for (int i = 0; i < H; i += 4) {
-        const f32x4 a4 = *reinterpret_cast<const AQ_AS1 f32x4 *>(vr + (size_t)tok0 * stride + off + i);
-        const f32x4 b4 = *reinterpret_cast<const AQ_AS1 f32x4 *>(vr + (size_t)tok1 * stride + off + i);
-        acc[i] = fmaf(b4.x, w1, fmaf(a4.x, w0, acc[i]));
-        acc[i + 1] = fmaf(b4.y, w1, fmaf(a4.y, w0, acc[i + 1]));
-        acc[i + 2] = fmaf(b4.z, w1, fmaf(a4.z, w0, acc[i + 2]));
-        acc[i + 3] = fmaf(b4.w, w1, fmaf(a4.w, w0, acc[i + 3]));
+      for (int s2 = 0; s2 < SPLIT; ++s2) {
+        const int tok = min(base + G * s2 + gcol, t_end - 1);
+        const AQ_AS1 float *row = vr + (size_t)tok * stride + grow * D;
+        const float ws = __uint_as_float(wv[s2]);
+#pragma unroll
+        for (int i = 0; i < D; i += 4) {
+          const f32x4 v4 = *reinterpret_cast<const AQ_AS1 f32x4 *>(row + i);
+          acc[i] = fmaf(v4.x, ws, acc[i]);
+          acc[i + 1] = fmaf(v4.y, ws, acc[i + 1]);
+          acc[i + 2] = fmaf(v4.z, ws, acc[i + 2]);
+          acc[i + 3] = fmaf(v4.w, ws, acc[i + 3]);
+        }
       }
+    }
+    logit = tile_logit(kc, ksc, base + kStride);
+    if constexpr (KQ) {
+      const int tn2 = min(base + 2 * kStride + lane, t_end - 1);
+      load_row_g<KNB>(k_rows, tn2, kc);
+      ksc = k_scale[tn2];
     }
   }
 
   // ---- block merge: waves -> one (m, l, acc) ----
   // l_run: every token's e is held by its own lane once.
   const float l_w = wave_reduce<false>(l_run);
-  // reduce acc[H] over the 32 lanes of each half-wave: lane L ends with the
-  // totals of dimensions 2(L%32), 2(L%32)+1 (+H for the upper half)
+  // reduce acc[D] over the G lanes of each row group: lane (grow, gcol) ends
+  // with the totals of dimensions grow*D + (D/G)*gcol + k, k < D/G
 #pragma unroll
-  for (int step = 0; step < 5; ++step) {
-    const int m = 16 >> step;
-    const int half = H >> (step + 1);
+  for (int step = 0; (G >> step) > 1; ++step) {
+    const int m = (G / 2) >> step;
+    const int half = D >> (step + 1);
     const uint32_t up = (lane & m) ? 0xFFFFFFFFu : 0u;
 #pragma unroll
     for (int j = 0; j < half; ++j) {
@@ -548,9 +674,9 @@ __global__ __launch_bounds__(kLutThreads, 2) void decode_lut_kernel(
     }
   }
   {
-    const int d0 = (upper ? H : 0) + (H / 32) * (lane & 31);
+    const int d0 = grow * D + (D / G) * gcol;
 #pragma unroll
-    for (int k = 0; k < H / 32; ++k) s_red[wave][d0 + k] = acc[k];
+    for (int k = 0; k < D / G; ++k) s_red[wave][d0 + k] = acc[k];
   }
   if (lane == 0) {
     s_ml[wave][0] = m_run;
