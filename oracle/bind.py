@@ -69,6 +69,7 @@ class Oracle:
         L.orc_fwht_inverse.argtypes = [_f, _i8, C.c_int]
         L.orc_quantize_fast.argtypes = [C.c_float, C.c_int]
         L.orc_quantize_fast.restype = C.c_int
+        L.orc_codebook.argtypes = [C.c_int, _f]
         L.orc_pack.argtypes = [_u8, C.c_int, C.c_int, _u8]
         L.orc_unpack.argtypes = [_u8, C.c_int, C.c_int, _u8]
         L.orc_quantize_vec.argtypes = [_f, C.c_int, C.c_int, _i8, C.c_int, _u8, _u8]
@@ -110,6 +111,11 @@ class Oracle:
 
     def quantize_fast(self, v: float, bits: int) -> int:
         return self.lib.orc_quantize_fast(v, bits)
+
+    def codebook(self, bits: int) -> np.ndarray:
+        cb = np.zeros(1 << bits, np.float32)
+        self.lib.orc_codebook(bits, fptr(cb))
+        return cb
 
     def pack(self, idx: np.ndarray, bits: int) -> np.ndarray:
         idx = np.ascontiguousarray(idx, np.uint8)

@@ -113,6 +113,11 @@ static const float *codebook(int bits) {
   return bits == 2 ? CB2 : bits == 3 ? CB3 : CB4;
 }
 
+void orc_codebook(int bits, float *out) {
+  const float *cb = codebook(bits);
+  for (int i = 0; i < (1 << bits); ++i) out[i] = cb[i];
+}
+
 /* Decision thresholds: midpoints (c[k] + c[k+1]) * 0.5f evaluated in float,
  * with the centre threshold exactly 0 (core/codebook.cpp:67-100). */
 static float thresholds[3][15];

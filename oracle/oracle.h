@@ -28,6 +28,7 @@ void  orc_rademacher(int8_t *D, int n, uint64_t seed);
 void  orc_fwht_forward(float *x, const int8_t *D, int p);
 void  orc_fwht_inverse(float *x, const int8_t *D, int p);
 int   orc_quantize_fast(float v, int bits);
+void  orc_codebook(int bits, float *out);  /* 2^bits centroids */
 void  orc_pack(const uint8_t *idx, int p, int bits, uint8_t *dst);
 void  orc_unpack(const uint8_t *src, int p, int bits, uint8_t *idx);
 int   orc_packed_bytes(int p, int bits);
