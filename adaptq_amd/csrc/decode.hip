@@ -561,18 +561,21 @@ __global__ __launch_bounds__(kLutThreads, 2) void decode_lut_kernel(
       }
       dot = ((p4[0] + p4[1]) + (p4[2] + p4[3])) * attn_s * kscale;
     } else {
+      // fp32 keys: the reference's sequential, unfused dot product
+      // (attention.cpp:212-219 and :497-502), so that peaked softmaxes see
+      // the same logits to the last bit.
       const AQ_AS1 float *kr =
           (const AQ_AS1 float *)k_rows + (size_t)min(tt, t_end - 1) * (RAW ? dim : P);
-      float p4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      float acc_d = 0.0f;
 #pragma unroll
       for (int i = 0; i < P; i += 4) {
         const f32x4 k4 = *reinterpret_cast<const AQ_AS1 f32x4 *>(kr + i);
-        p4[0] = fmaf(s_q[i], k4.x, p4[0]);
-        p4[1] = fmaf(s_q[i + 1], k4.y, p4[1]);
-        p4[2] = fmaf(s_q[i + 2], k4.z, p4[2]);
-        p4[3] = fmaf(s_q[i + 3], k4.w, p4[3]);
+        acc_d = __fadd_rn(acc_d, __fmul_rn(s_q[i], k4.x));
+        acc_d = __fadd_rn(acc_d, __fmul_rn(s_q[i + 1], k4.y));
+        acc_d = __fadd_rn(acc_d, __fmul_rn(s_q[i + 2], k4.z));
+        acc_d = __fadd_rn(acc_d, __fmul_rn(s_q[i + 3], k4.w));
       }
-      dot = ((p4[0] + p4[1]) + (p4[2] + p4[3])) * attn_s;
+      dot = __fmul_rn(acc_d, attn_s);
     }
     return tt < t_end ? dot : -INFINITY;
   };
@@ -789,24 +792,32 @@ __global__ __launch_bounds__(kThreads) void decode_generic_kernel(
   float m_run = -INFINITY, l_run = 0.0f;
 
   for (int t0 = t_begin; t0 < t_end; t0 += G) {
-    float pd[G];
+    if constexpr (KQ) {
+      float pd[G];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      pd[g] = 0.0f;
-      const int t = t0 + g;
-      if (t >= t_end) continue;
-      const uint8_t *row = iv.k_rows + (size_t)t * kstride;
-      for (int i = threadIdx.x; i < own; i += kThreads) {
-        float kv;
-        if constexpr (KQ) kv = cbv<KB>(code_at<KB>(row, i));
-        else kv = reinterpret_cast<const float *>(row)[i];
-        pd[g] = fmaf(s_q[i], kv, pd[g]);
+      for (int g = 0; g < G; ++g) {
+        pd[g] = 0.0f;
+        const int t = t0 + g;
+        if (t >= t_end) continue;
+        const uint8_t *row = iv.k_rows + (size_t)t * kstride;
+        for (int i = threadIdx.x; i < own; i += kThreads)
+          pd[g] = fmaf(s_q[i], cbv<KB>(code_at<KB>(row, i)), pd[g]);
       }
-    }
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float s = wave_sum(pd[g]);
-      if (lane == 0) s_part[wave][g] = s;
+      for (int g = 0; g < G; ++g) {
+        const float s = wave_sum(pd[g]);
+        if (lane == 0) s_part[wave][g] = s;
+      }
+    } else if (threadIdx.x < G) {
+      // fp32 keys: one thread per token, the reference's sequential unfused
+      // dot product (attention.cpp:212-219 and :497-502)
+      const int t = t0 + threadIdx.x;
+      float dsum = 0.0f;
+      if (t < t_end) {
+        const float *row = reinterpret_cast<const float *>(iv.k_rows + (size_t)t * kstride);
+        for (int i = 0; i < dim; ++i) dsum = __fadd_rn(dsum, __fmul_rn(s_q[i], row[i]));
+      }
+      s_part[0][threadIdx.x] = dsum;
     }
     __syncthreads();
     float lg[G];
@@ -814,10 +825,14 @@ __global__ __launch_bounds__(kThreads) void decode_generic_kernel(
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float s = 0.0f;
+      if constexpr (KQ) {
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) s += s_part[w][g];
+        for (int w = 0; w < kWaves; ++w) s += s_part[w][g];
+      } else {
+        s = s_part[0][g];
+      }
       const int t = t0 + g;
-      lg[g] = t < t_end ? (KQ ? s * attn_s * iv.k_scale[t] : s * attn_s) : -INFINITY;
+      lg[g] = t < t_end ? (KQ ? s * attn_s * iv.k_scale[t] : __fmul_rn(s, attn_s)) : -INFINITY;
       gmax = fmaxf(gmax, lg[g]);
     }
     __syncthreads();
