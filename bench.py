@@ -47,22 +47,27 @@ def cpu_baseline(cfg, seconds=12.0, heads=8, seed=0):
     from /root/reference) on this host: `heads` heads of the bench shape, each
     filled with cfg['ctx'] tokens, then compute() repeated for ~seconds, first
     on one thread (the reference's execution model), then on one thread per
-    head.  Returns the multi-thread figure with the single-thread one attached."""
+    head.  Returns the multi-thread figure with the single-thread one attached.
+    Where the reference build is absent, the CPU restatement (oracle/) is timed
+    instead and reported as kind "port"."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    from bind import Ref, REF_SO, fptr  # test infrastructure: the checker/baseline only
-    if not os.path.exists(REF_SO):
-        return None
-    r = Ref()
-    L = r.lib
+    # test infrastructure: the checker/baseline only
+    from bind import Oracle, Ref, REF_SO, fptr
+    if os.path.exists(REF_SO):
+        L, kind = Ref().lib, "reference"
+        create, append, compute = L.adaptq_create, L.adaptq_append, L.adaptq_compute
+    else:
+        L, kind = Oracle().lib, "port"
+        create, append, compute = L.orc_head_create, L.orc_head_append, L.orc_head_compute
     dim, n = cfg["dim"], cfg["ctx"]
     rng = np.random.default_rng(seed)
     hs = []
     for h in range(heads):
-        c = L.adaptq_create(dim, cfg["k_bits"], cfg["v_bits"], n, 1000 + h, 0.0, 0)
+        c = create(dim, cfg["k_bits"], cfg["v_bits"], n, 1000 + h, 0.0, 0)
         kv = rng.standard_normal((n, 2, dim)).astype(np.float32)
         for t in range(n):
-            L.adaptq_append(c, fptr(kv[t, 0]), fptr(kv[t, 1]), t)
+            append(c, fptr(kv[t, 0]), fptr(kv[t, 1]), t)
         hs.append(c)
     q = rng.standard_normal((heads, dim)).astype(np.float32)
     out = np.zeros((heads, dim), np.float32)
@@ -71,7 +76,7 @@ def cpu_baseline(cfg, seconds=12.0, heads=8, seed=0):
         t0 = time.perf_counter()
         k = 0
         while time.perf_counter() - t0 < budget:
-            L.adaptq_compute(hs[idx], fptr(q[idx]), fptr(out[idx]))
+            compute(hs[idx], fptr(q[idx]), fptr(out[idx]))
             k += 1
         counts[idx] = (k, time.perf_counter() - t0)
 
@@ -86,7 +91,7 @@ def cpu_baseline(cfg, seconds=12.0, heads=8, seed=0):
         t.join()
     multi = sum(k * n / dt for k, dt in counts.values())
     for c in hs:
-        L.adaptq_destroy(c)
+        (L.adaptq_destroy if kind == "reference" else L.orc_head_destroy)(c)
     model = "unknown"
     try:
         with open("/proc/cpuinfo") as f:
@@ -97,13 +102,25 @@ def cpu_baseline(cfg, seconds=12.0, heads=8, seed=0):
     except OSError:
         pass
     return {
-        "value": multi, "unit": "token*heads/s", "cores": heads, "kind": "reference",
+        "value": multi, "unit": "token*heads/s", "cores": heads, "kind": kind,
         "sample": f"{heads} heads x {n} tokens, d{dim} K{cfg['k_bits']}/V{cfg['v_bits']}, "
                   f"v_mass=0, hybrid=0; compute() repeated ~{seconds:.0f}s "
                   f"(1/3 on 1 thread, 2/3 on {heads} threads); CPU: {model}",
         "single_thread_value": single,
         "gb_per_s": multi * decode_bytes_per_token(dim, cfg["k_bits"], cfg["v_bits"]) / 1e9,
     }
+
+
+def profiled_traffic(name="decode_lut_k4v2_d128_cfg5.md"):
+    """HBM bytes per decode launch from the committed rocprofv3 summary: two
+    PMC passes (FETCH_SIZE, WRITE_SIZE) scaled by the copy calibration."""
+    import re
+    try:
+        with open(os.path.join(ROOT, "profiles", name)) as f:
+            m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", f.read(), re.M)
+        return int(m.group(1)) if m else None
+    except OSError:
+        return None
 
 
 def main():
@@ -234,7 +251,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+            "frac": achieved / HBM_PEAK_GBS, "traffic": profiled_traffic(),
             "kernel": "decode_lut_kernel<128,4,2>", "bytes_per_launch": bytes_launch,
             "kernel_ms": ms,
         },
