@@ -42,6 +42,12 @@ SIGNATURES = {
     "adaptq_ring_info": (C.c_int, [C.c_void_p, _ip, _ip, _ip, _ip, _ip, _ip]),
     "adaptq_read_slots": (C.c_int, [C.c_void_p, C.c_int, C.c_int, _u8, _u8, _f, _f]),
     "adaptq_mha_head": (C.c_void_p, [C.c_void_p, C.c_int]),
+    "adaptq_mha_append_all": (C.c_int, [C.c_void_p, _f, _f, C.c_int]),
+    "adaptq_mha_compute_all": (C.c_int, [C.c_void_p, _f, _f]),
+    "adaptq_mha_append_all_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,
+                                               C.c_int, C.c_void_p]),
+    "adaptq_mha_compute_all_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p,
+                                                C.c_void_p]),
     "adaptq_plan_create": (C.c_void_p, [C.POINTER(C.c_void_p), C.c_int]),
     "adaptq_plan_destroy": (None, [C.c_void_p]),
     "adaptq_plan_append_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,

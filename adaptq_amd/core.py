@@ -5,6 +5,10 @@ hybrid_thresh=512)`` with ``append(k, v)``, ``compute(q)``, ``reset()`` and the
 ``kv_bytes`` property, over the pybind11 module ``adaptq_py.MHAContext`` built
 from adaptq_amd/csrc/adapter_python.cpp.  Same defaults, shapes and errors as
 the reference; the ring buffers live in GPU memory.
+
+Where the reference loops over heads in Python (adaptq/core.py:45-74), this
+Engine makes one call for all heads (``MHAContext.append_all`` /
+``compute_all``): one append launch and one decode launch per step.
 """
 from __future__ import annotations
 
@@ -31,19 +35,15 @@ class Engine:
         """Append one token's keys and values, each of shape (heads, dim)."""
         if k.shape != (self.heads, self.dim) or v.shape != (self.heads, self.dim):
             raise ValueError(f"k and v must be shape ({self.heads}, {self.dim})")
-        for h in range(self.heads):
-            self._ctx.append(h, np.ascontiguousarray(k[h], dtype=np.float32),
-                             np.ascontiguousarray(v[h], dtype=np.float32), self.pos)
+        self._ctx.append_all(np.ascontiguousarray(k, dtype=np.float32),
+                             np.ascontiguousarray(v, dtype=np.float32), self.pos)
         self.pos += 1
 
     def compute(self, q: np.ndarray) -> np.ndarray:
         """Attention output for q of shape (heads, dim); returns (heads, dim)."""
         if q.shape != (self.heads, self.dim):
             raise ValueError(f"q must be shape ({self.heads}, {self.dim})")
-        out = np.zeros((self.heads, self.dim), dtype=np.float32)
-        for h in range(self.heads):
-            out[h] = self._ctx.compute(h, np.ascontiguousarray(q[h], dtype=np.float32))
-        return out
+        return np.asarray(self._ctx.compute_all(np.ascontiguousarray(q, dtype=np.float32)))
 
     def reset(self) -> None:
         self._ctx.reset()

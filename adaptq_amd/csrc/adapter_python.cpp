@@ -8,6 +8,7 @@
 // with adaptq_last_error() (the reference would carry a NULL handle on).
 #include <pybind11/numpy.h>
 #include <pybind11/pybind11.h>
+#include <cstdint>
 
 #include <stdexcept>
 #include <string>
@@ -54,6 +55,42 @@ class PyMHAContext {
     return out;
   }
 
+  // Whole-MHA forms (adaptq_mha_append_all / _compute_all): one call for all
+  // heads instead of the reference Engine's per-head loop.
+  void append_all(farray keys, farray vals, int pos) {
+    if (keys.ndim() != 2 || vals.ndim() != 2 || keys.shape(0) != n_heads_ ||
+        vals.shape(0) != n_heads_ || keys.shape(1) != head_dim_ || vals.shape(1) != head_dim_)
+      throw std::invalid_argument("keys/vals must be (n_heads, head_dim)");
+    if (adaptq_mha_append_all(backend_.handle(), keys.data(), vals.data(), pos) != 0)
+      throw std::runtime_error(adaptq_last_error());
+  }
+
+  farray compute_all(farray queries) {
+    if (queries.ndim() != 2 || queries.shape(0) != n_heads_ || queries.shape(1) != head_dim_)
+      throw std::invalid_argument("queries must be (n_heads, head_dim)");
+    farray out({n_heads_, head_dim_});
+    if (adaptq_mha_compute_all(backend_.handle(), queries.data(), out.mutable_data()) < 0)
+      throw std::runtime_error(adaptq_last_error());
+    return out;
+  }
+
+  // Device pointers (torch-ROCm tensors' data_ptr()), asynchronous on stream.
+  void append_all_device(uintptr_t d_keys, uintptr_t d_vals, int n_tokens, int pos,
+                         uintptr_t stream) {
+    if (adaptq_mha_append_all_device(backend_.handle(), reinterpret_cast<const float *>(d_keys),
+                                     reinterpret_cast<const float *>(d_vals), n_tokens, pos,
+                                     reinterpret_cast<void *>(stream)) != 0)
+      throw std::runtime_error(adaptq_last_error());
+  }
+
+  int compute_all_device(uintptr_t d_queries, uintptr_t d_outs, uintptr_t stream) {
+    const int n = adaptq_mha_compute_all_device(
+        backend_.handle(), reinterpret_cast<const float *>(d_queries),
+        reinterpret_cast<float *>(d_outs), reinterpret_cast<void *>(stream));
+    if (n < 0) throw std::runtime_error(adaptq_last_error());
+    return n;
+  }
+
   void reset() { backend_.reset(); }
   size_t kv_bytes() const { return backend_.kv_bytes(); }
   int n_heads() const { return n_heads_; }
@@ -76,6 +113,13 @@ PYBIND11_MODULE(adaptq_py, m) {
            py::arg("pos"))
       .def("compute", &PyMHAContext::compute, py::arg("head"), py::arg("query"))
       .def("compute_batch", &PyMHAContext::compute_batch, py::arg("head"), py::arg("queries"))
+      .def("append_all", &PyMHAContext::append_all, py::arg("keys"), py::arg("vals"),
+           py::arg("pos") = 0)
+      .def("compute_all", &PyMHAContext::compute_all, py::arg("queries"))
+      .def("append_all_device", &PyMHAContext::append_all_device, py::arg("d_keys"),
+           py::arg("d_vals"), py::arg("n_tokens"), py::arg("pos"), py::arg("stream"))
+      .def("compute_all_device", &PyMHAContext::compute_all_device, py::arg("d_queries"),
+           py::arg("d_outs"), py::arg("stream"))
       .def("reset", &PyMHAContext::reset)
       .def("kv_bytes", &PyMHAContext::kv_bytes)
       .def_property_readonly("n_heads", &PyMHAContext::n_heads)

@@ -124,6 +124,11 @@ struct Ctx {
 struct Mha {
   std::vector<Ctx *> heads;
   int n_heads = 0;
+  int device = 0;
+  std::mutex mu;  // whole-MHA calls; taken before any head's lock
+  DevBuf d_list;  // [n_heads] device pointers to the heads' descriptors
+  DevBuf d_ws, d_io, d_stage;
+  std::vector<float> pack_k, pack_v;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -366,6 +371,89 @@ struct Plan {
   DevBuf d_list, d_ws;
 };
 
+// Locks every head of an MHA in index order (per-head calls take one head
+// lock only, so the order cannot deadlock against them).
+struct HeadLocks {
+  std::vector<std::unique_lock<std::mutex>> locks;
+  explicit HeadLocks(Mha *m) {
+    locks.reserve(m->heads.size());
+    for (Ctx *c : m->heads) locks.emplace_back(c->mu);
+  }
+};
+
+// Quantise the staged tokens of every head (caller holds all head locks).
+// When every head holds the same number of staged tokens -- the usual case,
+// one token per head per step -- they go to the device in one copy per side
+// and one append launch over all heads.
+bool flush_all_locked(Mha *m, const char *fn) {
+  const int S = m->heads[0]->staged;
+  bool uniform = S > 0;
+  for (Ctx *c : m->heads) uniform = uniform && c->staged == S;
+  if (!uniform) {
+    for (Ctx *c : m->heads)
+      if (!flush_locked(c, fn)) return false;
+    return true;
+  }
+  const Ctx *c0 = m->heads[0];
+  const int H = m->n_heads;
+  const size_t per = (size_t)S * c0->dim;
+  m->pack_k.resize(per * H);
+  m->pack_v.resize(per * H);
+  for (int h = 0; h < H; ++h) {
+    std::memcpy(m->pack_k.data() + per * h, m->heads[h]->stage_k.data(), per * 4);
+    std::memcpy(m->pack_v.data() + per * h, m->heads[h]->stage_v.data(), per * 4);
+  }
+  DeviceGuard g(m->device);
+  hipStream_t s = lib_stream(m->device);
+  const size_t half = align256(per * H * 4);
+  if (hip_fail(m->d_stage.ensure(2 * half), fn)) return false;
+  float *dk = static_cast<float *>(m->d_stage.p);
+  float *dv = reinterpret_cast<float *>(static_cast<uint8_t *>(m->d_stage.p) + half);
+  hipError_t e = hipMemcpyAsync(dk, m->pack_k.data(), per * H * 4, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) e = hipMemcpyAsync(dv, m->pack_v.data(), per * H * 4, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess)
+    e = aq::launch_append(static_cast<aq::HeadDesc **>(m->d_list.p), H, c0->dim, c0->padded,
+                          c0->k_bits, c0->v_bits, dk, dv, S, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (hip_fail(e, fn)) return false;
+  for (Ctx *c : m->heads) {
+    c->st = aq::ring_after(c->st, S, c->cap, c->hyb);
+    c->staged = 0;
+    c->stage_k.clear();
+    c->stage_v.clear();
+  }
+  return true;
+}
+
+// One decode launch over all heads of an MHA (caller holds all head locks and
+// has flushed).  Returns the common ring size, or -2 when the heads differ in
+// size or branch (the caller then works head by head), or -1 on error.
+// Queries/outs are device pointers; the launch is asynchronous on `s`.
+int launch_all_locked(Mha *m, const float *dq, float *dout, hipStream_t s, const char *fn) {
+  const Ctx *c0 = m->heads[0];
+  const int n = c0->st.size;
+  const Mode mode = mode_of(c0);
+  for (const Ctx *c : m->heads)
+    if (c->st.size != n || mode_of(c) != mode) return -2;
+  const int H = m->n_heads;
+  aq::DecodeShape sh{c0->dim, c0->padded, c0->k_bits, c0->v_bits, mode == Mode::Hybrid,
+                     n > 0 ? n : 1};
+  const size_t wsf = mode == Mode::Sparse ? aq::sparse_workspace_floats(H, sh)
+                                          : aq::decode_workspace_floats(H, sh);
+  if (hip_fail(m->d_ws.ensure(wsf * 4), fn)) return -1;
+  auto **items = static_cast<aq::HeadDesc **>(m->d_list.p);
+  hipError_t e;
+  if (n == 0)  // the decode kernels write zeros for empty rings
+    e = aq::launch_decode(items, H, sh, dq, dout, static_cast<float *>(m->d_ws.p), s);
+  else if (mode == Mode::Sparse)
+    e = aq::launch_decode_sparse(items, H, sh, c0->v_mass, dq, dout,
+                                 static_cast<float *>(m->d_ws.p), s);
+  else
+    e = aq::launch_decode(items, H, sh, dq, dout, static_cast<float *>(m->d_ws.p), s);
+  if (hip_fail(e, fn)) return -1;
+  return n;
+}
+
 }  // namespace
 
 extern "C" {
@@ -464,6 +552,19 @@ adaptq_mha_t adaptq_mha_create(int n_heads, int dim, int k_bits, int v_bits, int
     }
     m->heads.push_back(c);
   }
+  m->device = m->heads[0]->device;
+  std::vector<aq::HeadDesc *> list((size_t)n_heads);
+  for (int i = 0; i < n_heads; ++i) list[i] = m->heads[i]->d_desc;
+  {
+    DeviceGuard g(m->device);
+    if (hip_fail(m->d_list.ensure(sizeof(void *) * (size_t)n_heads), "adaptq_mha_create") ||
+        hip_fail(hipMemcpy(m->d_list.p, list.data(), sizeof(void *) * n_heads,
+                           hipMemcpyHostToDevice),
+                 "adaptq_mha_create")) {
+      adaptq_mha_destroy(m);
+      return nullptr;
+    }
+  }
   return m;
 }
 
@@ -471,6 +572,13 @@ void adaptq_mha_destroy(adaptq_mha_t h) {
   if (!h) return;
   Mha *m = static_cast<Mha *>(h);
   for (Ctx *c : m->heads) free_ctx(c);
+  {
+    DeviceGuard g(m->device);
+    m->d_list.release();
+    m->d_ws.release();
+    m->d_io.release();
+    m->d_stage.release();
+  }
   delete m;
 }
 
@@ -543,6 +651,111 @@ unsigned int adaptq_features(void) {
 const char *adaptq_version(void) { return "3.2.0-hip-gfx950"; }
 
 // ---- extensions ----
+
+int adaptq_mha_append_all(adaptq_mha_t h, const float *keys, const float *vals, int token_pos) {
+  (void)token_pos;
+  const char *fn = "adaptq_mha_append_all";
+  if (!require_handle(h, fn) || !require_pointer(keys, fn, "keys") ||
+      !require_pointer(vals, fn, "vals"))
+    return -1;
+  Mha *m = static_cast<Mha *>(h);
+  std::lock_guard<std::mutex> gm(m->mu);
+  HeadLocks locks(m);
+  const int dim = m->heads[0]->dim;
+  for (int i = 0; i < m->n_heads; ++i) {
+    Ctx *c = m->heads[i];
+    c->stage_k.insert(c->stage_k.end(), keys + (size_t)i * dim, keys + (size_t)(i + 1) * dim);
+    c->stage_v.insert(c->stage_v.end(), vals + (size_t)i * dim, vals + (size_t)(i + 1) * dim);
+    ++c->staged;
+  }
+  if (m->heads[0]->staged >= kStageTokens && !flush_all_locked(m, fn)) return -1;
+  clear_error();
+  return 0;
+}
+
+int adaptq_mha_compute_all(adaptq_mha_t h, const float *queries, float *outs) {
+  const char *fn = "adaptq_mha_compute_all";
+  if (!require_handle(h, fn) || !require_pointer(queries, fn, "queries") ||
+      !require_pointer(outs, fn, "outs"))
+    return -1;
+  Mha *m = static_cast<Mha *>(h);
+  std::lock_guard<std::mutex> gm(m->mu);
+  HeadLocks locks(m);
+  if (!flush_all_locked(m, fn)) return -1;
+  const int H = m->n_heads, dim = m->heads[0]->dim;
+  DeviceGuard g(m->device);
+  hipStream_t s = lib_stream(m->device);
+  const size_t io = align256((size_t)H * dim * 4);
+  if (hip_fail(m->d_io.ensure(2 * io), fn)) return -1;
+  float *dq = static_cast<float *>(m->d_io.p);
+  float *dout = reinterpret_cast<float *>(static_cast<uint8_t *>(m->d_io.p) + io);
+  if (hip_fail(hipMemcpyAsync(dq, queries, (size_t)H * dim * 4, hipMemcpyHostToDevice, s), fn))
+    return -1;
+  int n = launch_all_locked(m, dq, dout, s, fn);
+  if (n == -2) {  // heads differ in size or branch: one head at a time
+    n = 0;
+    for (int i = 0; i < H; ++i) {
+      const int r = compute_locked(m->heads[i], queries + (size_t)i * dim, 1,
+                                   outs + (size_t)i * dim, fn);
+      if (r < 0) return -1;
+      if (i == 0) n = r;
+    }
+    clear_error();
+    return n;
+  }
+  if (n < 0) return -1;
+  hipError_t e = hipMemcpyAsync(outs, dout, (size_t)H * dim * 4, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (hip_fail(e, fn)) return -1;
+  clear_error();
+  return n;
+}
+
+int adaptq_mha_append_all_device(adaptq_mha_t h, const float *d_keys, const float *d_vals,
+                                 int n_tokens, int first_pos, void *stream) {
+  (void)first_pos;
+  const char *fn = "adaptq_mha_append_all_device";
+  if (!require_handle(h, fn) || !require_pointer(d_keys, fn, "d_keys") ||
+      !require_pointer(d_vals, fn, "d_vals"))
+    return -1;
+  if (n_tokens < 0) {
+    set_error("adaptq_mha_append_all_device: negative n_tokens");
+    return -1;
+  }
+  Mha *m = static_cast<Mha *>(h);
+  if (n_tokens == 0) return 0;
+  std::lock_guard<std::mutex> gm(m->mu);
+  HeadLocks locks(m);
+  if (!flush_all_locked(m, fn)) return -1;
+  const Ctx *c0 = m->heads[0];
+  DeviceGuard g(m->device);
+  hipError_t e = aq::launch_append(static_cast<aq::HeadDesc **>(m->d_list.p), m->n_heads, c0->dim,
+                                   c0->padded, c0->k_bits, c0->v_bits, d_keys, d_vals, n_tokens,
+                                   static_cast<hipStream_t>(stream));
+  if (hip_fail(e, fn)) return -1;
+  for (Ctx *c : m->heads) c->st = aq::ring_after(c->st, n_tokens, c->cap, c->hyb);
+  return 0;
+}
+
+int adaptq_mha_compute_all_device(adaptq_mha_t h, const float *d_queries, float *d_outs,
+                                  void *stream) {
+  const char *fn = "adaptq_mha_compute_all_device";
+  if (!require_handle(h, fn) || !require_pointer(d_queries, fn, "d_queries") ||
+      !require_pointer(d_outs, fn, "d_outs"))
+    return -1;
+  Mha *m = static_cast<Mha *>(h);
+  std::lock_guard<std::mutex> gm(m->mu);
+  HeadLocks locks(m);
+  if (!flush_all_locked(m, fn)) return -1;
+  DeviceGuard g(m->device);
+  const int n = launch_all_locked(m, d_queries, d_outs, static_cast<hipStream_t>(stream), fn);
+  if (n == -2) {
+    set_error("adaptq_mha_compute_all_device: heads differ in ring size or branch; "
+              "use adaptq_mha_compute_all");
+    return -1;
+  }
+  return n;
+}
 
 int adaptq_flush(adaptq_ctx_t h) {
   if (!require_handle(h, "adaptq_flush")) return -1;

@@ -145,6 +145,36 @@ int adaptq_read_slots(adaptq_ctx_t ctx, int first_slot, int count,
  * heads: the context of head head_idx of an MHA (NULL if out of range). */
 adaptq_ctx_t adaptq_mha_head(adaptq_mha_t mha, int head_idx);
 
+/* ---- Whole-MHA batches ----
+ * Extension, no counterpart in the reference.  For callers that step all
+ * heads of an MHA together (the Python Engine, framework adapters): one call
+ * instead of one per head (reference adaptq/core.py:45-74 loops over heads),
+ * one append launch and one decode launch for all heads. */
+
+/* Append one token to every head: keys, vals host [n_heads][dim].
+ * Returns 0, or -1 with the last error set. */
+int adaptq_mha_append_all(adaptq_mha_t mha, const float *keys, const float *vals,
+                          int token_pos);
+
+/* Attention for every head: queries host [n_heads][dim] -> outs host
+ * [n_heads][dim], synchronous.  Same results as adaptq_mha_compute per head
+ * (every branch: dense, hybrid, sparse-V).  Returns the number of cached
+ * tokens (of head 0), 0 when empty (outs zeroed), -1 on error. */
+int adaptq_mha_compute_all(adaptq_mha_t mha, const float *queries, float *outs);
+
+/* Device-pointer forms for torch-ROCm callers, asynchronous on `stream`
+ * (a hipStream_t; NULL = the HIP null stream).  append: d_keys, d_vals
+ * [n_heads][n_tokens][dim].  compute: d_queries, d_outs [n_heads][dim];
+ * returns the ring size, or -1 (also when the heads differ in ring size or
+ * branch, e.g. after per-head appends: use adaptq_mha_compute_all then).
+ * Host inspection calls (read_slots, ring_info) see device-path appends once
+ * the caller's stream has been synchronised. */
+int adaptq_mha_append_all_device(adaptq_mha_t mha, const float *d_keys,
+                                 const float *d_vals, int n_tokens,
+                                 int first_pos, void *stream);
+int adaptq_mha_compute_all_device(adaptq_mha_t mha, const float *d_queries,
+                                  float *d_outs, void *stream);
+
 /* ---- Batched device-pointer path ----
  * Extension, no counterpart in the reference.  For callers whose data is
  * already in device memory (torch-ROCm tensors, serving loops) and for the

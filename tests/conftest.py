@@ -3,6 +3,11 @@ import sys
 
 import pytest
 
+try:  # load torch's HIP runtime first, as bench.py does, so one runtime serves both
+    import torch  # noqa: F401
+except ImportError:
+    pass
+
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "oracle"))
