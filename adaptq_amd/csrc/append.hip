@@ -75,6 +75,18 @@ __device__ __forceinline__ void store_row(uint8_t *dst, const uint32_t (&w)[(NB 
   }
 }
 
+// Store a K row with its bytes in the slot's XOR order (kperm_mask): word i,
+// bytes permuted within the word by x & 3, goes to word position i ^ (x >> 2).
+template <int NB>
+__device__ __forceinline__ void store_row_perm(uint8_t *dst, const uint32_t (&w)[NB / 4], int slot,
+                                               uint32_t x) {
+  uint32_t *p = reinterpret_cast<uint32_t *>(dst + (size_t)slot * NB);
+  const uint32_t sel = 0x03020100u ^ ((x & 3u) * 0x01010101u);
+  const uint32_t xw = x >> 2;
+#pragma unroll
+  for (int i = 0; i < NB / 4; ++i) p[i ^ xw] = __builtin_amdgcn_perm(0u, w[i], sel);
+}
+
 template <int P, int B>
 struct Row {
   static constexpr int bytes = B == 16 ? 4 * P : (P * B + 7) / 8;
@@ -214,7 +226,15 @@ __global__ __launch_bounds__(128) void append_kernel(HeadDesc *const *descs, int
       }
       w[byte / 4] |= q << (8 * (byte % 4) + shift);
     }
-    store_row<Row<P, B>::bytes>(codes, w, slot);
+    constexpr int xmask = kperm_mask(P, B);
+    bool stored = false;
+    if constexpr (xmask != 0) {
+      if (side == 0) {
+        store_row_perm<Row<P, B>::bytes>(codes, w, slot, (uint32_t)slot & (uint32_t)xmask);
+        stored = true;
+      }
+    }
+    if (!stored) store_row<Row<P, B>::bytes>(codes, w, slot);
     scales[slot] = norm;
   }
 }

@@ -806,6 +806,17 @@ int adaptq_read_slots(adaptq_ctx_t h, int first_slot, int count, uint8_t *k_code
     e = hipMemcpyAsync(v_scale, hd.v_scale + first_slot, (size_t)count * 4, hipMemcpyDeviceToHost, s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
   if (hip_fail(e, "adaptq_read_slots")) return -1;
+  // K rows stored in XOR byte order go back to the reference's order
+  const int xmask = aq::kperm_mask(c->padded, c->k_bits);
+  if (k_codes && xmask) {
+    uint8_t tmp[64];
+    for (int r = 0; r < count; ++r) {
+      uint8_t *row = k_codes + (size_t)r * c->k_pb;
+      const int x = (first_slot + r) & xmask;
+      for (int j = 0; j < c->k_pb; ++j) tmp[j] = row[j ^ x];
+      std::memcpy(row, tmp, (size_t)c->k_pb);
+    }
+  }
   return 0;
 }
 

@@ -93,10 +93,12 @@ __device__ __forceinline__ uint32_t pair3(const uint32_t *w, int g, int m) {
   return (w24 >> (18 - 6 * m)) & 63u;
 }
 
+// K lookup table entries.  2 and 4 bits: byte value b, byte position jj at
+// word b * 64 + jj (position jj in LDS bank jj; see kperm_mask); 3 bits:
+// code pair m of group g, 6-bit value v at word (4g + m) * 64 + v.
 template <int P, int KB>
 struct KLut {
-  // entries of the K lookup table
-  static constexpr int size = KB == 4 ? (P / 2) * 256 : KB == 2 ? (P / 4) * 256 : KB == 3 ? (P / 2) * 64 : 1;
+  static constexpr int size = (KB == 4 || KB == 2) ? 256 * 64 : KB == 3 ? (P / 2) * 64 : 1;
 };
 template <int VB>
 struct VLut {
@@ -128,15 +130,17 @@ __device__ void load_query(float *s_q, const float *q, int dim, bool rotate, con
 template <int P, int KB>
 __device__ void build_klut(float *lut, const float *qr) {
   if constexpr (KB == 4) {
-    for (int e = threadIdx.x; e < (P / 2) * 256; e += blockDim.x) {
-      const int j = e >> 8, b = e & 255;
-      lut[e] = qr[2 * j] * cbv<4>(b >> 4) + qr[2 * j + 1] * cbv<4>(b & 15);
+    constexpr int NB = P / 2;
+    for (int e = threadIdx.x; e < NB * 256; e += blockDim.x) {
+      const int b = e / NB, j = e % NB;
+      lut[b * 64 + j] = qr[2 * j] * cbv<4>(b >> 4) + qr[2 * j + 1] * cbv<4>(b & 15);
     }
   } else if constexpr (KB == 2) {
-    for (int e = threadIdx.x; e < (P / 4) * 256; e += blockDim.x) {
-      const int j = e >> 8, b = e & 255;
-      lut[e] = (qr[4 * j] * cbv<2>(b >> 6) + qr[4 * j + 1] * cbv<2>((b >> 4) & 3)) +
-               (qr[4 * j + 2] * cbv<2>((b >> 2) & 3) + qr[4 * j + 3] * cbv<2>(b & 3));
+    constexpr int NB = P / 4;
+    for (int e = threadIdx.x; e < NB * 256; e += blockDim.x) {
+      const int b = e / NB, j = e % NB;
+      lut[b * 64 + j] = (qr[4 * j] * cbv<2>(b >> 6) + qr[4 * j + 1] * cbv<2>((b >> 4) & 3)) +
+                        (qr[4 * j + 2] * cbv<2>((b >> 2) & 3) + qr[4 * j + 3] * cbv<2>(b & 3));
     }
   } else if constexpr (KB == 3) {
     for (int e = threadIdx.x; e < (P / 2) * 64; e += blockDim.x) {
@@ -522,6 +526,19 @@ __global__ __launch_bounds__(kLutThreads, 2) void decode_lut_kernel(
   constexpr int kStride = kLutWaves * kTile;
   int base = t_begin + wave * kTile;
   uint32_t kc[KW], vw[VW];
+
+  // K rows in XOR byte order (kperm_mask): this lane's tokens all sit in
+  // slots = lane (mod 64), so stored byte 4i+k of its rows is byte position
+  // jj = (4i+k) ^ x.  xr[i] holds 4*jj for k = 0..3 in its bytes; v_perm
+  // joins a code byte b and 4*jj into the table offset b*256 + 4*jj.
+  constexpr bool KPERM = KQ && (KB == 2 || KB == 4);
+  constexpr uint32_t kXMask = (uint32_t)kperm_mask(P, KB);
+  uint32_t xr[KPERM ? KW : 1];
+  if constexpr (KPERM) {
+    const uint32_t lx = (4u * ((uint32_t)lane & kXMask)) * 0x01010101u;
+#pragma unroll
+    for (int i = 0; i < KW; ++i) xr[i] = ((uint32_t)(16 * i) * 0x01010101u + 0x0C080400u) ^ lx;
+  }
   float ksc = 1.0f, vsc = 1.0f;
   {
     const int tt = min(base + lane, t_end - 1);  // t_begin < t_end here
@@ -554,10 +571,18 @@ __global__ __launch_bounds__(kLutThreads, 2) void decode_lut_kernel(
 #pragma unroll
           for (int m = 0; m < 4; ++m) p4[m] += s_klut[(4 * g + m) * 64 + pair3(kcw, g, m)];
       } else {
+        // selector k: byte 0 <- byte k of xr[i], byte 1 <- code byte k, bytes 2-3 <- 0
+        const uint8_t *lb = reinterpret_cast<const uint8_t *>(s_klut);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) p4[j] = s_klut[j * 256 + byte_of(kcw, j)];
+        for (int k = 0; k < 4; ++k)
+          p4[k] = *reinterpret_cast<const float *>(
+              lb + __builtin_amdgcn_perm(kcw[0], xr[0], 0x0C0C0000u | ((4u + k) << 8) | (uint32_t)k));
 #pragma unroll
-        for (int j = 4; j < KNB; ++j) p4[j & 3] += s_klut[j * 256 + byte_of(kcw, j)];
+        for (int i = 1; i < KW; ++i)
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+            p4[k] += *reinterpret_cast<const float *>(
+                lb + __builtin_amdgcn_perm(kcw[i], xr[i], 0x0C0C0000u | ((4u + k) << 8) | (uint32_t)k));
       }
       dot = ((p4[0] + p4[1]) + (p4[2] + p4[3])) * attn_s * kscale;
     } else {
@@ -734,6 +759,19 @@ __device__ __forceinline__ int code_at(const uint8_t *row, int i) {
   }
 }
 
+// Code i of a K row stored in the slot's XOR byte order (x = slot & mask).
+template <int B>
+__device__ __forceinline__ int kcode_at(const uint8_t *row, int i, int x) {
+  if constexpr (B == 4) {
+    const uint32_t b = row[(i >> 1) ^ x];
+    return (i & 1) ? (b & 15) : (b >> 4);
+  } else if constexpr (B == 2) {
+    return (row[(i >> 2) ^ x] >> (6 - 2 * (i & 3))) & 3;
+  } else {
+    return code_at<B>(row, i);
+  }
+}
+
 // Generic kernel: any padded up to 1024.  Thread j owns dims j, j+256, ...;
 // tokens are processed in groups of 8 with one block reduction per group.
 template <int KB, int VB, bool RAW>
@@ -794,14 +832,16 @@ __global__ __launch_bounds__(kThreads) void decode_generic_kernel(
   for (int t0 = t_begin; t0 < t_end; t0 += G) {
     if constexpr (KQ) {
       float pd[G];
+      const int xmask = kperm_mask(P, KB);
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         pd[g] = 0.0f;
         const int t = t0 + g;
         if (t >= t_end) continue;
         const uint8_t *row = iv.k_rows + (size_t)t * kstride;
+        const int x = t & xmask;
         for (int i = threadIdx.x; i < own; i += kThreads)
-          pd[g] = fmaf(s_q[i], cbv<KB>(code_at<KB>(row, i)), pd[g]);
+          pd[g] = fmaf(s_q[i], cbv<KB>(kcode_at<KB>(row, i, x)), pd[g]);
       }
 #pragma unroll
       for (int g = 0; g < G; ++g) {

@@ -1,7 +1,9 @@
 // device.hpp -- data layout shared by the host C ABI and the gfx950 kernels.
 //
 // One attention head ("context") owns, in device HBM:
-//   k_codes [cap][k_pb] u8   packed K codes, reference byte layout
+//   k_codes [cap][k_pb] u8   packed K codes, reference bytes; for 2/4-bit K at
+//                            padded 64/128 the bytes of slot s are stored in
+//                            XOR order (kperm_mask below)
 //   v_codes [cap][v_pb] u8   packed V codes       (cache/ring_buffer.cpp:47-84)
 //   k_scale [cap] f32, v_scale [cap] f32          L2 norms (1.0 for bits=16)
 //   raw_k/raw_v [hyb][dim] f32                    hybrid mirror (attention.cpp:356-365)
@@ -43,6 +45,20 @@ struct HeadDesc {
 
 __host__ __device__ inline int packed_bytes(int padded, int bits) {
   return bits == 16 ? padded * 4 : (padded * bits + 7) / 8;
+}
+
+// K rows of 2/4-bit codes at padded 64 or 128 are stored with their bytes
+// permuted per slot: stored[j ^ (slot & mask)] = reference[j], with mask =
+// min(row bytes, 32) - 1 (0 = unpermuted).  Decode gives lane l the token of
+// slot l mod 64, so at any static byte position the 32 lanes of a half-wave
+// read 32 different byte positions of their rows; the K lookup table keeps
+// position jj in LDS bank jj, and its reads are conflict-free.  The byte
+// values are the reference's; adaptq_read_slots returns them in reference
+// order.
+__host__ __device__ constexpr int kperm_mask(int padded, int bits) {
+  return (bits == 2 || bits == 4) && (padded == 64 || padded == 128)
+             ? ((padded * bits / 8) < 32 ? (padded * bits / 8) : 32) - 1
+             : 0;
 }
 
 // State after appending n tokens starting from s, restating

@@ -44,6 +44,20 @@ __device__ __forceinline__ int code_at(const uint8_t *row, int i) {
   }
 }
 
+// Code i of a K row stored in the slot's XOR byte order (x = slot & mask,
+// kperm_mask in device.hpp; x = 0 for unpermuted rows).
+template <int B>
+__device__ __forceinline__ int kcode_at(const uint8_t *row, int i, int x) {
+  if constexpr (B == 4) {
+    const uint32_t b = row[(i >> 1) ^ x];
+    return (i & 1) ? (b & 15) : (b >> 4);
+  } else if constexpr (B == 2) {
+    return (row[(i >> 2) ^ x] >> (6 - 2 * (i & 3))) & 3;
+  } else {
+    return code_at<B>(row, i);
+  }
+}
+
 template <int B>
 __device__ __forceinline__ float cbv(int i) {
   return cb<B>(i);
@@ -106,12 +120,13 @@ __global__ __launch_bounds__(kThreads) void sparse_logits_kernel(HeadDesc *const
   if (i >= n) return;
   const int slot = (int)(((long long)d->st.head - n + cap + i) % cap);
   const uint8_t *row = d->k_codes + (size_t)slot * d->k_pb;
+  const int x = slot & kperm_mask(P, KB);
   // 8 FMA lanes over codes L, L+8, ...; lanes summed pairwise.
   float s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   for (int j = 0; j < P; j += 8)
 #pragma unroll
     for (int L = 0; L < 8; ++L)
-      if (j + L < P) s[L] = fmaf(cbv<KB>(code_at<KB>(row, j + L)), s_q[j + L], s[L]);
+      if (j + L < P) s[L] = fmaf(cbv<KB>(kcode_at<KB>(row, j + L, x)), s_q[j + L], s[L]);
   const float t0 = s[0] + s[4], t1 = s[1] + s[5], t2 = s[2] + s[6], t3 = s[3] + s[7];
   const float dot = (t0 + t1) + (t2 + t3);
   const float attn_s = 1.0f / (sqrtf((float)dim) * (float)P);
