@@ -152,6 +152,49 @@ __device__ void build_klut(float *lut, const float *qr) {
   }
 }
 
+// Fixed-point K table for 2- and 4-bit codes: entry[b][jj] = trunc(f * the
+// byte's contribution qr . CB[codes]), f the largest power of two with
+// f * max|CB| * sum_i |qr_i| <= 2^29, so every partial sum of a row's lookups
+// stays below 2^29 + 64 in magnitude and a row's lookups add in int32, two per
+// v_add3_u32.  f being a power of two, an entry is the float table's entry
+// scaled exactly, truncated by less than one unit (2^-28 of the bound); the
+// 64-term sum is then exact, where a float sum would round at every step.  A
+// byte splits into a high half (code pair or code) taken per wave, so its
+// codebook index is wave-uniform, and a low half unrolled over compile-time
+// codebook entries.
+template <int KB>
+struct KMaxCode {
+  static constexpr float value = KB == 4 ? 2.4008f : 1.5104f;  // max |CB|
+};
+
+template <int P, int KB>
+__device__ void build_klut_fixed(int32_t *lut, const float *qr, float f) {
+  constexpr int NB = P * KB / 8;  // byte positions
+  const int j = threadIdx.x & 63;
+  const int nw = blockDim.x >> 6;
+  if (j >= NB) return;
+  float b[16];
+  float qa0, qa1 = 0.0f;
+  if constexpr (KB == 4) {
+    qa0 = qr[2 * j] * f;
+    const float qb = qr[2 * j + 1] * f;
+#pragma unroll
+    for (int lo = 0; lo < 16; ++lo) b[lo] = qb * cbv<4>(lo);
+  } else {
+    qa0 = qr[4 * j] * f;
+    qa1 = qr[4 * j + 1] * f;
+    const float qb0 = qr[4 * j + 2] * f, qb1 = qr[4 * j + 3] * f;
+#pragma unroll
+    for (int lo = 0; lo < 16; ++lo) b[lo] = qb0 * cbv<2>(lo >> 2) + qb1 * cbv<2>(lo & 3);
+  }
+  for (int hi = threadIdx.x >> 6; hi < 16; hi += nw) {
+    const int h = __builtin_amdgcn_readfirstlane(hi);
+    const float a = KB == 4 ? qa0 * CB::b4[h] : qa0 * CB::b2[h >> 2] + qa1 * CB::b2[h & 3];
+#pragma unroll
+    for (int lo = 0; lo < 16; ++lo) lut[(h * 16 + lo) * 64 + j] = (int32_t)(a + b[lo]);
+  }
+}
+
 // Codebook tables for V; distinct entries never share an LDS bank.
 // 2-bit: nibble n (two codes) -> float2 at byte 16n; 4-bit: nibble n -> float
 // at byte 16n (with a 16-byte stride the high nibble's table offset is its
@@ -515,7 +558,7 @@ __device__ __forceinline__ void transpose_segments(uint32_t *x) {
 //   4-bit: nibble (1 code)  -> float, 16 entries
 //   3-bit: code             -> float, 8 entries
 template <int P, int KB, int VB, bool RAW>
-__global__ __launch_bounds__(kLutThreads, 2) void decode_lut_kernel(
+__global__ __launch_bounds__(kLutThreads, (KB == 2 || KB == 4) ? 4 : 2) void decode_lut_kernel(
     HeadDesc *const *item_desc, const float *__restrict__ queries, int chunk, int n_splits,
     float *__restrict__ partials, float *__restrict__ outs) {
   constexpr bool KQ = KB != 16;
@@ -581,16 +624,12 @@ __global__ __launch_bounds__(kLutThreads, 2) void decode_lut_kernel(
 
   // K rows in XOR byte order (kperm_mask): this lane's tokens all sit in
   // slots = lane (mod 64), so stored byte 4i+k of its rows is byte position
-  // jj = (4i+k) ^ x.  xr[i] holds 4*jj for k = 0..3 in its bytes; v_perm
-  // joins a code byte b and 4*jj into the table offset b*256 + 4*jj.
+  // jj = (4i+k) ^ x.  A word xr[i] holds 4*jj for k = 0..3 in its bytes
+  // (lx0 = 4x in every byte, XORed with the static part); v_perm joins a code
+  // byte b and 4*jj into the table offset b*256 + 4*jj.
   constexpr bool KPERM = KQ && (KB == 2 || KB == 4);
   constexpr uint32_t kXMask = (uint32_t)kperm_mask(P, KB);
-  uint32_t xr[KPERM ? KW : 1];
-  if constexpr (KPERM) {
-    const uint32_t lx = (4u * ((uint32_t)lane & kXMask)) * 0x01010101u;
-#pragma unroll
-    for (int i = 0; i < KW; ++i) xr[i] = ((uint32_t)(16 * i) * 0x01010101u + 0x0C080400u) ^ lx;
-  }
+  const uint32_t lx0 = (4u * ((uint32_t)lane & kXMask)) * 0x01010101u;
   // Row offsets are 32-bit (the host routes rings of 4 GiB and more to the
   // generic kernel) so loads take a scalar base plus one VGPR offset.
   float ksc = 1.0f, vsc = 1.0f;
@@ -603,7 +642,26 @@ __global__ __launch_bounds__(kLutThreads, 2) void decode_lut_kernel(
   }
 
   load_query<P>(s_q, queries + (size_t)item * dim, dim, KQ, signs);
-  if constexpr (KQ) build_klut<P, KB>(s_klut, s_q);
+  // fixed-point scale of the K table (2/4-bit keys): f and 1/f
+  __shared__ float s_fix[2];
+  if constexpr (KPERM) {
+    if (threadIdx.x < 64) {
+      float a = 0.0f;
+#pragma unroll
+      for (int i = 0; i < P / 64; ++i) a += fabsf(s_q[threadIdx.x + 64 * i]);
+      a = wave_sum(a) * KMaxCode<KB>::value;
+      if (threadIdx.x == 0) {
+        // the largest power of two f with f * max|CB| * sum|qr| <= 2^29
+        const float f = a > 0.0f ? ldexpf(1.0f, min(ilogbf(536870912.0f / a), 100)) : 1.0f;
+        s_fix[0] = f;
+        s_fix[1] = 1.0f / f;
+      }
+    }
+    __syncthreads();
+    build_klut_fixed<P, KB>(reinterpret_cast<int32_t *>(s_klut), s_q, s_fix[0]);
+  } else if constexpr (KQ) {
+    build_klut<P, KB>(s_klut, s_q);
+  }
   if constexpr (VQ) build_vlut<VB>(s_vlut);
   __syncthreads();
 
@@ -612,6 +670,7 @@ __global__ __launch_bounds__(kLutThreads, 2) void decode_lut_kernel(
   // reference's natural-unit logits and expf, bit for bit.
   constexpr float kLog2e = 1.44269504088896340736f;
   const float attn_s = KQ ? kLog2e / (sqrtf((float)dim) * (float)P) : 1.0f / sqrtf((float)dim);
+  const float attn_fix = KPERM ? attn_s * s_fix[1] : attn_s;  // undoes the table's fixed point
   const float isp = VQ ? 1.0f / sqrtf((float)P) : 1.0f;
   const uint32_t vmask = 0xF0u;
   auto wexp = [](float z) -> float {
@@ -623,30 +682,37 @@ __global__ __launch_bounds__(kLutThreads, 2) void decode_lut_kernel(
   auto tile_logit = [&](const uint32_t *kcw, float kscale, int tile_base) -> float {
     const int tt = tile_base + lane;
     float dot;
-    if constexpr (KQ) {
+    if constexpr (KQ && KB == 3) {
       float p4[4];
-      if constexpr (KB == 3) {
 #pragma unroll
-        for (int m = 0; m < 4; ++m) p4[m] = s_klut[m * 64 + pair3(kcw, 0, m)];
+      for (int m = 0; m < 4; ++m) p4[m] = s_klut[m * 64 + pair3(kcw, 0, m)];
 #pragma unroll
-        for (int g = 1; g < P / 8; ++g)
+      for (int g = 1; g < P / 8; ++g)
 #pragma unroll
-          for (int m = 0; m < 4; ++m) p4[m] += s_klut[(4 * g + m) * 64 + pair3(kcw, g, m)];
-      } else {
-        // selector k: byte 0 <- byte k of xr[i], byte 1 <- code byte k, bytes 2-3 <- 0
-        const uint8_t *lb = reinterpret_cast<const uint8_t *>(s_klut);
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-          p4[k] = *reinterpret_cast<const float *>(
-              lb + __builtin_amdgcn_perm(kcw[0], xr[0], 0x0C0C0000u | ((4u + k) << 8) | (uint32_t)k));
-#pragma unroll
-        for (int i = 1; i < KW; ++i)
-#pragma unroll
-          for (int k = 0; k < 4; ++k)
-            p4[k] += *reinterpret_cast<const float *>(
-                lb + __builtin_amdgcn_perm(kcw[i], xr[i], 0x0C0C0000u | ((4u + k) << 8) | (uint32_t)k));
-      }
+        for (int m = 0; m < 4; ++m) p4[m] += s_klut[(4 * g + m) * 64 + pair3(kcw, g, m)];
       dot = ((p4[0] + p4[1]) + (p4[2] + p4[3])) * attn_s * kscale;
+    } else if constexpr (KQ) {
+      // selector k: byte 0 <- byte k of xr[i], byte 1 <- code byte k, bytes 2-3 <- 0.
+      // xr[i] is rebuilt per tile (one XOR each) rather than held in 16
+      // registers; the empty asm keeps the compiler from hoisting it.
+      const uint8_t *lb = reinterpret_cast<const uint8_t *>(s_klut);
+      uint32_t lx = lx0;
+      asm volatile("" : "+v"(lx));
+      uint32_t xr[KW];
+#pragma unroll
+      for (int i = 0; i < KW; ++i) xr[i] = ((uint32_t)(16 * i) * 0x01010101u + 0x0C080400u) ^ lx;
+      auto look = [&](int i, int k) -> int32_t {
+        return *reinterpret_cast<const int32_t *>(
+            lb + __builtin_amdgcn_perm(kcw[i], xr[i], 0x0C0C0000u | ((4u + k) << 8) | (uint32_t)k));
+      };
+      int32_t p4[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) p4[k] = look(0, k) + look(1, k);
+#pragma unroll
+      for (int i = 2; i < KW; i += 2)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) p4[k] = p4[k] + look(i, k) + look(i + 1, k);
+      dot = (float)((p4[0] + p4[1]) + (p4[2] + p4[3])) * (attn_fix * kscale);
     } else {
       // fp32 keys: the reference's sequential, unfused dot product
       // (attention.cpp:212-219 and :497-502), so that peaked softmaxes see
