@@ -48,6 +48,18 @@ SIGNATURES = {
                                                C.c_int, C.c_void_p]),
     "adaptq_mha_compute_all_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p,
                                                 C.c_void_p]),
+    "adaptq_ggml_append_f32": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int,
+                                         C.c_int, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t,
+                                         C.c_int]),
+    "adaptq_ggml_attn_f32": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int,
+                                       C.c_size_t, C.c_size_t, C.c_void_p, C.c_size_t,
+                                       C.c_size_t]),
+    "adaptq_ggml_append_f32_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,
+                                                C.c_int, C.c_int, C.c_size_t, C.c_size_t,
+                                                C.c_size_t, C.c_size_t, C.c_int, C.c_void_p]),
+    "adaptq_ggml_attn_f32_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int,
+                                              C.c_size_t, C.c_size_t, C.c_void_p, C.c_size_t,
+                                              C.c_size_t, C.c_void_p]),
     "adaptq_plan_create": (C.c_void_p, [C.POINTER(C.c_void_p), C.c_int]),
     "adaptq_plan_destroy": (None, [C.c_void_p]),
     "adaptq_plan_append_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,

@@ -127,8 +127,10 @@ struct Mha {
   int device = 0;
   std::mutex mu;  // whole-MHA calls; taken before any head's lock
   DevBuf d_list;  // [n_heads] device pointers to the heads' descriptors
+  DevBuf d_rep;   // [reps][n_heads] the same pointers repeated (multi-query launches)
+  int rep_n = 0;  // reps held in d_rep
   DevBuf d_ws, d_io, d_stage;
-  std::vector<float> pack_k, pack_v;
+  std::vector<float> pack_k, pack_v, pack_q;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -429,19 +431,37 @@ bool flush_all_locked(Mha *m, const char *fn) {
 // has flushed).  Returns the common ring size, or -2 when the heads differ in
 // size or branch (the caller then works head by head), or -1 on error.
 // Queries/outs are device pointers; the launch is asynchronous on `s`.
-int launch_all_locked(Mha *m, const float *dq, float *dout, hipStream_t s, const char *fn) {
+// With reps > 1 the launch holds reps queries per head, ordered [rep][head]
+// (item r * n_heads + h is head h).
+int launch_all_locked(Mha *m, const float *dq, float *dout, hipStream_t s, const char *fn,
+                      int reps = 1) {
   const Ctx *c0 = m->heads[0];
   const int n = c0->st.size;
   const Mode mode = mode_of(c0);
   for (const Ctx *c : m->heads)
     if (c->st.size != n || mode_of(c) != mode) return -2;
-  const int H = m->n_heads;
+  const int H = m->n_heads * reps;
   aq::DecodeShape sh{c0->dim, c0->padded, c0->k_bits, c0->v_bits, mode == Mode::Hybrid,
                      n > 0 ? n : 1};
   const size_t wsf = mode == Mode::Sparse ? aq::sparse_workspace_floats(H, sh)
                                           : aq::decode_workspace_floats(H, sh);
   if (hip_fail(m->d_ws.ensure(wsf * 4), fn)) return -1;
   auto **items = static_cast<aq::HeadDesc **>(m->d_list.p);
+  if (reps > 1) {
+    if (m->rep_n != reps) {
+      std::vector<aq::HeadDesc *> list((size_t)H);
+      for (int i = 0; i < H; ++i) list[i] = m->heads[i % m->n_heads]->d_desc;
+      m->rep_n = 0;
+      if (hip_fail(m->d_rep.ensure(list.size() * sizeof(void *)), fn)) return -1;
+      if (hip_fail(hipMemcpyAsync(m->d_rep.p, list.data(), list.size() * sizeof(void *),
+                                  hipMemcpyHostToDevice, s),
+                   fn) ||
+          hip_fail(hipStreamSynchronize(s), fn))
+        return -1;
+      m->rep_n = reps;
+    }
+    items = static_cast<aq::HeadDesc **>(m->d_rep.p);
+  }
   hipError_t e;
   if (n == 0)  // the decode kernels write zeros for empty rings
     e = aq::launch_decode(items, H, sh, dq, dout, static_cast<float *>(m->d_ws.p), s);
@@ -575,6 +595,7 @@ void adaptq_mha_destroy(adaptq_mha_t h) {
   {
     DeviceGuard g(m->device);
     m->d_list.release();
+    m->d_rep.release();
     m->d_ws.release();
     m->d_io.release();
     m->d_stage.release();
@@ -754,6 +775,197 @@ int adaptq_mha_compute_all_device(adaptq_mha_t h, const float *d_queries, float 
               "use adaptq_mha_compute_all");
     return -1;
   }
+  return n;
+}
+
+// ---- ggml operator forms (GGML_OP_ADAPTQ_APPEND / GGML_OP_ADAPTQ_ATTN) ----
+
+}  // extern "C"
+
+namespace {
+
+// Shape and stride checks shared by the ggml forms: dims must match the MHA,
+// strides are byte strides of f32 rows (multiples of 4).
+bool ggml_shape_ok(Mha *m, int head_dim, int n_heads, int n_rows, const size_t *strides,
+                   int n_strides, const char *fn) {
+  if (head_dim != m->heads[0]->dim || n_heads != m->n_heads) {
+    set_errorf(fn, "tensor shape does not match the MHA (head_dim, n_heads)");
+    return false;
+  }
+  if (n_rows < 0) {
+    set_errorf(fn, "negative token or query count");
+    return false;
+  }
+  for (int i = 0; i < n_strides; ++i)
+    if (strides[i] % 4 != 0) {
+      set_errorf(fn, "strides must be multiples of 4 bytes (f32 rows)");
+      return false;
+    }
+  return true;
+}
+
+const float *row_at(const float *base, size_t a, size_t sa, size_t b, size_t sb) {
+  return reinterpret_cast<const float *>(reinterpret_cast<const uint8_t *>(base) + a * sa + b * sb);
+}
+
+}  // namespace
+
+extern "C" {
+
+int adaptq_ggml_append_f32(adaptq_mha_t h, const float *k, const float *v, int head_dim,
+                           int n_heads, int n_tokens, size_t k_nb1, size_t k_nb2, size_t v_nb1,
+                           size_t v_nb2, int first_pos) {
+  (void)first_pos;
+  const char *fn = "adaptq_ggml_append_f32";
+  if (!require_handle(h, fn)) return -1;
+  Mha *m = static_cast<Mha *>(h);
+  const size_t st[4] = {k_nb1, k_nb2, v_nb1, v_nb2};
+  if (!ggml_shape_ok(m, head_dim, n_heads, n_tokens, st, 4, fn)) return -1;
+  if (n_tokens == 0) return 0;
+  if (!require_pointer(k, fn, "k") || !require_pointer(v, fn, "v")) return -1;
+  std::lock_guard<std::mutex> gm(m->mu);
+  HeadLocks locks(m);
+  for (int t = 0; t < n_tokens; ++t) {
+    for (int i = 0; i < m->n_heads; ++i) {
+      Ctx *c = m->heads[i];
+      const float *kr = row_at(k, (size_t)i, k_nb1, (size_t)t, k_nb2);
+      const float *vr = row_at(v, (size_t)i, v_nb1, (size_t)t, v_nb2);
+      c->stage_k.insert(c->stage_k.end(), kr, kr + head_dim);
+      c->stage_v.insert(c->stage_v.end(), vr, vr + head_dim);
+      ++c->staged;
+    }
+    if (m->heads[0]->staged >= kStageTokens && !flush_all_locked(m, fn)) return -1;
+  }
+  clear_error();
+  return 0;
+}
+
+int adaptq_ggml_attn_f32(adaptq_mha_t h, const float *q, int head_dim, int n_heads, int n_queries,
+                         size_t q_nb1, size_t q_nb2, float *dst, size_t d_nb1, size_t d_nb2) {
+  const char *fn = "adaptq_ggml_attn_f32";
+  if (!require_handle(h, fn)) return -1;
+  Mha *m = static_cast<Mha *>(h);
+  const size_t st[4] = {q_nb1, q_nb2, d_nb1, d_nb2};
+  if (!ggml_shape_ok(m, head_dim, n_heads, n_queries, st, 4, fn)) return -1;
+  if (n_queries > 0 && (!require_pointer(q, fn, "q") || !require_pointer(dst, fn, "dst")))
+    return -1;
+  std::lock_guard<std::mutex> gm(m->mu);
+  HeadLocks locks(m);
+  if (!flush_all_locked(m, fn)) return -1;
+  const int H = m->n_heads, dim = head_dim;
+  if (n_queries == 0) {
+    clear_error();
+    return m->heads[0]->st.size;
+  }
+  // queries packed [query][head][dim]; outputs come back in the same order
+  const size_t rows = (size_t)n_queries * H;
+  m->pack_q.resize(2 * rows * dim);
+  float *pq = m->pack_q.data(), *po = pq + rows * dim;
+  for (int j = 0; j < n_queries; ++j)
+    for (int i = 0; i < H; ++i)
+      std::memcpy(pq + ((size_t)j * H + i) * dim, row_at(q, (size_t)i, q_nb1, (size_t)j, q_nb2),
+                  (size_t)dim * 4);
+  DeviceGuard g(m->device);
+  hipStream_t s = lib_stream(m->device);
+  const size_t io = align256(rows * dim * 4);
+  if (hip_fail(m->d_io.ensure(2 * io), fn)) return -1;
+  float *dq = static_cast<float *>(m->d_io.p);
+  float *dout = reinterpret_cast<float *>(static_cast<uint8_t *>(m->d_io.p) + io);
+  if (hip_fail(hipMemcpyAsync(dq, pq, rows * dim * 4, hipMemcpyHostToDevice, s), fn)) return -1;
+  int n = launch_all_locked(m, dq, dout, s, fn, n_queries);
+  if (n == -2) {  // heads differ in size or branch: head by head, all queries of a head at once
+    std::vector<float> hq((size_t)n_queries * dim), ho((size_t)n_queries * dim);
+    for (int i = 0; i < H; ++i) {
+      for (int j = 0; j < n_queries; ++j)
+        std::memcpy(hq.data() + (size_t)j * dim, pq + ((size_t)j * H + i) * dim, (size_t)dim * 4);
+      const int r = compute_locked(m->heads[i], hq.data(), n_queries, ho.data(), fn);
+      if (r < 0) return -1;
+      if (i == 0) n = r;
+      for (int j = 0; j < n_queries; ++j)
+        std::memcpy(po + ((size_t)j * H + i) * dim, ho.data() + (size_t)j * dim, (size_t)dim * 4);
+    }
+  } else {
+    if (n < 0) return -1;
+    hipError_t e = hipMemcpyAsync(po, dout, rows * dim * 4, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (hip_fail(e, fn)) return -1;
+  }
+  for (int j = 0; j < n_queries; ++j)
+    for (int i = 0; i < H; ++i)
+      std::memcpy(const_cast<float *>(row_at(dst, (size_t)i, d_nb1, (size_t)j, d_nb2)),
+                  po + ((size_t)j * H + i) * dim, (size_t)dim * 4);
+  clear_error();
+  return n;
+}
+
+int adaptq_ggml_append_f32_device(adaptq_mha_t h, const float *d_k, const float *d_v,
+                                  int head_dim, int n_heads, int n_tokens, size_t k_nb1,
+                                  size_t k_nb2, size_t v_nb1, size_t v_nb2, int first_pos,
+                                  void *stream) {
+  (void)first_pos;
+  const char *fn = "adaptq_ggml_append_f32_device";
+  if (!require_handle(h, fn)) return -1;
+  Mha *m = static_cast<Mha *>(h);
+  const size_t st[4] = {k_nb1, k_nb2, v_nb1, v_nb2};
+  if (!ggml_shape_ok(m, head_dim, n_heads, n_tokens, st, 4, fn)) return -1;
+  if (n_tokens == 0) return 0;
+  if (!require_pointer(d_k, fn, "d_k") || !require_pointer(d_v, fn, "d_v")) return -1;
+  std::lock_guard<std::mutex> gm(m->mu);
+  HeadLocks locks(m);
+  if (!flush_all_locked(m, fn)) return -1;
+  const Ctx *c0 = m->heads[0];
+  const int H = m->n_heads;
+  DeviceGuard g(m->device);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // [head][token][dim] rows for the append launch
+  const size_t half = align256((size_t)H * n_tokens * head_dim * 4);
+  if (hip_fail(m->d_stage.ensure(2 * half), fn)) return -1;
+  float *dk = static_cast<float *>(m->d_stage.p);
+  float *dv = reinterpret_cast<float *>(static_cast<uint8_t *>(m->d_stage.p) + half);
+  hipError_t e = aq::launch_gather_rows(dk, d_k, H, n_tokens, head_dim, k_nb1, k_nb2, s);
+  if (e == hipSuccess) e = aq::launch_gather_rows(dv, d_v, H, n_tokens, head_dim, v_nb1, v_nb2, s);
+  if (e == hipSuccess)
+    e = aq::launch_append(static_cast<aq::HeadDesc **>(m->d_list.p), H, c0->dim, c0->padded,
+                          c0->k_bits, c0->v_bits, dk, dv, n_tokens, s);
+  if (hip_fail(e, fn)) return -1;
+  for (Ctx *c : m->heads) c->st = aq::ring_after(c->st, n_tokens, c->cap, c->hyb);
+  return 0;
+}
+
+int adaptq_ggml_attn_f32_device(adaptq_mha_t h, const float *d_q, int head_dim, int n_heads,
+                                int n_queries, size_t q_nb1, size_t q_nb2, float *d_dst,
+                                size_t d_nb1, size_t d_nb2, void *stream) {
+  const char *fn = "adaptq_ggml_attn_f32_device";
+  if (!require_handle(h, fn)) return -1;
+  Mha *m = static_cast<Mha *>(h);
+  const size_t st[4] = {q_nb1, q_nb2, d_nb1, d_nb2};
+  if (!ggml_shape_ok(m, head_dim, n_heads, n_queries, st, 4, fn)) return -1;
+  if (n_queries > 0 && (!require_pointer(d_q, fn, "d_q") || !require_pointer(d_dst, fn, "d_dst")))
+    return -1;
+  std::lock_guard<std::mutex> gm(m->mu);
+  HeadLocks locks(m);
+  if (!flush_all_locked(m, fn)) return -1;
+  if (n_queries == 0) return m->heads[0]->st.size;
+  const int H = m->n_heads;
+  DeviceGuard g(m->device);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const size_t rows = (size_t)n_queries * H;
+  const size_t io = align256(rows * head_dim * 4);
+  if (hip_fail(m->d_io.ensure(2 * io), fn)) return -1;
+  float *dq = static_cast<float *>(m->d_io.p);
+  float *dout = reinterpret_cast<float *>(static_cast<uint8_t *>(m->d_io.p) + io);
+  // queries as [query][head][dim]
+  if (hip_fail(aq::launch_gather_rows(dq, d_q, n_queries, H, head_dim, q_nb2, q_nb1, s), fn))
+    return -1;
+  const int n = launch_all_locked(m, dq, dout, s, fn, n_queries);
+  if (n == -2) {
+    set_error("adaptq_ggml_attn_f32_device: heads differ in ring size or branch; "
+              "use adaptq_ggml_attn_f32");
+    return -1;
+  }
+  if (n < 0) return -1;
+  if (hip_fail(aq::launch_scatter_rows(d_dst, dout, n_queries, H, head_dim, d_nb2, d_nb1, s), fn))
+    return -1;
   return n;
 }
 

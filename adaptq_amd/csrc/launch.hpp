@@ -41,4 +41,11 @@ hipError_t launch_decode_sparse(HeadDesc *const *d_item_desc, int n_items,
                                 const float *d_queries, float *d_outs, float *d_workspace,
                                 hipStream_t stream);
 
+// Strided rows <-> contiguous rows (layout.hip): contiguous row r = a * B + b
+// of dim floats is the row at byte offset a * sa + b * sb of the strided side.
+hipError_t launch_gather_rows(float *d_dst, const void *d_src, int A, int B, int dim, size_t sa,
+                              size_t sb, hipStream_t stream);
+hipError_t launch_scatter_rows(void *d_dst, const float *d_src, int A, int B, int dim, size_t sa,
+                               size_t sb, hipStream_t stream);
+
 }  // namespace aq

@@ -175,6 +175,41 @@ int adaptq_mha_append_all_device(adaptq_mha_t mha, const float *d_keys,
 int adaptq_mha_compute_all_device(adaptq_mha_t mha, const float *d_queries,
                                   float *d_outs, void *stream);
 
+/* ---- ggml operator forms ----
+ * Replace the forward functions of the reference's ggml integration
+ * (integration/ggml_operator_patch.md:6-117: GGML_OP_ADAPTQ_APPEND and
+ * GGML_OP_ADAPTQ_ATTN nodes carrying an adaptq_mha_t in op_params), with
+ * ggml's tensor layout: f32 tensors [head_dim, n_heads, n] with byte strides
+ * nb1 (between heads) and nb2 (between tokens or queries), multiples of 4.
+ * The reference's CPU forward passes q + h*head_dim as if a head's queries
+ * were contiguous, which holds only for n_queries == 1; these honour nb2.
+ *
+ * append: tokens t = 0..n_tokens-1 of k and v go to every head at position
+ * first_pos + t.  attn: every query attends over its head's whole current
+ * cache (the reference's compute_batch semantics; no causal mask), dst gets
+ * the outputs in q's layout.  Returns 0 (append) or the number of cached
+ * tokens (attn), -1 on error.  The host forms are synchronous; the _device
+ * forms take device pointers and run asynchronously on `stream` (a
+ * hipStream_t, for a ggml HIP backend), sharing the MHA's scratch memory:
+ * calls on one MHA from different streams must be ordered by the caller. */
+int adaptq_ggml_append_f32(adaptq_mha_t mha, const float *k, const float *v,
+                           int head_dim, int n_heads, int n_tokens,
+                           size_t k_nb1, size_t k_nb2, size_t v_nb1,
+                           size_t v_nb2, int first_pos);
+int adaptq_ggml_attn_f32(adaptq_mha_t mha, const float *q, int head_dim,
+                         int n_heads, int n_queries, size_t q_nb1,
+                         size_t q_nb2, float *dst, size_t dst_nb1,
+                         size_t dst_nb2);
+int adaptq_ggml_append_f32_device(adaptq_mha_t mha, const float *d_k,
+                                  const float *d_v, int head_dim, int n_heads,
+                                  int n_tokens, size_t k_nb1, size_t k_nb2,
+                                  size_t v_nb1, size_t v_nb2, int first_pos,
+                                  void *stream);
+int adaptq_ggml_attn_f32_device(adaptq_mha_t mha, const float *d_q,
+                                int head_dim, int n_heads, int n_queries,
+                                size_t q_nb1, size_t q_nb2, float *d_dst,
+                                size_t dst_nb1, size_t dst_nb2, void *stream);
+
 /* ---- Batched device-pointer path ----
  * Extension, no counterpart in the reference.  For callers whose data is
  * already in device memory (torch-ROCm tensors, serving loops) and for the

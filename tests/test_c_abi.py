@@ -121,3 +121,20 @@ def test_pybind_module_loads():
     assert hasattr(m, "MHAContext")
     with pytest.raises(RuntimeError, match="invalid parameters"):
         m.MHAContext(0, 64, 4, 2, 16)  # rejected before any device call
+
+
+def test_llama_adapter_header_compiles():
+    """include/adapter_llamacpp.h builds as llama.cpp would include it, and a
+    program using it links against libadaptq.so (run on the GPU in
+    test_gpu_ggml.py)."""
+    import shutil
+    import subprocess
+    import tempfile
+    if not shutil.which("g++"):
+        pytest.skip("no g++")
+    src = os.path.join(ROOT, "tests", "cpp", "llama_adapter_check.cpp")
+    with tempfile.TemporaryDirectory() as d:
+        r = subprocess.run(["g++", "-std=c++17", "-I", os.path.join(ROOT, "include"), src,
+                            "-L", os.path.join(ROOT, "adaptq_amd"), "-ladaptq",
+                            "-o", os.path.join(d, "check")], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
