@@ -60,6 +60,8 @@ SIGNATURES = {
     "adaptq_ggml_attn_f32_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int,
                                               C.c_size_t, C.c_size_t, C.c_void_p, C.c_size_t,
                                               C.c_size_t, C.c_void_p]),
+    "adaptq_snapshot_save": (C.c_int, [C.POINTER(C.c_void_p), C.c_int, C.c_char_p]),
+    "adaptq_snapshot_load": (C.c_int, [C.POINTER(C.c_void_p), C.c_int, C.c_char_p]),
     "adaptq_plan_create": (C.c_void_p, [C.POINTER(C.c_void_p), C.c_int]),
     "adaptq_plan_destroy": (None, [C.c_void_p]),
     "adaptq_plan_append_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,

@@ -1156,3 +1156,332 @@ int adaptq_plan_compute_device(adaptq_plan_t h, const float *d_queries, float *d
 }
 
 }  // extern "C"
+
+// ---- Packed-ring snapshots (AQSS v2) ----
+//
+// Layout (little-endian), as documented in reference replay/session_snapshot.h:16-40
+// and written/read by session_snapshot.cpp:205-300:
+//   u32 magic 0x41515353, u32 version 2, i32 n_layers, i32 n_heads, i32 dim,
+//   i32 bits, i32 n_tokens, i32 n_heads_total, u64 flags
+//   per head (layer-major): i32 layer, i32 head, i32 cache_size, i32 slot_bytes,
+//     u64 data_bytes, data[cache_size * 2 * slot_bytes] (K slots then V slots),
+//     i32 n_scales, f32 scales[2 * cache_size], i32 n_tags, u8 tags[2 * cache_size]
+//   [flags & 2: per head i32 len + strategy state]  [flags & 1: token log]
+
+namespace {
+
+uint8_t snap_tag(int bits) { return bits == 16 ? 0xFF : (uint8_t)bits; }  // har_fixed.cpp:40-42, fp_passthrough.cpp:36
+
+struct SnapOut {
+  std::vector<uint8_t> buf;
+  template <class T>
+  void put(T v) {
+    const uint8_t *p = reinterpret_cast<const uint8_t *>(&v);
+    buf.insert(buf.end(), p, p + sizeof(T));
+  }
+  void put_bytes(const void *p, size_t n) {
+    const uint8_t *b = static_cast<const uint8_t *>(p);
+    buf.insert(buf.end(), b, b + n);
+  }
+};
+
+struct SnapIn {
+  const uint8_t *p;
+  size_t n, off = 0;
+  bool ok = true;
+  template <class T>
+  T get() {
+    T v{};
+    if (n - off < sizeof(T)) {
+      ok = false;
+      off = n;
+      return v;
+    }
+    std::memcpy(&v, p + off, sizeof(T));
+    off += sizeof(T);
+    return v;
+  }
+  const uint8_t *take(uint64_t bytes) {
+    if (bytes > n - off) {
+      ok = false;
+      off = n;
+      return nullptr;
+    }
+    const uint8_t *r = p + off;
+    off += (size_t)bytes;
+    return r;
+  }
+};
+
+// The rings of one head in logical order (oldest first), K rows in the
+// reference's byte order.  Caller holds the head's lock and has flushed.
+bool read_ring(Ctx *c, std::vector<uint8_t> &kc, std::vector<uint8_t> &vc,
+               std::vector<float> &ks, std::vector<float> &vs, const char *fn) {
+  const int n = c->st.size, cap = c->cap;
+  kc.assign((size_t)n * c->k_pb, 0);
+  vc.assign((size_t)n * c->v_pb, 0);
+  ks.assign((size_t)n, 0.f);
+  vs.assign((size_t)n, 0.f);
+  if (n == 0) return true;
+  DeviceGuard g(c->device);
+  aq::HeadDesc hd;
+  hipError_t e = hipMemcpy(&hd, c->d_desc, sizeof(hd), hipMemcpyDeviceToHost);
+  std::vector<uint8_t> ak((size_t)cap * c->k_pb), av((size_t)cap * c->v_pb);
+  std::vector<float> aks((size_t)cap), avs((size_t)cap);
+  if (e == hipSuccess) e = hipMemcpy(ak.data(), hd.k_codes, ak.size(), hipMemcpyDeviceToHost);
+  if (e == hipSuccess) e = hipMemcpy(av.data(), hd.v_codes, av.size(), hipMemcpyDeviceToHost);
+  if (e == hipSuccess) e = hipMemcpy(aks.data(), hd.k_scale, aks.size() * 4, hipMemcpyDeviceToHost);
+  if (e == hipSuccess) e = hipMemcpy(avs.data(), hd.v_scale, avs.size() * 4, hipMemcpyDeviceToHost);
+  if (hip_fail(e, fn)) return false;
+  const int xmask = aq::kperm_mask(c->padded, c->k_bits);
+  for (int i = 0; i < n; ++i) {
+    const int slot = (int)(((long long)c->st.head - n + cap + i) % cap);
+    const uint8_t *kr = ak.data() + (size_t)slot * c->k_pb;
+    uint8_t *ko = kc.data() + (size_t)i * c->k_pb;
+    const int x = slot & xmask;
+    for (int j = 0; j < c->k_pb; ++j) ko[j] = kr[j ^ x];
+    std::memcpy(vc.data() + (size_t)i * c->v_pb, av.data() + (size_t)slot * c->v_pb, c->v_pb);
+    ks[i] = aks[slot];
+    vs[i] = avs[slot];
+  }
+  return true;
+}
+
+// Rebuild a head's ring from logical-order rows: slots 0..n-1, head at n
+// (mod cap), hybrid mirror empty.  Caller holds the head's lock.
+bool write_ring(Ctx *c, int n, const uint8_t *kc, const uint8_t *vc, int row_stride,
+                const float *ks, const float *vs, const char *fn) {
+  const int cap = c->cap;
+  std::vector<uint8_t> ak((size_t)cap * c->k_pb, 0), av((size_t)cap * c->v_pb, 0);
+  std::vector<float> aks((size_t)cap, 1.0f), avs((size_t)cap, 1.0f);
+  const int xmask = aq::kperm_mask(c->padded, c->k_bits);
+  for (int i = 0; i < n; ++i) {
+    const uint8_t *kr = kc + (size_t)i * row_stride;
+    uint8_t *ko = ak.data() + (size_t)i * c->k_pb;
+    const int x = i & xmask;
+    for (int j = 0; j < c->k_pb; ++j) ko[j ^ x] = kr[j];
+    std::memcpy(av.data() + (size_t)i * c->v_pb, vc + (size_t)i * row_stride, c->v_pb);
+    aks[i] = ks[i];
+    avs[i] = vs[i];
+  }
+  aq::RingState st{cap > 0 ? n % cap : 0, n, 0, 0};
+  DeviceGuard g(c->device);
+  aq::HeadDesc hd;
+  hipError_t e = hipMemcpy(&hd, c->d_desc, sizeof(hd), hipMemcpyDeviceToHost);
+  if (e == hipSuccess && cap > 0) e = hipMemcpy(hd.k_codes, ak.data(), ak.size(), hipMemcpyHostToDevice);
+  if (e == hipSuccess && cap > 0) e = hipMemcpy(hd.v_codes, av.data(), av.size(), hipMemcpyHostToDevice);
+  if (e == hipSuccess && cap > 0) e = hipMemcpy(hd.k_scale, aks.data(), aks.size() * 4, hipMemcpyHostToDevice);
+  if (e == hipSuccess && cap > 0) e = hipMemcpy(hd.v_scale, avs.data(), avs.size() * 4, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(&c->d_desc->st, &st, sizeof(st), hipMemcpyHostToDevice);
+  if (hip_fail(e, fn)) return false;
+  c->st = st;
+  c->staged = 0;
+  c->stage_k.clear();
+  c->stage_v.clear();
+  return true;
+}
+
+bool snap_layers_ok(const adaptq_mha_t *layers, int n_layers, const char *fn) {
+  if (!layers || n_layers <= 0) {
+    set_errorf(fn, "need at least one MHA");
+    return false;
+  }
+  for (int l = 0; l < n_layers; ++l)
+    if (!require_handle(layers[l], fn)) return false;
+  const Mha *m0 = static_cast<const Mha *>(layers[0]);
+  const Ctx *c0 = m0->heads[0];
+  for (int l = 1; l < n_layers; ++l) {
+    const Mha *m = static_cast<const Mha *>(layers[l]);
+    const Ctx *c = m->heads[0];
+    if (m->n_heads != m0->n_heads || c->dim != c0->dim || c->k_bits != c0->k_bits ||
+        c->v_bits != c0->v_bits || c->padded != c0->padded) {
+      set_errorf(fn, "layers differ in n_heads, dim or bits");
+      return false;
+    }
+  }
+  return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+int adaptq_snapshot_save(const adaptq_mha_t *layers, int n_layers, const char *path) {
+  const char *fn = "adaptq_snapshot_save";
+  if (!require_pointer(path, fn, "path") || !snap_layers_ok(layers, n_layers, fn)) return -1;
+  const Mha *m0 = static_cast<const Mha *>(layers[0]);
+  const Ctx *c0 = m0->heads[0];
+  const int H = m0->n_heads;
+  const int slot_bytes = std::max(c0->k_pb, c0->v_pb);
+  SnapOut o;
+  o.put<uint32_t>(0x41515353u);
+  o.put<uint32_t>(2u);
+  o.put<int32_t>(n_layers);
+  o.put<int32_t>(H);
+  o.put<int32_t>(c0->dim);
+  o.put<int32_t>(c0->k_bits);
+  const size_t ntok_at = o.buf.size();
+  o.put<int32_t>(0);  // n_tokens: patched below
+  o.put<int32_t>(n_layers * H);
+  o.put<uint64_t>(0);  // no token log, no strategy state
+  int n_tokens = 0;
+  std::vector<uint8_t> kc, vc, pad((size_t)slot_bytes, 0);
+  std::vector<float> ks, vs;
+  for (int l = 0; l < n_layers; ++l) {
+    Mha *m = static_cast<Mha *>(layers[l]);
+    std::lock_guard<std::mutex> gm(m->mu);
+    HeadLocks locks(m);
+    if (!flush_all_locked(m, fn)) return -1;
+    for (int h = 0; h < H; ++h) {
+      Ctx *c = m->heads[h];
+      if (!read_ring(c, kc, vc, ks, vs, fn)) return -1;
+      const int n = c->st.size;
+      n_tokens = std::max(n_tokens, n);
+      o.put<int32_t>(l);
+      o.put<int32_t>(h);
+      o.put<int32_t>(n);
+      o.put<int32_t>(slot_bytes);
+      o.put<uint64_t>((uint64_t)n * 2 * slot_bytes);
+      for (int i = 0; i < n; ++i) {
+        o.put_bytes(kc.data() + (size_t)i * c->k_pb, c->k_pb);
+        o.put_bytes(pad.data(), slot_bytes - c->k_pb);
+      }
+      for (int i = 0; i < n; ++i) {
+        o.put_bytes(vc.data() + (size_t)i * c->v_pb, c->v_pb);
+        o.put_bytes(pad.data(), slot_bytes - c->v_pb);
+      }
+      o.put<int32_t>(2 * n);
+      o.put_bytes(ks.data(), (size_t)n * 4);
+      o.put_bytes(vs.data(), (size_t)n * 4);
+      o.put<int32_t>(2 * n);
+      o.buf.insert(o.buf.end(), (size_t)n, snap_tag(c->k_bits));
+      o.buf.insert(o.buf.end(), (size_t)n, snap_tag(c->v_bits));
+    }
+  }
+  std::memcpy(o.buf.data() + ntok_at, &n_tokens, 4);
+  FILE *f = std::fopen(path, "wb");
+  if (!f) {
+    set_errorf(fn, "cannot open the file for writing");
+    return -1;
+  }
+  const bool ok = std::fwrite(o.buf.data(), 1, o.buf.size(), f) == o.buf.size();
+  if (std::fclose(f) != 0 || !ok) {
+    set_errorf(fn, "write error");
+    return -1;
+  }
+  clear_error();
+  return 0;
+}
+
+int adaptq_snapshot_load(const adaptq_mha_t *layers, int n_layers, const char *path) {
+  const char *fn = "adaptq_snapshot_load";
+  if (!require_pointer(path, fn, "path") || !snap_layers_ok(layers, n_layers, fn)) return -1;
+  std::vector<uint8_t> file;
+  {
+    FILE *f = std::fopen(path, "rb");
+    if (!f) {
+      set_errorf(fn, "cannot open the file");
+      return -1;
+    }
+    uint8_t chunk[1 << 16];
+    size_t got;
+    while ((got = std::fread(chunk, 1, sizeof(chunk), f)) > 0) file.insert(file.end(), chunk, chunk + got);
+    std::fclose(f);
+  }
+  if (file.size() < 40) {
+    set_errorf(fn, "file too small");
+    return -1;
+  }
+  const Mha *m0 = static_cast<const Mha *>(layers[0]);
+  const Ctx *c0 = m0->heads[0];
+  const int H = m0->n_heads;
+  SnapIn in{file.data(), file.size()};
+  const uint32_t magic = in.get<uint32_t>(), version = in.get<uint32_t>();
+  const int32_t nl = in.get<int32_t>(), nh = in.get<int32_t>(), dim = in.get<int32_t>();
+  const int32_t bits = in.get<int32_t>(), ntok = in.get<int32_t>(), nht = in.get<int32_t>();
+  const uint64_t flags = in.get<uint64_t>();
+  (void)bits;
+  if (magic != 0x41515353u) {
+    set_errorf(fn, "invalid magic (not an AQSS file)");
+    return -1;
+  }
+  if (version > 2u) {
+    set_errorf(fn, "snapshot version newer than 2");
+    return -1;
+  }
+  if (nl != n_layers || nh != H || dim != c0->dim || nht != nl * nh || ntok < 0) {
+    set_errorf(fn, "snapshot shape does not match the MHAs (layers, heads, dim)");
+    return -1;
+  }
+  struct Block {
+    int layer, head, n, slot_bytes;
+    const uint8_t *data;
+    const uint8_t *scales;  // 2n f32, possibly unaligned in the file buffer
+    const uint8_t *tags;
+  };
+  std::vector<Block> blocks((size_t)nht);
+  std::vector<char> seen((size_t)nht, 0);
+  const int slot_bytes = std::max(c0->k_pb, c0->v_pb);
+  for (auto &b : blocks) {
+    b.layer = in.get<int32_t>();
+    b.head = in.get<int32_t>();
+    b.n = in.get<int32_t>();
+    b.slot_bytes = in.get<int32_t>();
+    const uint64_t data_bytes = in.get<uint64_t>();
+    if (!in.ok || b.layer < 0 || b.layer >= nl || b.head < 0 || b.head >= nh) {
+      set_errorf(fn, in.ok ? "invalid head coordinates" : "truncated snapshot");
+      return -1;
+    }
+    const Ctx *c = static_cast<const Mha *>(layers[b.layer])->heads[b.head];
+    if (b.n < 0 || b.n > c->cap || b.slot_bytes != slot_bytes ||
+        data_bytes != (uint64_t)b.n * 2 * (uint64_t)slot_bytes) {
+      set_errorf(fn, "head storage does not fit the MHA (cache size, slot bytes)");
+      return -1;
+    }
+    b.data = in.take(data_bytes);
+    const int32_t n_scales = in.get<int32_t>();
+    b.scales = in.take(n_scales == 2 * b.n ? (uint64_t)n_scales * 4 : ~0ull);
+    const int32_t n_tags = in.get<int32_t>();
+    b.tags = in.take(n_tags == 2 * b.n ? (uint64_t)n_tags : ~0ull);
+    if (!in.ok) {
+      set_errorf(fn, "truncated or inconsistent head block");
+      return -1;
+    }
+    for (int i = 0; i < b.n; ++i)
+      if (b.tags[i] != snap_tag(c->k_bits) || b.tags[b.n + i] != snap_tag(c->v_bits)) {
+        set_errorf(fn, "format tags do not match the MHA's bit widths");
+        return -1;
+      }
+    char &s = seen[(size_t)b.layer * nh + b.head];
+    if (s) {
+      set_errorf(fn, "duplicate head block");
+      return -1;
+    }
+    s = 1;
+  }
+  if (flags & 2u)
+    for (int i = 0; i < nht; ++i) {
+      const int32_t len = in.get<int32_t>();
+      in.take(len >= 0 ? (uint64_t)len : ~0ull);
+    }
+  if (!in.ok) {
+    set_errorf(fn, "truncated strategy state");
+    return -1;
+  }
+  // The token log (flags & 1) is not needed to restore packed rings.
+  for (const auto &b : blocks) {
+    Mha *m = static_cast<Mha *>(layers[b.layer]);
+    std::lock_guard<std::mutex> gm(m->mu);
+    Ctx *c = m->heads[b.head];
+    std::lock_guard<std::mutex> gc(c->mu);
+    const uint8_t *kc = b.data, *vc = b.data + (size_t)b.n * slot_bytes;
+    std::vector<float> ks((size_t)b.n), vs((size_t)b.n);
+    std::memcpy(ks.data(), b.scales, (size_t)b.n * 4);
+    std::memcpy(vs.data(), b.scales + (size_t)b.n * 4, (size_t)b.n * 4);
+    if (!write_ring(c, b.n, kc, vc, slot_bytes, ks.data(), vs.data(), fn)) return -1;
+  }
+  clear_error();
+  return 0;
+}
+
+}  // extern "C"

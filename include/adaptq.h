@@ -210,6 +210,28 @@ int adaptq_ggml_attn_f32_device(adaptq_mha_t mha, const float *d_q,
                                 size_t q_nb1, size_t q_nb2, float *d_dst,
                                 size_t dst_nb1, size_t dst_nb2, void *stream);
 
+/* ---- Packed-ring snapshots (AQSS v2) ----
+ * Replace reference replay/session_snapshot.{h,cpp} (SessionSnapshot
+ * capture/save/load, session_snapshot.h:16-40 for the format) for the rings
+ * of this library: layers[l] is the MHA of layer l; all share n_heads, dim
+ * and bit widths.  Each head block holds its cache_size cached tokens in
+ * logical order (oldest first): K rows then V rows in the reference's packed
+ * byte layout, each zero-padded to slot_bytes = max(K row, V row) bytes, the
+ * scales (K then V) and one format tag per slot (0x02/0x03/0x04 for 2/3/4-bit
+ * codes, 0xFF for fp32 rows).  `bits` in the header is the K bit width and
+ * n_tokens the largest cache_size; no token log and no strategy state are
+ * written (flags 0), and both are skipped on load.
+ *
+ * load: validates the whole file against the MHAs first (magic, version <= 2,
+ * layer/head counts, dim, slot bytes, cache sizes <= capacity, format tags),
+ * then replaces every head's ring: tokens in slots 0..n-1, staged appends
+ * discarded, hybrid mirror empty (a loaded ring decodes from its packed
+ * codes).  Device-form appends must be synchronised by the caller first.
+ * Both return 0, or -1 with the last error set (nothing changed on a failed
+ * load). */
+int adaptq_snapshot_save(const adaptq_mha_t *layers, int n_layers, const char *path);
+int adaptq_snapshot_load(const adaptq_mha_t *layers, int n_layers, const char *path);
+
 /* ---- Batched device-pointer path ----
  * Extension, no counterpart in the reference.  For callers whose data is
  * already in device memory (torch-ROCm tensors, serving loops) and for the

@@ -307,3 +307,68 @@ class RefHead:
         self.L.refx_head_read_slots(self.h, first, count, u8ptr(kc), u8ptr(vc), fptr(ks),
                                     fptr(vs))
         return kc, vc, ks, vs
+
+
+SNAP_REF_SO = os.path.join(HERE, "_ref", "libsnapshot_ref.so")
+
+
+class SnapshotRef:
+    """The reference's SessionSnapshot::load/save (replay/session_snapshot.cpp),
+    compiled in place into oracle/_ref/libsnapshot_ref.so and opened with lazy
+    binding (its capture() needs the unbuilt V2 runtime and is never called)."""
+
+    available = os.path.exists(SNAP_REF_SO)
+
+    def __init__(self, path: str = SNAP_REF_SO):
+        L = self.lib = C.CDLL(path, mode=os.RTLD_LAZY)
+        L.snapref_load.argtypes = [C.c_char_p, C.c_char_p, C.c_int]
+        L.snapref_load.restype = C.c_void_p
+        L.snapref_free.argtypes = [C.c_void_p]
+        L.snapref_info.argtypes = [C.c_void_p, _ip]
+        L.snapref_head.argtypes = [C.c_void_p, C.c_int, _ip, C.POINTER(C.POINTER(C.c_uint8)),
+                                   C.POINTER(C.POINTER(C.c_float)),
+                                   C.POINTER(C.POINTER(C.c_uint8))]
+        L.snapref_head.restype = C.c_int
+        L.snapref_save.argtypes = [C.c_void_p, C.c_char_p, C.c_char_p, C.c_int]
+        L.snapref_save.restype = C.c_int
+
+    def load(self, path: str) -> dict:
+        """The file as the reference reads it; raises ValueError with the
+        reference's exception text when it refuses the file."""
+        err = C.create_string_buffer(512)
+        h = self.lib.snapref_load(path.encode(), err, 512)
+        if not h:
+            raise ValueError(err.value.decode())
+        try:
+            info = np.zeros(7, np.int32)
+            self.lib.snapref_info(h, info.ctypes.data_as(_ip))
+            keys = ["n_layers", "n_heads", "dim", "bits", "n_tokens", "n_blocks", "flags"]
+            out = {k: int(v) for k, v in zip(keys, info)}
+            heads = []
+            for i in range(out["n_blocks"]):
+                ints = np.zeros(4, np.int32)
+                d, s, t = C.POINTER(C.c_uint8)(), C.POINTER(C.c_float)(), C.POINTER(C.c_uint8)()
+                assert self.lib.snapref_head(h, i, ints.ctypes.data_as(_ip), C.byref(d),
+                                             C.byref(s), C.byref(t)) == 0
+                layer, head, n, sb = (int(x) for x in ints)
+                heads.append(dict(
+                    layer=layer, head=head, cache_size=n, slot_bytes=sb,
+                    data=np.ctypeslib.as_array(d, (2 * n * sb,)).copy() if n * sb else np.zeros(0, np.uint8),
+                    scales=np.ctypeslib.as_array(s, (2 * n,)).copy() if n else np.zeros(0, np.float32),
+                    tags=np.ctypeslib.as_array(t, (2 * n,)).copy() if n else np.zeros(0, np.uint8)))
+            out["heads"] = heads
+            return out
+        finally:
+            self.lib.snapref_free(h)
+
+    def resave(self, src: str, dst: str) -> None:
+        """load(src) then save(dst), both by the reference."""
+        err = C.create_string_buffer(512)
+        h = self.lib.snapref_load(src.encode(), err, 512)
+        if not h:
+            raise ValueError(err.value.decode())
+        try:
+            if self.lib.snapref_save(h, dst.encode(), err, 512) != 0:
+                raise ValueError(err.value.decode())
+        finally:
+            self.lib.snapref_free(h)
