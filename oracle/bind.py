@@ -372,3 +372,40 @@ class SnapshotRef:
                 raise ValueError(err.value.decode())
         finally:
             self.lib.snapref_free(h)
+
+
+KERNEL_REF_SO = os.path.join(HERE, "_ref", "libkernel_ref.so")
+
+
+class KernelRef:
+    """The reference's scalar IKernelBackend (kernels/scalar/kdot_scalar.cpp),
+    compiled in place into oracle/_ref/libkernel_ref.so."""
+
+    available = os.path.exists(KERNEL_REF_SO)
+
+    def __init__(self, path: str = KERNEL_REF_SO):
+        L = self.lib = C.CDLL(path)
+        L.kref_kdot.argtypes = [_f, _u8, _f, C.c_int, C.c_int, C.c_int, _f]
+        L.kref_vaccum.argtypes = [_u8, _f, _f, C.c_int, C.c_int, C.c_int, _f]
+        L.kref_fwht.argtypes = [_f, _i8, C.c_int, C.c_int]
+
+    def kdot(self, q, rows, scales, bits):
+        q = np.ascontiguousarray(q, np.float32)
+        rows = np.ascontiguousarray(rows, np.uint8)
+        scales = np.ascontiguousarray(scales, np.float32)
+        out = np.zeros(len(scales), np.float32)
+        self.lib.kref_kdot(fptr(q), u8ptr(rows), fptr(scales), len(scales), q.size, bits, fptr(out))
+        return out
+
+    def vaccum(self, rows, scales, w, padded, bits):
+        rows = np.ascontiguousarray(rows, np.uint8)
+        scales = np.ascontiguousarray(scales, np.float32)
+        w = np.ascontiguousarray(w, np.float32)
+        acc = np.zeros(padded, np.float32)
+        self.lib.kref_vaccum(u8ptr(rows), fptr(scales), fptr(w), len(scales), padded, bits, fptr(acc))
+        return acc
+
+    def fwht(self, x, D, forward):
+        y = np.ascontiguousarray(x, np.float32).copy()
+        self.lib.kref_fwht(fptr(y), i8ptr(np.ascontiguousarray(D, np.int8)), y.size, int(forward))
+        return y
