@@ -14,42 +14,16 @@
 //   signs + butterflies, * RN(1/RN(sqrtp)) fwht.cpp:33-66
 //   * sqrtf(p)                            quantizer.cpp:73-75
 //   sigma, +-3 sigma clamp                quantizer.cpp:81-89
-//   binary-search index, NaN -> 1/3/7     codebook.cpp:119-144
+//   binary-search index, NaN -> 1/3/7     codebook.cpp:119-144 (quant.hpp;
+//                                         4-bit codes by one table lookup)
 //   MSB-first pack                        quantizer.cpp:156-209
 //   ring insert, mirror                   ring_buffer.cpp:105-119, attention.cpp:338-366
 #include "launch.hpp"
+#include "quant.hpp"
 
 namespace aq {
 
 namespace {
-
-// Index of v in the B-bit codebook: the count of thresholds t with v >= t,
-// found by the reference's branchless binary search; thresholds are selected
-// with compares already made, so no table is indexed per lane.
-template <int B>
-__device__ __forceinline__ uint32_t quantize(float v) {
-  if (v != v) return B == 2 ? 1u : B == 3 ? 3u : 7u;
-  if constexpr (B == 2) {
-    bool c1 = v >= thr<2>(1);
-    bool c0 = v >= (c1 ? thr<2>(2) : thr<2>(0));
-    return (c1 ? 2u : 0u) | (c0 ? 1u : 0u);
-  } else if constexpr (B == 3) {
-    bool c2 = v >= thr<3>(3);
-    bool c1 = v >= (c2 ? thr<3>(5) : thr<3>(1));
-    float t0 = c2 ? (c1 ? thr<3>(6) : thr<3>(4)) : (c1 ? thr<3>(2) : thr<3>(0));
-    bool c0 = v >= t0;
-    return (c2 ? 4u : 0u) | (c1 ? 2u : 0u) | (c0 ? 1u : 0u);
-  } else {
-    bool c3 = v >= thr<4>(7);
-    bool c2 = v >= (c3 ? thr<4>(11) : thr<4>(3));
-    float t1 = c3 ? (c2 ? thr<4>(13) : thr<4>(9)) : (c2 ? thr<4>(5) : thr<4>(1));
-    bool c1 = v >= t1;
-    float t0 = c3 ? (c2 ? (c1 ? thr<4>(14) : thr<4>(12)) : (c1 ? thr<4>(10) : thr<4>(8)))
-                  : (c2 ? (c1 ? thr<4>(6) : thr<4>(4)) : (c1 ? thr<4>(2) : thr<4>(0)));
-    bool c0 = v >= t0;
-    return (c3 ? 8u : 0u) | (c2 ? 4u : 0u) | (c1 ? 2u : 0u) | (c0 ? 1u : 0u);
-  }
-}
 
 // Store nbytes (a compile-time count) from w[] to dst with the widest stores
 // the row alignment allows.
@@ -99,6 +73,12 @@ __global__ __launch_bounds__(128) void append_kernel(HeadDesc *const *descs, int
                                                      int side, const float *__restrict__ src,
                                                      int n_tok, int dim, float inv_sqrt_p,
                                                      float sqrt_p) {
+  // 4-bit codes: the bucket table of quantize4_tab, built before any lane leaves
+  __shared__ Q4Entry s_q4[B == 4 ? kQ4Entries : 1];
+  if constexpr (B == 4) {
+    for (int i = threadIdx.x; i < kQ4Entries; i += blockDim.x) s_q4[i] = q4_entry(i);
+    __syncthreads();
+  }
   const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (g >= (long long)n_ctx * n_tok) return;
   const int c = (int)(g / n_tok);
@@ -196,7 +176,7 @@ __global__ __launch_bounds__(128) void append_kernel(HeadDesc *const *descs, int
       float v = buf[i];
       if (v > clip) v = clip;
       if (v < -clip) v = -clip;
-      const uint32_t q = quantize<B>(v);
+      const uint32_t q = B == 4 ? quantize4_tab(v, s_q4) : quantize<B>(v);
       // Bit position of code i inside the little-endian word stream.
       int byte, shift;
       if constexpr (B == 4) {
@@ -247,6 +227,11 @@ __global__ __launch_bounds__(128) void append_kernel_wide(HeadDesc *const *descs
                                                           int side, const float *__restrict__ src,
                                                           int n_tok, int dim, int P,
                                                           float inv_sqrt_p, float sqrt_p) {
+  __shared__ Q4Entry s_q4[B == 4 ? kQ4Entries : 1];
+  if constexpr (B == 4) {
+    for (int i = threadIdx.x; i < kQ4Entries; i += blockDim.x) s_q4[i] = q4_entry(i);
+    __syncthreads();
+  }
   const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (g >= (long long)n_ctx * n_tok) return;
   const int c = (int)(g / n_tok);
@@ -308,7 +293,7 @@ __global__ __launch_bounds__(128) void append_kernel_wide(HeadDesc *const *descs
       float v = buf[i];
       if (v > clip) v = clip;
       if (v < -clip) v = -clip;
-      const uint32_t q = quantize<B>(v);
+      const uint32_t q = B == 4 ? quantize4_tab(v, s_q4) : quantize<B>(v);
       if constexpr (B == 4) {
         row[i / 2] |= (uint8_t)(q << ((i % 2) ? 0 : 4));
       } else if constexpr (B == 2) {

@@ -1,0 +1,38 @@
+// Every float bit pattern: quantize4_tab (adaptq_amd/csrc/quant.hpp, the
+// append kernel's 4-bit quantiser) against quantize<4> (the reference's binary
+// search restated) and, on a stride, against the oracle's quantize_fast.
+// Prints the mismatch count; exits 0 when it is 0.
+#include <atomic>
+#include <cstdio>
+#include <cstring>
+#include <thread>
+#include <vector>
+
+#include "../../adaptq_amd/csrc/quant.hpp"
+
+extern "C" int orc_quantize_fast(float v, int bits);
+
+int main() {
+  aq::Q4Entry tab[aq::kQ4Entries];
+  for (int i = 0; i < aq::kQ4Entries; ++i) tab[i] = aq::q4_entry(i);
+  std::atomic<unsigned long long> bad{0};
+  const int T = 8;
+  std::vector<std::thread> pool;
+  for (int w = 0; w < T; ++w)
+    pool.emplace_back([&, w] {
+      const uint64_t lo = ((uint64_t)w << 32) / T, hi = ((uint64_t)(w + 1) << 32) / T;
+      for (uint64_t x = lo; x < hi; ++x) {
+        const uint32_t u = (uint32_t)x;
+        float v;
+        std::memcpy(&v, &u, 4);
+        const uint32_t a = aq::quantize4_tab(v, tab), b = aq::quantize<4>(v);
+        bool wrong = a != b;
+        if ((u & 0xFFF) == 0x5A5) wrong = wrong || (int)b != orc_quantize_fast(v, 4);
+        if (wrong && bad.fetch_add(1) < 10)
+          std::printf("mismatch bits=%08x v=%g tab=%u search=%u\n", u, v, a, b);
+      }
+    });
+  for (auto &t : pool) t.join();
+  std::printf("checked 4294967296 mismatches %llu\n", bad.load());
+  return bad.load() == 0 ? 0 : 1;
+}
