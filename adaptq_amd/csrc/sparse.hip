@@ -19,8 +19,10 @@
 // reference's std::sort leaves their order unspecified.
 //
 // Kernels: one grid over (token blocks, items) computes the logits; one block
-// per item does softmax, a bitonic sort (in LDS up to 8192 tokens, else in the
-// workspace), the cut, the V gather and the inverse FWHT.
+// per item does softmax, a bitonic sort (in LDS up to 16384 tokens, else in
+// the workspace) and the cut, and turns the selection into per-token weights;
+// a grid over (token chunks, items) sums the weighted V rows; one block per
+// item adds the chunks and applies the inverse FWHT.
 #include "launch.hpp"
 
 namespace aq {
@@ -28,7 +30,9 @@ namespace aq {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kLdsSort = 8192;
+constexpr int kSelThreads = 1024;
+constexpr int kLdsSort = 16384;  // sort keys held in LDS up to this many tokens (128 KB)
+constexpr int kStage = 4096;    // floats per LDS staging chunk
 
 template <int B>
 __device__ __forceinline__ int code_at(const uint8_t *row, int i) {
@@ -72,15 +76,17 @@ __device__ __forceinline__ bool sign_plus(const uint32_t *signs, int i) {
 __device__ void rotate_query_exact(float *s_q, const float *q, int dim, int P,
                                    const uint32_t *signs, float inv_sqrt_p, float sqrt_p) {
   __shared__ float s_qn;
+  for (int i = threadIdx.x; i < P; i += blockDim.x) s_q[i] = i < dim ? q[i] : 0.0f;
+  __syncthreads();
   if (threadIdx.x == 0) {
     float s = 0.0f;
-    for (int i = 0; i < dim; ++i) s = __fadd_rn(s, __fmul_rn(q[i], q[i]));
+    for (int i = 0; i < dim; ++i) s = __fadd_rn(s, __fmul_rn(s_q[i], s_q[i]));
     s_qn = sqrtf(__fadd_rn(s, 1e-12f));
   }
   __syncthreads();
   const float qn = s_qn;
   const float inv = 1.0f / qn;
-  for (int i = threadIdx.x; i < P; i += blockDim.x) s_q[i] = __fmul_rn(i < dim ? q[i] : 0.0f, inv);
+  for (int i = threadIdx.x; i < P; i += blockDim.x) s_q[i] = __fmul_rn(s_q[i], inv);
   __syncthreads();
   for (int k = threadIdx.x; k < P / 2; k += blockDim.x) {
     const int i = 2 * k;
@@ -104,7 +110,46 @@ __device__ void rotate_query_exact(float *s_q, const float *q, int dim, int P,
   __syncthreads();
 }
 
-template <int KB>
+// dot(s_q, CB[codes of row]) with the reference's 8 FMA lanes (lane L takes
+// codes L, L+8, ...) summed pairwise (attention.cpp:83-136).
+// PT = 0: any padded size, codes read byte by byte.  PT = 64/128 with 2/4-bit
+// codes: the row is read as words; reference word w sits at stored word
+// w ^ (x >> 2) with its bytes permuted by b ^ (x & 3) (kperm_mask), and one
+// v_perm per word restores the reference byte order.
+template <int PT, int KB>
+__device__ __forceinline__ float kdot_row(const uint8_t *row, int x, const float *s_q, int P) {
+  float s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if constexpr (PT != 0 && (KB == 2 || KB == 4)) {
+    constexpr int W = PT * KB / 32;
+    const uint32_t *r32 = reinterpret_cast<const uint32_t *>(row);
+    const uint32_t xw = (uint32_t)x >> 2;
+    const uint32_t sel = 0x03020100u ^ (((uint32_t)x & 3u) * 0x01010101u);
+    uint32_t w[W];
+#pragma unroll
+    for (int i = 0; i < W; ++i) w[i] = __builtin_amdgcn_perm(0u, r32[i ^ xw], sel);
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+      int c;
+      if constexpr (KB == 4) {
+        const int byte = j >> 1;
+        c = (int)((w[byte >> 2] >> (8 * (byte & 3) + ((j & 1) ? 0 : 4))) & 15u);
+      } else {
+        const int byte = j >> 2;
+        c = (int)((w[byte >> 2] >> (8 * (byte & 3) + 6 - 2 * (j & 3))) & 3u);
+      }
+      s[j & 7] = fmaf(cbv<KB>(c), s_q[j], s[j & 7]);
+    }
+  } else {
+    for (int j = 0; j < P; j += 8)
+#pragma unroll
+      for (int L = 0; L < 8; ++L)
+        if (j + L < P) s[L] = fmaf(cbv<KB>(kcode_at<KB>(row, j + L, x)), s_q[j + L], s[L]);
+  }
+  const float t0 = s[0] + s[4], t1 = s[1] + s[5], t2 = s[2] + s[6], t3 = s[3] + s[7];
+  return (t0 + t1) + (t2 + t3);
+}
+
+template <int PT, int KB>
 __global__ __launch_bounds__(kThreads) void sparse_logits_kernel(HeadDesc *const *item_desc,
                                                                  const float *__restrict__ queries,
                                                                  int max_n, float inv_sqrt_p,
@@ -121,43 +166,41 @@ __global__ __launch_bounds__(kThreads) void sparse_logits_kernel(HeadDesc *const
   const int slot = (int)(((long long)d->st.head - n + cap + i) % cap);
   const uint8_t *row = d->k_codes + (size_t)slot * d->k_pb;
   const int x = slot & kperm_mask(P, KB);
-  // 8 FMA lanes over codes L, L+8, ...; lanes summed pairwise.
-  float s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int j = 0; j < P; j += 8)
-#pragma unroll
-    for (int L = 0; L < 8; ++L)
-      if (j + L < P) s[L] = fmaf(cbv<KB>(kcode_at<KB>(row, j + L, x)), s_q[j + L], s[L]);
-  const float t0 = s[0] + s[4], t1 = s[1] + s[5], t2 = s[2] + s[6], t3 = s[3] + s[7];
-  const float dot = (t0 + t1) + (t2 + t3);
+  const float dot = kdot_row<PT, KB>(row, x, s_q, P);
   const float attn_s = 1.0f / (sqrtf((float)dim) * (float)P);
   ws[(size_t)item * ws_stride + i] = __fmul_rn(__fmul_rn(dot, attn_s), d->k_scale[slot]);
 }
 
-struct Key {
-  float p;
-  int i;
-};
-
-// a precedes b: larger probability first, then older token; NaN last.
-__device__ __forceinline__ bool before(Key a, Key b) {
-  const bool an = a.p != a.p, bn = b.p != b.p;
-  if (an || bn) return !an && bn;
-  if (a.p != b.p) return a.p > b.p;
-  return a.i < b.i;
+// Sort key of token i with probability p: unsigned order of the key is the
+// selection order -- larger p first, equal p older first, NaN after every
+// number, padding (i >= n) after everything.  hi = 0x7F800000 - |p| bits for
+// numbers (p >= 0 here), 0xFFFFFFFF for NaN; lo = i.
+__device__ __forceinline__ uint64_t make_key(float p, int i) {
+  const uint32_t b = __float_as_uint(p) & 0x7FFFFFFFu;
+  const uint32_t hi = b > 0x7F800000u ? 0xFFFFFFFFu : 0x7F800000u - b;
+  return ((uint64_t)hi << 32) | (uint32_t)i;
 }
+constexpr uint64_t kPadKey = ~(uint64_t)0;
 
-__device__ void bitonic(Key *m, int N) {
+__device__ __forceinline__ float key_p(uint64_t k) {
+  const uint32_t hi = (uint32_t)(k >> 32);
+  return __uint_as_float(hi == 0xFFFFFFFFu ? 0x7FC00000u : 0x7F800000u - hi);
+}
+__device__ __forceinline__ int key_i(uint64_t k) { return (int)(uint32_t)k; }
+
+// Bitonic sort of N (a power of two) keys ascending; each thread takes whole
+// compare-exchange pairs, so no lane idles on the upper halves.
+__device__ void bitonic(uint64_t *m, int N) {
   for (int k = 2; k <= N; k <<= 1) {
     for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = threadIdx.x; i < N; i += blockDim.x) {
-        const int ixj = i ^ j;
-        if (ixj > i) {
-          const Key a = m[i], b = m[ixj];
-          const bool up = (i & k) == 0;
-          if (up ? before(b, a) : before(a, b)) {
-            m[i] = b;
-            m[ixj] = a;
-          }
+      const int lj = __builtin_ctz((unsigned)j);
+      for (int pr = threadIdx.x; pr < N / 2; pr += blockDim.x) {
+        const int i = ((pr >> lj) << (lj + 1)) | (pr & (j - 1));
+        const uint64_t a = m[i], b = m[i + j];
+        const bool up = (i & k) == 0;
+        if (up ? b < a : a < b) {
+          m[i] = b;
+          m[i + j] = a;
         }
       }
       __syncthreads();
@@ -165,97 +208,311 @@ __device__ void bitonic(Key *m, int N) {
   }
 }
 
-template <int VB>
-__global__ __launch_bounds__(kThreads) void sparse_select_kernel(HeadDesc *const *item_desc,
-                                                                 float v_mass, float *ws,
-                                                                 size_t ws_stride, int sort_cap,
-                                                                 float *__restrict__ outs) {
-  __shared__ Key s_keys[kLdsSort];
+// acc + s[0] + s[1] + ... + s[m-1], left to right, one lane.  s is 16-byte
+// aligned LDS; the reads of the next 32 values go out before the adds of the
+// current 32.
+__device__ float serial_sum(const float *s, int m, float acc) {
+  const float4 *s4 = reinterpret_cast<const float4 *>(s);
+  const int nb = m / 32;
+  float4 cur[8];
+  if (nb > 0) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) cur[k] = s4[k];
+  }
+  for (int b = 0; b < nb; ++b) {
+    float4 nxt[8];
+    if (b + 1 < nb) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) nxt[k] = s4[8 * (b + 1) + k];
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      acc = __fadd_rn(acc, cur[k].x);
+      acc = __fadd_rn(acc, cur[k].y);
+      acc = __fadd_rn(acc, cur[k].z);
+      acc = __fadd_rn(acc, cur[k].w);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) cur[k] = nxt[k];
+  }
+  for (int i = 32 * nb; i < m; ++i) acc = __fadd_rn(acc, s[i]);
+  return acc;
+}
+
+// The reference's mass loop over quad sums q[0..m): while mass < v_mass, add
+// the next one.  mass never decreases (the sums are >= 0) and stays NaN once
+// NaN, so a predicated add over a batch takes exactly the quads the loop
+// takes.  Returns how many were taken; *mass is updated.
+__device__ int mass_scan(const float *q, int m, float v_mass, float *mass) {
+  const float4 *q4 = reinterpret_cast<const float4 *>(q);
+  float ms = *mass;
+  int taken = 0;
+  for (int b = 0; b < m / 32 && ms < v_mass; ++b) {
+    float4 v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = q4[8 * b + k];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float e[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const bool go = ms < v_mass;
+        ms = go ? __fadd_rn(ms, e[c]) : ms;
+        taken += go ? 1 : 0;
+      }
+    }
+  }
+  for (int i = (m / 32) * 32; i < m && ms < v_mass; ++i) {
+    ms = __fadd_rn(ms, q[i]);
+    ++taken;
+  }
+  *mass = ms;
+  return taken;
+}
+
+// Logical token t of an n-token ring lives in slot s0 + t (mod cap), with
+// s0 = (head - n) mod cap (attention.cpp:562-563).
+__device__ __forceinline__ int ring_slot(int s0, int t, int cap) {
+  const int s = s0 + t;
+  return s >= cap ? s - cap : s;
+}
+
+// One block of kSelThreads per item.  Steps, each a parallel pass except the
+// two left-to-right sums the reference's results depend on:
+//   1. max of the logits (block reduction, the reference's NaN-skipping compare)
+//   2. e_t = expf(l_t - max) in chunks of kStage through LDS; thread 0 adds
+//      each chunk left to right (the softmax sum, attention.cpp:422-426)
+//   3. p_t = e_t * (1/sum); bitonic sort by p descending (LDS up to kLdsSort
+//      tokens, else the workspace)
+//   4. quad sums ((p0+p1)+p2)+p3 of the sorted order in parallel, staged
+//      through LDS; thread 0 runs the mass loop over them, then the single
+//      tokens (attention.cpp:454-472)
+//   5. the selection becomes a weight per token in natural order, written
+//      over the logits: (p_t * vscale_t) * isp if selected, else 0
+// sparse_vsum_kernel then sums the weighted V rows over many blocks and
+// sparse_finish_kernel applies the inverse FWHT.  The V sum runs in natural
+// token order instead of the reference's sorted order, which changes only its
+// rounding; the selected set is the reference's.
+__global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *const *item_desc,
+                                                                    float v_mass, float *ws,
+                                                                    size_t ws_stride,
+                                                                    int sort_cap) {
+  __shared__ uint64_t s_keys[kLdsSort];
+  __shared__ __align__(16) float s_stage[kStage];
+  __shared__ float s_red[kSelThreads];
   __shared__ float s_acc[kMaxPadded];
-  __shared__ float s_red[kThreads];
-  __shared__ float s_inv;
+  __shared__ float s_bcast[2];
   __shared__ int s_cut;
+  __shared__ uint64_t s_last;
+  const int item = blockIdx.x;
+  const int tid = threadIdx.x;
+  const HeadDesc *d = item_desc[item];
+  const int n = d->st.size, cap = d->cap, P = d->padded;
+  if (n == 0) return;
+  float *lg = ws + (size_t)item * ws_stride;
+  int N = 1;
+  while (N < n) N <<= 1;
+  uint64_t *keys = N <= kLdsSort ? s_keys : reinterpret_cast<uint64_t *>(lg + sort_cap);
+  const int s0 = (int)(((long long)d->st.head - n + cap) % cap);
+
+  // 1. max with the reference's starting value and NaN-skipping compare
+  float mx = -1e30f;
+  for (int i = tid; i < n; i += blockDim.x)
+    if (lg[i] > mx) mx = lg[i];
+  s_red[tid] = mx;
+  __syncthreads();
+  for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+    if (tid < w && s_red[tid + w] > s_red[tid]) s_red[tid] = s_red[tid + w];
+    __syncthreads();
+  }
+  mx = s_red[0];
+  __syncthreads();
+
+  // 2. exponentials and their left-to-right sum
+  float sv = 0.0f;
+  for (int base = 0; base < n; base += kStage) {
+    const int m = n - base < kStage ? n - base : kStage;
+    for (int i = tid; i < m; i += blockDim.x) {
+      const float e = expf(lg[base + i] - mx);
+      lg[base + i] = e;
+      s_stage[i] = e;
+    }
+    __syncthreads();
+    if (tid == 0) sv = serial_sum(s_stage, m, sv);
+    __syncthreads();
+  }
+  if (tid == 0) s_bcast[0] = 1.0f / sv;
+  __syncthreads();
+  const float inv = s_bcast[0];
+
+  // 3. probabilities, sorted descending (ties: older first)
+  for (int i = tid; i < N; i += blockDim.x) keys[i] = i < n ? make_key(__fmul_rn(lg[i], inv), i) : kPadKey;
+  __syncthreads();
+  bitonic(keys, N);
+
+  // 4. the cut: whole quads while mass < v_mass, then single tokens
+  const int n_quads = n / 4;  // quads with ii + 3 < n
+  float mass = 0.0f;
+  int ii = 0;
+  bool open = true;  // thread 0: the quad loop has not stopped
+  for (int base = 0; base < n_quads; base += kStage) {
+    const int m = n_quads - base < kStage ? n_quads - base : kStage;
+    for (int k = tid; k < m; k += blockDim.x) {
+      const uint64_t *q = keys + 4 * (base + k);
+      s_stage[k] = __fadd_rn(__fadd_rn(__fadd_rn(key_p(q[0]), key_p(q[1])), key_p(q[2])), key_p(q[3]));
+    }
+    __syncthreads();
+    if (tid == 0 && open) {
+      const int k = mass_scan(s_stage, m, v_mass, &mass);
+      ii = 4 * (base + k);
+      open = k == m;
+      s_bcast[1] = open ? 1.0f : 0.0f;
+    }
+    __syncthreads();
+    if (s_bcast[1] == 0.0f) break;
+    __syncthreads();
+  }
+  if (tid == 0) {
+    for (; ii < n && mass < v_mass; ++ii) mass = __fadd_rn(mass, key_p(keys[ii]));
+    s_cut = ii;
+    s_last = ii > 0 ? keys[ii - 1] : 0;
+  }
+  __syncthreads();
+  const int cut = s_cut;
+  const uint64_t last = s_last;
+
+  // 5. per-token weights in natural order: the selection is the cut first
+  // keys of the sorted order, i.e. every key up to the last one taken (keys
+  // are distinct); p_t is recomputed exactly as the key was made
+  const float isp = 1.0f / sqrtf((float)P);
+  for (int t = tid; t < n; t += blockDim.x) {
+    const float p = __fmul_rn(lg[t], inv);
+    lg[t] = cut > 0 && make_key(p, t) <= last
+                ? __fmul_rn(__fmul_rn(p, d->v_scale[ring_slot(s0, t, cap)]), isp)
+                : 0.0f;
+  }
+
+  // (the weights in lg are read by sparse_vsum_kernel)
+}
+
+// Codes per byte-aligned unit of a packed row and the unit's size in bytes:
+// 2-bit: 1 byte = 4 codes, 4-bit: 1 byte = 2 codes, 3-bit: 3 bytes = 8 codes.
+template <int VB>
+struct VUnit {
+  static constexpr int codes = VB == 3 ? 8 : 8 / VB;
+  static constexpr int bytes = VB == 3 ? 3 : 1;
+};
+
+// Weighted V sum of one block's chunk of tokens:
+//   part[item][split][j] = sum over t in the chunk of fma(CB_V[code_tj], w_t, .)
+// with w_t the selection weight (0 for tokens left out).  A row of P codes is
+// U = P / VUnit::codes units; a wave takes TPI = max(1, 64 / U) tokens per
+// step, lane (sub, u) the units u, u + 64, ... of token sub, so every lane
+// reads whole bytes of a row in one coalesced cache line.
+template <int VB>
+__global__ __launch_bounds__(kThreads) void sparse_vsum_kernel(HeadDesc *const *item_desc,
+                                                               const float *ws, size_t ws_stride,
+                                                               int chunk, int n_splits,
+                                                               float *partials) {
+  constexpr int CPU = VUnit<VB>::codes, UB = VUnit<VB>::bytes;
+  constexpr int kMaxAcc = 16;  // codes per lane at P = 1024: 4 x 4, 8 x 2 or 2 x 8
+  __shared__ float s_cb[16];
+  __shared__ float s_red[kThreads / 64][kMaxPadded];
+  const int item = blockIdx.y, split = blockIdx.x;
+  const HeadDesc *d = item_desc[item];
+  const int n = d->st.size, cap = d->cap, P = d->padded, vpb = d->v_pb;
+  const int t0 = split * chunk;
+  if (t0 >= n) return;
+  if (threadIdx.x < (1 << VB)) s_cb[threadIdx.x] = cbv<VB>(threadIdx.x);
+  const float *w = ws + (size_t)item * ws_stride;
+  const int s0 = (int)(((long long)d->st.head - n + cap) % cap);
+  const int U = (P + CPU - 1) / CPU;
+  const int TPI = U < 64 ? 64 / U : 1;
+  const int R = U > 64 ? U / 64 : 1;  // units per lane (R * CPU <= kMaxAcc)
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane / (U < 64 ? U : 64), u0 = lane % (U < 64 ? U : 64);
+  const bool active = sub < TPI;
+  float acc[kMaxAcc];
+#pragma unroll
+  for (int k = 0; k < kMaxAcc; ++k) acc[k] = 0.0f;
+  __syncthreads();
+  const int t_end = t0 + chunk < n ? t0 + chunk : n;
+  const uint8_t *vsrc = d->v_codes;
+  if (active) {
+    for (int t = t0 + wave * TPI + sub; t < t_end; t += (kThreads / 64) * TPI) {
+      const float wt = w[t];
+      if (wt == 0.0f) continue;
+      const uint8_t *row = vsrc + (size_t)ring_slot(s0, t, cap) * vpb;
+#pragma unroll
+      for (int r = 0; r < kMaxAcc / CPU; ++r) {
+        if (r >= R) break;
+        const int u = u0 + 64 * r;
+        uint32_t bits;
+        if constexpr (UB == 1) {
+          bits = row[u];
+        } else {
+          // a row of fewer than 8 codes holds a partial group
+          const int b0 = 3 * u;
+          bits = ((uint32_t)row[b0] << 16) | ((b0 + 1 < vpb ? (uint32_t)row[b0 + 1] : 0u) << 8) |
+                 (b0 + 2 < vpb ? (uint32_t)row[b0 + 2] : 0u);
+        }
+#pragma unroll
+        for (int c = 0; c < CPU; ++c) {
+          const int code = (int)((bits >> (VB * (CPU - 1 - c))) & ((1u << VB) - 1u));
+          acc[r * CPU + c] = fmaf(s_cb[code], wt, acc[r * CPU + c]);
+        }
+      }
+    }
+  }
+  // sum the TPI token groups of each wave (lanes u0 + U * sub), then the waves
+  for (int off = U; off < 64; off <<= 1)
+#pragma unroll
+    for (int k = 0; k < kMaxAcc; ++k) acc[k] += __shfl_xor(acc[k], off);
+  if (active && sub == 0) {
+    for (int r = 0; r < R; ++r)
+      for (int c = 0; c < CPU; ++c) {
+        const int j = (u0 + 64 * r) * CPU + c;
+        if (j < P) s_red[wave][j] = acc[r * CPU + c];
+      }
+  }
+  __syncthreads();
+  float *part = partials + ((size_t)item * n_splits + split) * P;
+  for (int j = threadIdx.x; j < P; j += kThreads) {
+    float a = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kThreads / 64; ++k) a += s_red[k][j];
+    part[j] = a;
+  }
+}
+
+// Sum of the splits of each item, inverse FWHT (fwht.cpp:106-134), signs.
+__global__ __launch_bounds__(kThreads) void sparse_finish_kernel(HeadDesc *const *item_desc,
+                                                                 int chunk, int n_splits,
+                                                                 const float *partials,
+                                                                 float *__restrict__ outs) {
+  __shared__ float s_acc[kMaxPadded];
   const int item = blockIdx.x;
   const HeadDesc *d = item_desc[item];
-  const int n = d->st.size, cap = d->cap, dim = d->dim, P = d->padded;
+  const int n = d->st.size, dim = d->dim, P = d->padded;
   float *out = outs + (size_t)item * dim;
   if (n == 0) {
     for (int i = threadIdx.x; i < dim; i += blockDim.x) out[i] = 0.0f;
     return;
   }
-  float *lg = ws + (size_t)item * ws_stride;
-  int N = 1;
-  while (N < n) N <<= 1;
-  Key *keys = N <= kLdsSort ? s_keys : reinterpret_cast<Key *>(lg + sort_cap);
-
-  // max with the reference's starting value and NaN-skipping compare
-  float mx = -1e30f;
-  for (int i = threadIdx.x; i < n; i += blockDim.x)
-    if (lg[i] > mx) mx = lg[i];
-  s_red[threadIdx.x] = mx;
-  __syncthreads();
-  for (int w = blockDim.x / 2; w > 0; w >>= 1) {
-    if ((int)threadIdx.x < w && s_red[threadIdx.x + w] > s_red[threadIdx.x])
-      s_red[threadIdx.x] = s_red[threadIdx.x + w];
-    __syncthreads();
-  }
-  mx = s_red[0];
-  __syncthreads();
-  for (int i = threadIdx.x; i < n; i += blockDim.x) lg[i] = expf(lg[i] - mx);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float sv = 0.0f;
-    for (int i = 0; i < n; ++i) sv = __fadd_rn(sv, lg[i]);
-    s_inv = 1.0f / sv;
-  }
-  __syncthreads();
-  const float inv = s_inv;
-  for (int i = threadIdx.x; i < N; i += blockDim.x) {
-    Key k;
-    if (i < n) {
-      lg[i] = __fmul_rn(lg[i], inv);
-      k.p = lg[i];
-      k.i = i;
-    } else {
-      k.p = -1.0f;
-      k.i = 0x7fffffff;
-    }
-    keys[i] = k;
-  }
-  __syncthreads();
-  bitonic(keys, N);
-
-  if (threadIdx.x == 0) {
-    float mass = 0.0f;
-    int ii = 0;
-    for (; ii + 3 < n && mass < v_mass; ii += 4) {
-      const float q4 = __fadd_rn(__fadd_rn(__fadd_rn(keys[ii].p, keys[ii + 1].p), keys[ii + 2].p),
-                                 keys[ii + 3].p);
-      mass = __fadd_rn(mass, q4);
-    }
-    for (; ii < n && mass < v_mass; ++ii) mass = __fadd_rn(mass, keys[ii].p);
-    s_cut = ii;
-  }
-  __syncthreads();
-  const int cut = s_cut;
-  const float isp = 1.0f / sqrtf((float)P);
+  const int used = (n + chunk - 1) / chunk;
+  const float *part = partials + (size_t)item * n_splits * P;
   for (int j = threadIdx.x; j < P; j += blockDim.x) {
     float a = 0.0f;
-    for (int k = 0; k < cut; ++k) {
-      const int t = keys[k].i;
-      const int slot = (int)(((long long)d->st.head - n + cap + t) % cap);
-      const float w = __fmul_rn(__fmul_rn(keys[k].p, d->v_scale[slot]), isp);
-      a = fmaf(cbv<VB>(code_at<VB>(d->v_codes + (size_t)slot * d->v_pb, j)), w, a);
-    }
+    for (int sp = 0; sp < used; ++sp) a += part[(size_t)sp * P + j];
     s_acc[j] = a;
   }
   __syncthreads();
   for (int len = 1; len < P; len <<= 1) {
     for (int k = threadIdx.x; k < P / 2; k += blockDim.x) {
-      const int j = (k / len) * 2 * len + (k % len);
-      const float lo = s_acc[j], hi = s_acc[j + len];
-      s_acc[j] = lo + hi;
-      s_acc[j + len] = lo - hi;
+      const int jj = (k / len) * 2 * len + (k % len);
+      const float lo = s_acc[jj], hi = s_acc[jj + len];
+      s_acc[jj] = lo + hi;
+      s_acc[jj + len] = lo - hi;
     }
     __syncthreads();
   }
@@ -280,9 +537,14 @@ size_t item_stride(int n) { return (size_t)keys_at(n) + 2 * (size_t)pow2_at_leas
 
 }  // namespace
 
+// Tokens per sparse_vsum_kernel block.
+constexpr int kVChunk = 256;
+
+int vsum_splits(int n) { return (n + kVChunk - 1) / kVChunk; }
+
 size_t sparse_workspace_floats(int n_items, const DecodeShape &sh) {
   const int n = sh.max_n > 0 ? sh.max_n : 1;
-  return (size_t)n_items * item_stride(n);
+  return (size_t)n_items * item_stride(n) + (size_t)n_items * vsum_splits(n) * sh.padded;
 }
 
 hipError_t launch_decode_sparse(HeadDesc *const *descs, int n_items, const DecodeShape &sh,
@@ -295,20 +557,40 @@ hipError_t launch_decode_sparse(HeadDesc *const *descs, int n_items, const Decod
   const float sp = sqrtf((float)sh.padded);
   const float isp = 1.0f / sp;
   const dim3 g1((n + kThreads - 1) / kThreads, n_items);
+#define AQ_LOGITS(PT, KB_) \
+  sparse_logits_kernel<PT, KB_><<<g1, kThreads, 0, s>>>(descs, d_q, n, isp, sp, ws, stride)
   switch (sh.k_bits) {
-    case 2: sparse_logits_kernel<2><<<g1, kThreads, 0, s>>>(descs, d_q, n, isp, sp, ws, stride); break;
-    case 3: sparse_logits_kernel<3><<<g1, kThreads, 0, s>>>(descs, d_q, n, isp, sp, ws, stride); break;
-    case 4: sparse_logits_kernel<4><<<g1, kThreads, 0, s>>>(descs, d_q, n, isp, sp, ws, stride); break;
+    case 2:
+      if (sh.padded == 64) AQ_LOGITS(64, 2);
+      else if (sh.padded == 128) AQ_LOGITS(128, 2);
+      else AQ_LOGITS(0, 2);
+      break;
+    case 3: AQ_LOGITS(0, 3); break;
+    case 4:
+      if (sh.padded == 64) AQ_LOGITS(64, 4);
+      else if (sh.padded == 128) AQ_LOGITS(128, 4);
+      else AQ_LOGITS(0, 4);
+      break;
     default: return hipErrorInvalidValue;
   }
+#undef AQ_LOGITS
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  sparse_select_kernel<<<n_items, kSelThreads, 0, s>>>(descs, v_mass, ws, stride, sort_cap);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int splits = vsum_splits(n);
+  float *parts = ws + (size_t)n_items * stride;
+  const dim3 g3(splits, n_items);
   switch (sh.v_bits) {
-    case 2: sparse_select_kernel<2><<<n_items, kThreads, 0, s>>>(descs, v_mass, ws, stride, sort_cap, d_out); break;
-    case 3: sparse_select_kernel<3><<<n_items, kThreads, 0, s>>>(descs, v_mass, ws, stride, sort_cap, d_out); break;
-    case 4: sparse_select_kernel<4><<<n_items, kThreads, 0, s>>>(descs, v_mass, ws, stride, sort_cap, d_out); break;
+    case 2: sparse_vsum_kernel<2><<<g3, kThreads, 0, s>>>(descs, ws, stride, kVChunk, splits, parts); break;
+    case 3: sparse_vsum_kernel<3><<<g3, kThreads, 0, s>>>(descs, ws, stride, kVChunk, splits, parts); break;
+    case 4: sparse_vsum_kernel<4><<<g3, kThreads, 0, s>>>(descs, ws, stride, kVChunk, splits, parts); break;
     default: return hipErrorInvalidValue;
   }
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  sparse_finish_kernel<<<n_items, kThreads, 0, s>>>(descs, kVChunk, splits, parts, d_out);
   return hipGetLastError();
 }
 

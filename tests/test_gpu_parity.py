@@ -138,19 +138,25 @@ def test_decode_hybrid(oracle, dim, kb, vb, hyb, n):
     assert rel_err(y, r) <= TOL
 
 
-@pytest.mark.parametrize("dim,kb,vb,cap,n,vm", [
-    (64, 4, 2, 2048, 2048, 0.95), (128, 4, 4, 512, 700, 0.95), (64, 3, 2, 600, 513, 0.7),
-    (128, 2, 3, 9000, 9000, 0.95), (64, 4, 2, 100, 7, 0.5),
+# Sort in LDS (n <= 16384) and in the workspace (above); quad sums staged in
+# one and in several chunks (n/4 above 4096); peaked queries (qs 20: the cut
+# falls after a few quads) and flat ones; v_mass near 1 (the single-token tail
+# runs); ragged n.
+@pytest.mark.parametrize("dim,kb,vb,cap,n,vm,qs", [
+    (64, 4, 2, 2048, 2048, 0.95, 3), (128, 4, 4, 512, 700, 0.95, 3), (64, 3, 2, 600, 513, 0.7, 3),
+    (128, 2, 3, 9000, 9000, 0.95, 3), (64, 4, 2, 100, 7, 0.5, 3), (64, 4, 2, 17000, 17001, 0.95, 3),
+    (64, 2, 4, 3000, 2999, 0.95, 20), (128, 4, 2, 20000, 20000, 0.999, 1),
+    (64, 4, 3, 5000, 4998, 0.9999, 0.5),
 ])
-def test_decode_sparse_v(oracle, dim, kb, vb, cap, n, vm):
-    print(f"decode sparse dim={dim} k{kb}v{vb} n={n} v_mass={vm}", flush=True)
+def test_decode_sparse_v(oracle, dim, kb, vb, cap, n, vm, qs):
+    print(f"decode sparse dim={dim} k{kb}v{vb} n={n} v_mass={vm} qscale={qs}", flush=True)
     rng = np.random.default_rng(3 * n + dim)
     k, v = _inputs(rng, n, dim, "normal")
     g = GpuHead(dim, kb, vb, cap, 5, vm, 0)
     o = oracle.head(dim, kb, vb, cap, 5, vm, 0)
     _fill([g, o], k, v)
     for _ in range(2):
-        q = (3 * rng.standard_normal(dim)).astype(np.float32)
+        q = (qs * rng.standard_normal(dim)).astype(np.float32)
         y, _ = g.compute(q)
         r, _ = o.compute(q)
         assert rel_err(y, r) <= TOL
