@@ -31,7 +31,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kSelThreads = 1024;
-constexpr int kLdsSort = 16384;  // sort keys held in LDS up to this many tokens (128 KB)
+constexpr int kLdsSort = 16384;  // tokens sorted in LDS (radix); above, in the workspace
 constexpr int kStage = 4096;    // floats per LDS staging chunk
 
 template <int B>
@@ -175,17 +175,19 @@ __global__ __launch_bounds__(kThreads) void sparse_logits_kernel(HeadDesc *const
 // selection order -- larger p first, equal p older first, NaN after every
 // number, padding (i >= n) after everything.  hi = 0x7F800000 - |p| bits for
 // numbers (p >= 0 here), 0xFFFFFFFF for NaN; lo = i.
-__device__ __forceinline__ uint64_t make_key(float p, int i) {
+__device__ __forceinline__ uint32_t key_hi(float p) {
   const uint32_t b = __float_as_uint(p) & 0x7FFFFFFFu;
-  const uint32_t hi = b > 0x7F800000u ? 0xFFFFFFFFu : 0x7F800000u - b;
-  return ((uint64_t)hi << 32) | (uint32_t)i;
+  return b > 0x7F800000u ? 0xFFFFFFFFu : 0x7F800000u - b;
+}
+__device__ __forceinline__ uint64_t make_key(float p, int i) {
+  return ((uint64_t)key_hi(p) << 32) | (uint32_t)i;
 }
 constexpr uint64_t kPadKey = ~(uint64_t)0;
 
-__device__ __forceinline__ float key_p(uint64_t k) {
-  const uint32_t hi = (uint32_t)(k >> 32);
+__device__ __forceinline__ float hi_p(uint32_t hi) {
   return __uint_as_float(hi == 0xFFFFFFFFu ? 0x7FC00000u : 0x7F800000u - hi);
 }
+__device__ __forceinline__ float key_p(uint64_t k) { return hi_p((uint32_t)(k >> 32)); }
 __device__ __forceinline__ int key_i(uint64_t k) { return (int)(uint32_t)k; }
 
 // Bitonic sort of N (a power of two) keys ascending; each thread takes whole
@@ -209,31 +211,33 @@ __device__ void bitonic(uint64_t *m, int N) {
 }
 
 // acc + s[0] + s[1] + ... + s[m-1], left to right, one lane.  s is 16-byte
-// aligned LDS; the reads of the next 32 values go out before the adds of the
-// current 32.
+// aligned LDS; two register buffers alternate, so the reads of the next 32
+// values are in flight while the current 32 are added.
+__device__ __forceinline__ void load32(float4 (&r)[8], const float4 *s4, int b) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) r[k] = s4[8 * b + k];
+}
+__device__ __forceinline__ float add32(float acc, const float4 (&r)[8]) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    acc = __fadd_rn(acc, r[k].x);
+    acc = __fadd_rn(acc, r[k].y);
+    acc = __fadd_rn(acc, r[k].z);
+    acc = __fadd_rn(acc, r[k].w);
+  }
+  return acc;
+}
 __device__ float serial_sum(const float *s, int m, float acc) {
   const float4 *s4 = reinterpret_cast<const float4 *>(s);
   const int nb = m / 32;
-  float4 cur[8];
-  if (nb > 0) {
-#pragma unroll
-    for (int k = 0; k < 8; ++k) cur[k] = s4[k];
-  }
-  for (int b = 0; b < nb; ++b) {
-    float4 nxt[8];
-    if (b + 1 < nb) {
-#pragma unroll
-      for (int k = 0; k < 8; ++k) nxt[k] = s4[8 * (b + 1) + k];
-    }
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      acc = __fadd_rn(acc, cur[k].x);
-      acc = __fadd_rn(acc, cur[k].y);
-      acc = __fadd_rn(acc, cur[k].z);
-      acc = __fadd_rn(acc, cur[k].w);
-    }
-#pragma unroll
-    for (int k = 0; k < 8; ++k) cur[k] = nxt[k];
+  float4 A[8], B[8];
+  if (nb > 0) load32(A, s4, 0);
+  for (int b = 0; b < nb; b += 2) {
+    if (b + 1 < nb) load32(B, s4, b + 1);
+    acc = add32(acc, A);
+    if (b + 1 >= nb) break;
+    if (b + 2 < nb) load32(A, s4, b + 2);
+    acc = add32(acc, B);
   }
   for (int i = 32 * nb; i < m; ++i) acc = __fadd_rn(acc, s[i]);
   return acc;
@@ -277,43 +281,249 @@ __device__ __forceinline__ int ring_slot(int s0, int t, int cap) {
   return s >= cap ? s - cap : s;
 }
 
-// One block of kSelThreads per item.  Steps, each a parallel pass except the
-// two left-to-right sums the reference's results depend on:
-//   1. max of the logits (block reduction, the reference's NaN-skipping compare)
-//   2. e_t = expf(l_t - max) in chunks of kStage through LDS; thread 0 adds
-//      each chunk left to right (the softmax sum, attention.cpp:422-426)
-//   3. p_t = e_t * (1/sum); bitonic sort by p descending (LDS up to kLdsSort
-//      tokens, else the workspace)
-//   4. quad sums ((p0+p1)+p2)+p3 of the sorted order in parallel, staged
-//      through LDS; thread 0 runs the mass loop over them, then the single
-//      tokens (attention.cpp:454-472)
-//   5. the selection becomes a weight per token in natural order, written
-//      over the logits: (p_t * vscale_t) * isp if selected, else 0
+// Shared memory of the select kernel.  The small path (n <= kLdsSort) keeps
+// 32-bit keys, 16-bit token indices and 16 x kSelThreads 16-bit radix counts;
+// the large path keeps its sort keys in the workspace.
+struct SelectShared {
+  uint32_t key[kLdsSort];                 // also the exponentials, as floats
+  uint16_t idx[kLdsSort];
+  uint16_t cnt[16 * kSelThreads];         // cnt[digit * kSelThreads + thread]
+  __align__(16) float stage[kStage];
+  float red[kSelThreads];
+  uint32_t wsum[kSelThreads / 64];
+  float bcast[2];
+  int cut;
+  uint64_t last;
+};
+
+// Block maximum with the reference's NaN-skipping compare (x > m ? x : m;
+// every partial maximum is a number, so the tree gives the sequential value).
+__device__ __forceinline__ float block_max(float m, SelectShared &sh) {
+  for (int off = 32; off > 0; off >>= 1) {
+    const float y = __shfl_xor(m, off);
+    if (y > m) m = y;
+  }
+  if ((threadIdx.x & 63) == 0) sh.red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  float r = sh.red[0];
+  for (int w = 1; w < (int)(blockDim.x >> 6); ++w)
+    if (sh.red[w] > r) r = sh.red[w];
+  __syncthreads();
+  return r;
+}
+
+// Exclusive scan of cnt[] (16 x kSelThreads 16-bit counts, digit-major) in
+// place: thread t scans entries 16t .. 16t+15, waves scan the thread totals,
+// the wave totals are added in order.
+__device__ __forceinline__ void scan_counts(SelectShared &sh) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint4 *c4 = reinterpret_cast<uint4 *>(sh.cnt) + 2 * tid;
+  const uint4 a = c4[0], b = c4[1];
+  const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  uint32_t v[16];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    v[2 * i] = w[i] & 0xFFFFu;
+    v[2 * i + 1] = w[i] >> 16;
+  }
+  uint32_t run = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const uint32_t t = v[i];
+    v[i] = run;
+    run += t;
+  }
+  uint32_t incl = run;
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t y = __shfl_up(incl, off);
+    if (lane >= off) incl += y;
+  }
+  if (lane == 63) sh.wsum[wave] = incl;
+  __syncthreads();
+  uint32_t base = incl - run;
+  for (int k = 0; k < wave; ++k) base += sh.wsum[k];
+  uint32_t o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = (v[2 * i] + base) | ((v[2 * i + 1] + base) << 16);
+  c4[0] = make_uint4(o[0], o[1], o[2], o[3]);
+  c4[1] = make_uint4(o[4], o[5], o[6], o[7]);
+  __syncthreads();
+}
+
+// Selection for n <= kLdsSort tokens.  Thread t owns tokens E t .. E t + E - 1
+// in registers.  Steps:
+//   1. max of the logits (the reference's start value -1e30 and compare)
+//   2. e = expf(l - max) into LDS; thread 0 adds them left to right
+//      (attention.cpp:422-426); p = e * (1/sum)
+//   3. stable LSD radix sort of the 32-bit keys, 4 bits a pass, skipping
+//      digits every key shares: order p descending, ties older first
+//   4. quad sums ((p0+p1)+p2)+p3 of the sorted order in parallel; thread 0
+//      runs the mass loop over them, then the single tokens
+//      (attention.cpp:454-472)
+//   5. per-token weights (p * vscale) * isp for the selected tokens, else 0,
+//      written over the logits at each token's index
+template <int E>
+__device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, float *lg, int n, int s0,
+                             SelectShared &sh) {
+  const int tid = threadIdx.x, p0 = tid * E;
+  const int cap = d->cap, P = d->padded;
+  float ev[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) ev[e] = p0 + e < n ? lg[p0 + e] : 0.0f;
+  float mx = -1e30f;
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+    if (p0 + e < n && ev[e] > mx) mx = ev[e];
+  mx = block_max(mx, sh);
+
+  // (the exponentials wait in LDS, not in registers, while thread 0 adds)
+  float *ef = reinterpret_cast<float *>(sh.key);
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+    if (p0 + e < n) ef[p0 + e] = expf(ev[e] - mx);
+  __syncthreads();
+  if (tid == 0) sh.bcast[0] = 1.0f / serial_sum(ef, n, 0.0f);
+  __syncthreads();
+  const float inv = sh.bcast[0];
+#pragma unroll
+  for (int e = 0; e < E; ++e) ev[e] = ef[p0 + e];
+  __syncthreads();
+
+  uint32_t k[E], ix[E];
+  uint32_t kor = 0, kand = 0xFFFFFFFFu;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    k[e] = p0 + e < n ? key_hi(__fmul_rn(ev[e], inv)) : 0xFFFFFFFFu;
+    ix[e] = (uint32_t)(p0 + e);
+    kor |= k[e];
+    kand &= k[e];
+  }
+  // digits every key shares do not move anything: skip their passes
+  for (int off = 32; off > 0; off >>= 1) {
+    kor |= __shfl_xor(kor, off);
+    kand &= __shfl_xor(kand, off);
+  }
+  if ((tid & 63) == 0) {
+    sh.wsum[tid >> 6] = kor;
+    reinterpret_cast<uint32_t *>(sh.red)[tid >> 6] = kand;
+  }
+  __syncthreads();
+  uint32_t diff = 0;
+  {
+    uint32_t o = 0, a = 0xFFFFFFFFu;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) {
+      o |= sh.wsum[w];
+      a &= reinterpret_cast<uint32_t *>(sh.red)[w];
+    }
+    diff = o ^ a;
+  }
+  __syncthreads();
+
+  for (int sft = 0; sft < 32; sft += 4) {
+    if (((diff >> sft) & 15u) == 0) continue;
+    // counts of each digit among this thread's tokens (8-bit fields) and the
+    // rank of each token among its thread's tokens of the same digit
+    // (the rank goes into bits 16.. of ix, below the token index's 16 bits)
+    uint64_t c_lo = 0, c_hi = 0;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const uint32_t dg = (k[e] >> sft) & 15u;
+      const uint32_t f = (dg & 7u) * 8u;
+      const uint64_t cw = dg < 8u ? c_lo : c_hi;
+      ix[e] = (ix[e] & 0xFFFFu) | ((uint32_t)(cw >> f) & 255u) << 16;
+      if (dg < 8u) c_lo += (uint64_t)1 << f;
+      else c_hi += (uint64_t)1 << f;
+    }
+#pragma unroll
+    for (int dd = 0; dd < 16; ++dd)
+      sh.cnt[dd * kSelThreads + tid] =
+          (uint16_t)(((dd < 8 ? c_lo : c_hi) >> ((dd & 7) * 8)) & 255u);
+    __syncthreads();
+    scan_counts(sh);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const uint32_t dg = (k[e] >> sft) & 15u;
+      const uint32_t dst = (uint32_t)sh.cnt[dg * kSelThreads + tid] + (ix[e] >> 16);
+      sh.key[dst] = k[e];
+      sh.idx[dst] = (uint16_t)ix[e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      k[e] = sh.key[p0 + e];
+      ix[e] = sh.idx[p0 + e];
+    }
+    __syncthreads();
+  }
+  // sorted order into LDS (the passes may all have been skipped)
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    sh.key[p0 + e] = k[e];
+    sh.idx[p0 + e] = (uint16_t)ix[e];
+  }
+  __syncthreads();
+
+  const int n_quads = n / 4;
+  for (int q = tid; q < n_quads; q += blockDim.x)
+    sh.stage[q] = __fadd_rn(__fadd_rn(__fadd_rn(hi_p(sh.key[4 * q]), hi_p(sh.key[4 * q + 1])),
+                                      hi_p(sh.key[4 * q + 2])),
+                            hi_p(sh.key[4 * q + 3]));
+  __syncthreads();
+  if (tid == 0) {
+    float mass = 0.0f;
+    int ii = 4 * mass_scan(sh.stage, n_quads, v_mass, &mass);
+    for (; ii < n && mass < v_mass; ++ii) mass = __fadd_rn(mass, hi_p(sh.key[ii]));
+    sh.cut = ii;
+  }
+  __syncthreads();
+  // sorted position r holds token idx[r] with probability hi_p(key[r]); the
+  // first cut positions are the selection
+  const int cut = sh.cut;
+  const float isp = 1.0f / sqrtf((float)P);
+  float vs[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int r = p0 + e;
+    vs[e] = r < cut ? d->v_scale[ring_slot(s0, sh.idx[r], cap)] : 0.0f;
+  }
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int r = p0 + e;
+    if (r < n) lg[sh.idx[r]] = r < cut ? __fmul_rn(__fmul_rn(hi_p(sh.key[r]), vs[e]), isp) : 0.0f;
+  }
+}
+
+// One block of kSelThreads per item: the sparse-V selection as per-token
+// weights.  n <= kLdsSort: select_small.  Larger n: the same steps with the
+// logits and 64-bit sort keys in the workspace and a bitonic sort there.
 // sparse_vsum_kernel then sums the weighted V rows over many blocks and
-// sparse_finish_kernel applies the inverse FWHT.  The V sum runs in natural
-// token order instead of the reference's sorted order, which changes only its
+// sparse_finish_kernel applies the inverse FWHT.  The V sum runs in token
+// order instead of the reference's sorted order, which changes only its
 // rounding; the selected set is the reference's.
 __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *const *item_desc,
                                                                     float v_mass, float *ws,
                                                                     size_t ws_stride,
                                                                     int sort_cap) {
-  __shared__ uint64_t s_keys[kLdsSort];
-  __shared__ __align__(16) float s_stage[kStage];
-  __shared__ float s_red[kSelThreads];
-  __shared__ float s_acc[kMaxPadded];
-  __shared__ float s_bcast[2];
-  __shared__ int s_cut;
-  __shared__ uint64_t s_last;
+  __shared__ SelectShared sh;
   const int item = blockIdx.x;
   const int tid = threadIdx.x;
   const HeadDesc *d = item_desc[item];
   const int n = d->st.size, cap = d->cap, P = d->padded;
   if (n == 0) return;
   float *lg = ws + (size_t)item * ws_stride;
+  const int s0 = (int)(((long long)d->st.head - n + cap) % cap);
+  if (n <= kLdsSort) {
+    if (n <= kSelThreads) select_small<1>(d, v_mass, lg, n, s0, sh);
+    else if (n <= 2 * kSelThreads) select_small<2>(d, v_mass, lg, n, s0, sh);
+    else if (n <= 4 * kSelThreads) select_small<4>(d, v_mass, lg, n, s0, sh);
+    else if (n <= 8 * kSelThreads) select_small<8>(d, v_mass, lg, n, s0, sh);
+    else select_small<16>(d, v_mass, lg, n, s0, sh);
+    return;
+  }
   int N = 1;
   while (N < n) N <<= 1;
-  uint64_t *keys = N <= kLdsSort ? s_keys : reinterpret_cast<uint64_t *>(lg + sort_cap);
-  const int s0 = (int)(((long long)d->st.head - n + cap) % cap);
+  uint64_t *keys = reinterpret_cast<uint64_t *>(lg + sort_cap);
+  float *s_stage = sh.stage, *s_red = sh.red, *s_bcast = sh.bcast;
 
   // 1. max with the reference's starting value and NaN-skipping compare
   float mx = -1e30f;
@@ -374,12 +584,12 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
   }
   if (tid == 0) {
     for (; ii < n && mass < v_mass; ++ii) mass = __fadd_rn(mass, key_p(keys[ii]));
-    s_cut = ii;
-    s_last = ii > 0 ? keys[ii - 1] : 0;
+    sh.cut = ii;
+    sh.last = ii > 0 ? keys[ii - 1] : 0;
   }
   __syncthreads();
-  const int cut = s_cut;
-  const uint64_t last = s_last;
+  const int cut = sh.cut;
+  const uint64_t last = sh.last;
 
   // 5. per-token weights in natural order: the selection is the cut first
   // keys of the sorted order, i.e. every key up to the last one taken (keys
