@@ -67,22 +67,43 @@ struct Row {
   static constexpr int words = (bytes + 3) / 4;
 };
 
+// The packed word k of a row whose codes are all the NaN code (1 / 3 / 7 for
+// 2 / 3 / 4 bits): 0x55 and 0x77 bytes; 3-bit rows repeat the 24-bit group
+// 011 x 8 = bytes 6D B6 DB.
+template <int B>
+__device__ __forceinline__ uint32_t nan_word(int k) {
+  if constexpr (B == 2) return 0x55555555u;
+  else if constexpr (B == 4) return 0x77777777u;
+  else return k % 3 == 0 ? 0x6DDBB66Du : k % 3 == 1 ? 0xB66DDBB6u : 0xDBB66DDBu;
+}
+
 // Encode n_tok tokens of one side (K or V) for n_ctx heads.
-template <int P, int B>
+// UNIFORM: block (x, y) holds tokens x * 128 .. of head y, so a wave never
+// mixes heads: the descriptor and sign words are scalar loads and a sign flip
+// is one XOR with a scalar mask.  Otherwise lanes run over (head, token)
+// pairs in order (for few tokens per head).
+template <int P, int B, bool UNIFORM>
 __global__ __launch_bounds__(128) void append_kernel(HeadDesc *const *descs, int n_ctx,
                                                      int side, const float *__restrict__ src,
                                                      int n_tok, int dim, float inv_sqrt_p,
                                                      float sqrt_p) {
-  // 4-bit codes: the bucket table of quantize4_tab, built before any lane leaves
+  // 4-bit codes: the bucket table of quantize_ss4, built before any lane leaves
   __shared__ Q4Entry s_q4[B == 4 ? kQ4Entries : 1];
   if constexpr (B == 4) {
-    for (int i = threadIdx.x; i < kQ4Entries; i += blockDim.x) s_q4[i] = q4_entry(i);
+    for (int i = threadIdx.x; i < kQ4Entries; i += blockDim.x) s_q4[i] = q4s_entry(i);
     __syncthreads();
   }
-  const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (g >= (long long)n_ctx * n_tok) return;
-  const int c = (int)(g / n_tok);
-  const int t = (int)(g - (long long)c * n_tok);
+  int c, t;
+  if constexpr (UNIFORM) {
+    c = blockIdx.y;
+    t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n_tok) return;
+  } else {
+    const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= (long long)n_ctx * n_tok) return;
+    c = (int)(g / n_tok);
+    t = (int)(g - (long long)c * n_tok);
+  }
   const HeadDesc *d = descs[c];
   const RingState st = d->st;
   const int cap = d->cap;
@@ -131,24 +152,18 @@ __global__ __launch_bounds__(128) void append_kernel(HeadDesc *const *descs, int
     for (int i = 0; i < P; ++i) s = __fadd_rn(s, __fmul_rn(buf[i], buf[i]));
     const float norm = sqrtf(__fadd_rn(s, 1e-12f));
     const float inv = 1.0f / norm;
-#pragma unroll
-    for (int i = 0; i < P; ++i) buf[i] = __fmul_rn(buf[i], inv);
 
-    // Signs fused into the first butterfly stage (exact: a sign flip).
+    // Normalise; the sign D[i] = -1 is an exact flip of the sign bit.
     uint32_t sg[(P + 31) / 32];
 #pragma unroll
     for (int k = 0; k < (P + 31) / 32; ++k) sg[k] = d->signs[k];
 #pragma unroll
-    for (int i = 0; i < P; i += 2) {
-      const uint32_t f0 = ((sg[i / 32] >> (i % 32)) & 1u) ^ 1u;
-      const uint32_t f1 = ((sg[(i + 1) / 32] >> ((i + 1) % 32)) & 1u) ^ 1u;
-      const float a = __uint_as_float(__float_as_uint(buf[i]) ^ (f0 << 31));
-      const float b = __uint_as_float(__float_as_uint(buf[i + 1]) ^ (f1 << 31));
-      buf[i] = __fadd_rn(a, b);
-      buf[i + 1] = __fsub_rn(a, b);
+    for (int i = 0; i < P; ++i) {
+      const uint32_t flip = (~sg[i / 32] >> (i % 32)) << 31;
+      buf[i] = __uint_as_float(__float_as_uint(__fmul_rn(buf[i], inv)) ^ flip);
     }
 #pragma unroll
-    for (int len = 2; len < P; len <<= 1) {
+    for (int len = 1; len < P; len <<= 1) {
 #pragma unroll
       for (int base = 0; base < P; base += 2 * len) {
 #pragma unroll
@@ -167,16 +182,16 @@ __global__ __launch_bounds__(128) void append_kernel(HeadDesc *const *descs, int
     for (int i = 0; i < P; ++i) s2 = __fadd_rn(s2, __fmul_rn(buf[i], buf[i]));
     const float sigma = sqrtf(__fadd_rn(s2 / (float)P, 1e-12f));
     const float clip = __fmul_rn(3.0f, sigma);
+    const float nclip = -clip;
 
     uint32_t w[Row<P, B>::words];
 #pragma unroll
     for (int k = 0; k < Row<P, B>::words; ++k) w[k] = 0u;
 #pragma unroll
     for (int i = 0; i < P; ++i) {
-      float v = buf[i];
-      if (v > clip) v = clip;
-      if (v < -clip) v = -clip;
-      const uint32_t q = B == 4 ? quantize4_tab(v, s_q4) : quantize<B>(v);
+      // the reference's two-sided clamp is the median for finite values
+      const float v = __builtin_amdgcn_fmed3f(buf[i], nclip, clip);
+      const uint32_t q = B == 4 ? quantize_ss4(v, s_q4) : B == 3 ? quantize_ss3(v) : quantize_ss2(v);
       // Bit position of code i inside the little-endian word stream.
       int byte, shift;
       if constexpr (B == 4) {
@@ -205,6 +220,12 @@ __global__ __launch_bounds__(128) void append_kernel(HeadDesc *const *descs, int
         }
       }
       w[byte / 4] |= q << (8 * (byte % 4) + shift);
+    }
+    // A NaN anywhere in the input reaches every element (the FWHT sums all of
+    // them), and then s2 is NaN: every code is the NaN code.
+    if (s2 != s2) {
+#pragma unroll
+      for (int k = 0; k < Row<P, B>::words; ++k) w[k] = nan_word<B>(k);
     }
     constexpr int xmask = kperm_mask(P, B);
     bool stored = false;
@@ -340,21 +361,35 @@ hipError_t launch_wide(HeadDesc *const *descs, int n_ctx, int side, int bits, co
   return hipGetLastError();
 }
 
-template <int P>
-hipError_t launch_side(HeadDesc *const *descs, int n_ctx, int side, int bits, const float *src,
-                       int n_tok, int dim, hipStream_t s) {
+template <int P, bool U>
+hipError_t launch_side_as(HeadDesc *const *descs, int n_ctx, int side, int bits, const float *src,
+                          int n_tok, int dim, hipStream_t s) {
   const float sp = sqrtf((float)P);
   const float isp = 1.0f / sp;
-  const long long total = (long long)n_ctx * n_tok;
-  const dim3 grid((unsigned)((total + 127) / 128));
+  dim3 grid;
+  if (U) {
+    grid = dim3((unsigned)((n_tok + 127) / 128), (unsigned)n_ctx);
+  } else {
+    const long long total = (long long)n_ctx * n_tok;
+    grid = dim3((unsigned)((total + 127) / 128));
+  }
   switch (bits) {
-    case 2: append_kernel<P, 2><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp); break;
-    case 3: append_kernel<P, 3><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp); break;
-    case 4: append_kernel<P, 4><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp); break;
-    case 16: append_kernel<P, 16><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp); break;
+    case 2: append_kernel<P, 2, U><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp); break;
+    case 3: append_kernel<P, 3, U><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp); break;
+    case 4: append_kernel<P, 4, U><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp); break;
+    case 16: append_kernel<P, 16, U><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+// Head-per-block launches once a head has at least a wave of tokens.
+template <int P>
+hipError_t launch_side(HeadDesc *const *descs, int n_ctx, int side, int bits, const float *src,
+                       int n_tok, int dim, hipStream_t s) {
+  if (n_tok >= 64 && n_ctx <= 65535)
+    return launch_side_as<P, true>(descs, n_ctx, side, bits, src, n_tok, dim, s);
+  return launch_side_as<P, false>(descs, n_ctx, side, bits, src, n_tok, dim, s);
 }
 
 }  // namespace

@@ -83,4 +83,63 @@ AQ_HD inline uint32_t quantize4_tab(float v, const Q4Entry *tab) {
   return v != v ? 7u : idx;
 }
 
+// Sign-split quantisers of the append kernel, for finite v (a NaN vector is
+// given the NaN code by the caller: a NaN in any input element reaches every
+// element through the FWHT, so NaN is a property of the whole vector).
+//   s   = sign of v as 0 or ~0
+//   key = bits(|v|) + [sign bit clear]
+//   u   = centre code 2^(B-1) + #{positive thresholds t : key > bits(t)}
+//   code = u ^ (s & (2^B - 1))
+// For v >= 0, key > bits(t) is v >= t; for v < 0 it is |v| > t, and the
+// negative side's count 2^(B-1) - 1 - m equals (2^(B-1) + m) ^ (2^B - 1).
+// -0.0 belongs to the positive side (-0.0 >= 0 holds): the 2- and 3-bit forms
+// add +0.0 first (which turns -0.0 into +0.0 and changes nothing else); the
+// 4-bit form reads the bucket table with n raised by 8 (q4s_entry), whose
+// lowest bucket holds a threshold at key 0 over a base count of 7, so key 0
+// (only -0.0 has it) gives 7 ^ 15 = 8 and every other key in it gives 8.
+// Equality with quantize<B> over every finite float is checked on the host
+// (tests/cpp/quant_exhaustive.cpp).
+struct SignSplit {
+  uint32_t s, ab, key;
+};
+
+AQ_HD inline SignSplit sign_split(float c) {
+  const uint32_t bits = f32_bits(c);
+  SignSplit r;
+  r.s = (uint32_t)((int32_t)bits >> 31);
+  r.ab = bits & 0x7FFFFFFFu;
+  r.key = r.ab + 1u + r.s;
+  return r;
+}
+
+AQ_HD inline Q4Entry q4s_entry(int i) {
+  Q4Entry e = q4_entry(i);
+  if (i == 0) return Q4Entry{0u, 7u};  // holds no threshold (checked below)
+  e.n += 8u;
+  return e;
+}
+
+AQ_HD inline uint32_t quantize_ss4(float v, const Q4Entry *tab8) {
+  const SignSplit x = sign_split(v);
+  uint32_t b = x.ab >> 18;
+  b = b < (uint32_t)kQ4Lo ? (uint32_t)kQ4Lo : b > (uint32_t)kQ4Hi ? (uint32_t)kQ4Hi : b;
+  const Q4Entry e = tab8[b - kQ4Lo];
+  const uint32_t u = e.n + (x.key > e.t ? 1u : 0u);
+  return u ^ (x.s & 15u);
+}
+
+AQ_HD inline uint32_t quantize_ss3(float v) {
+  const SignSplit x = sign_split(v + 0.0f);
+  const uint32_t u = 4u + (x.key > f32_bits(thr<3>(4)) ? 1u : 0u) +
+                     (x.key > f32_bits(thr<3>(5)) ? 1u : 0u) +
+                     (x.key > f32_bits(thr<3>(6)) ? 1u : 0u);
+  return u ^ (x.s & 7u);
+}
+
+AQ_HD inline uint32_t quantize_ss2(float v) {
+  const SignSplit x = sign_split(v + 0.0f);
+  const uint32_t u = 2u + (x.key > f32_bits(thr<2>(2)) ? 1u : 0u);
+  return u ^ (x.s & 3u);
+}
+
 }  // namespace aq

@@ -1,7 +1,10 @@
-// Every float bit pattern: quantize4_tab (adaptq_amd/csrc/quant.hpp, the
-// append kernel's 4-bit quantiser) against quantize<4> (the reference's binary
-// search restated) and, on a stride, against the oracle's quantize_fast.
-// Prints the mismatch count; exits 0 when it is 0.
+// Every float bit pattern: quantize4_tab and the sign-split quantisers
+// quantize_ss2/3/4 (adaptq_amd/csrc/quant.hpp, the append kernel's) against
+// quantize<B> (the reference's binary search restated) and, on a stride,
+// against the oracle's quantize_fast.  The sign-split forms are defined for
+// finite inputs (the kernel gives NaN vectors their code as a whole), so NaN
+// patterns are skipped for them.  Prints the mismatch count; exits 0 when it
+// is 0.
 #include <atomic>
 #include <cstdio>
 #include <cstring>
@@ -13,8 +16,15 @@
 extern "C" int orc_quantize_fast(float v, int bits);
 
 int main() {
-  aq::Q4Entry tab[aq::kQ4Entries];
-  for (int i = 0; i < aq::kQ4Entries; ++i) tab[i] = aq::q4_entry(i);
+  aq::Q4Entry tab[aq::kQ4Entries], tab8[aq::kQ4Entries];
+  for (int i = 0; i < aq::kQ4Entries; ++i) {
+    tab[i] = aq::q4_entry(i);
+    tab8[i] = aq::q4s_entry(i);
+  }
+  if (tab[0].n != 0 || tab[0].t != ~0u) {
+    std::printf("lowest bucket holds a threshold\n");
+    return 1;
+  }
   std::atomic<unsigned long long> bad{0};
   const int T = 8;
   std::vector<std::thread> pool;
@@ -28,8 +38,15 @@ int main() {
         const uint32_t a = aq::quantize4_tab(v, tab), b = aq::quantize<4>(v);
         bool wrong = a != b;
         if ((u & 0xFFF) == 0x5A5) wrong = wrong || (int)b != orc_quantize_fast(v, 4);
+        if (v == v) {
+          wrong = wrong || aq::quantize_ss4(v, tab8) != b;
+          wrong = wrong || aq::quantize_ss3(v) != aq::quantize<3>(v);
+          wrong = wrong || aq::quantize_ss2(v) != aq::quantize<2>(v);
+        }
         if (wrong && bad.fetch_add(1) < 10)
-          std::printf("mismatch bits=%08x v=%g tab=%u search=%u\n", u, v, a, b);
+          std::printf("mismatch bits=%08x v=%g tab=%u search=%u ss4=%u ss3=%u/%u ss2=%u/%u\n", u, v,
+                      a, b, aq::quantize_ss4(v, tab8), aq::quantize_ss3(v), aq::quantize<3>(v),
+                      aq::quantize_ss2(v), aq::quantize<2>(v));
       }
     });
   for (auto &t : pool) t.join();

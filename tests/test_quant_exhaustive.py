@@ -1,7 +1,8 @@
-"""The append kernel's 4-bit quantiser (quantize4_tab in adaptq_amd/csrc/quant.hpp,
-one table lookup) equals the reference's binary search (quantize<4>) on every
-float bit pattern, and the oracle's quantize_fast on a stride of them: the
-header is compiled for the host by tests/cpp/quant_exhaustive.cpp (~3 s on 8
+"""The append kernel's quantisers (quantize4_tab and the sign-split
+quantize_ss2/3/4 in adaptq_amd/csrc/quant.hpp) equal the reference's binary
+search (quantize<B>) on every float bit pattern (every finite one for the
+sign-split forms), and the oracle's quantize_fast on a stride of them: the
+header is compiled for the host by tests/cpp/quant_exhaustive.cpp (~10 s on 8
 threads)."""
 import os
 import shutil
