@@ -1132,25 +1132,38 @@ int adaptq_plan_compute_device(adaptq_plan_t h, const float *d_queries, float *d
     return -1;
   Plan *p = static_cast<Plan *>(h);
   int max_n = 0;
+  bool have_mode = false;
+  Mode mode = Mode::Dense;
   for (Ctx *c : p->ctxs) {
     std::lock_guard<std::mutex> g(c->mu);
     if (!flush_locked(c, fn)) return -1;
-    if (c->st.size > 0 && mode_of(c) != Mode::Dense) {
-      set_error(
-          "adaptq_plan_compute_device: a context takes the sparse-V or hybrid branch; "
-          "use adaptq_compute for it");
-      return -1;
+    if (c->st.size > 0) {
+      const Mode m = mode_of(c);
+      if (have_mode && m != mode) {
+        set_error(
+            "adaptq_plan_compute_device: contexts take different branches (dense, sparse-V, "
+            "hybrid); use one plan per branch or adaptq_compute");
+        return -1;
+      }
+      mode = m;
+      have_mode = true;
     }
     max_n = std::max(max_n, c->st.size);
   }
   const Ctx *c0 = p->ctxs[0];
   const int n_items = (int)p->ctxs.size();
-  aq::DecodeShape sh{c0->dim, c0->padded, c0->k_bits, c0->v_bits, false, max_n};
+  aq::DecodeShape sh{c0->dim, c0->padded, c0->k_bits, c0->v_bits, mode == Mode::Hybrid, max_n};
   DeviceGuard g(p->device);
-  if (hip_fail(p->d_ws.ensure(aq::decode_workspace_floats(n_items, sh) * 4), fn)) return -1;
+  const size_t wsf = mode == Mode::Sparse ? aq::sparse_workspace_floats(n_items, sh)
+                                          : aq::decode_workspace_floats(n_items, sh);
+  if (hip_fail(p->d_ws.ensure(wsf * 4), fn)) return -1;
   hipStream_t s = static_cast<hipStream_t>(stream);  // NULL = the HIP null stream
-  hipError_t e = aq::launch_decode(static_cast<aq::HeadDesc **>(p->d_list.p), n_items, sh,
-                                   d_queries, d_outs, static_cast<float *>(p->d_ws.p), s);
+  auto **items = static_cast<aq::HeadDesc **>(p->d_list.p);
+  float *ws = static_cast<float *>(p->d_ws.p);
+  const hipError_t e = mode == Mode::Sparse && max_n > 0
+                           ? aq::launch_decode_sparse(items, n_items, sh, c0->v_mass, d_queries,
+                                                      d_outs, ws, s)
+                           : aq::launch_decode(items, n_items, sh, d_queries, d_outs, ws, s);
   if (hip_fail(e, fn)) return -1;
   return 0;
 }

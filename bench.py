@@ -125,7 +125,9 @@ def secondary(L, last_error, torch, np, stream, reps=20):
           (Engine defaults: every layer takes the raw-mirror branch).
       C3: 22 layers x 4 heads d64 (layer 0 K16/V2, others K3/V2), Student-t(4)
           / sqrt 2: 1024-token bulk append, then 256 steps of (append 1 +
-          decode) for every layer; µs per step, host wall clock included.
+          decode) for every layer; µs per step, host wall clock included;
+          per-layer calls (as the reference's Engine makes them) and two
+          plans (layer 0, layers 1-21) per step.
       C4: 8 heads d128 K4/V4, cap 32768, 40000 tokens appended (7232
           evictions), 64 queries per head in one launch."""
     import ctypes as C
@@ -258,7 +260,34 @@ def secondary(L, last_error, torch, np, stream, reps=20):
         wall = (time.perf_counter() - t0) * 1e6
         c3[name] = {"us_per_step": wall / steps, "gpu_us_per_step": a.elapsed_time(b) * 1e3 / steps,
                     "bulk_append_us": append_us, "decode_bytes_256_steps": step_bytes,
-                    "launches_per_step": 2 * nl}
+                    "calls_per_step": 2 * nl}
+        free(ms)
+
+        # the same steps through two plans (layer 0, layers 1-21): one append
+        # call and one decode call per plan and step
+        ms = stack([(nh, 64, 16 if l == 0 else 3, 2, 1280, l, vm, hyb) for l in range(nl)])
+        bulk_append()
+        ctx = [L.adaptq_mha_head(m, h) for m in ms for h in range(nh)]
+        plans = [L.adaptq_plan_create((C.c_void_p * nh)(*ctx[:nh]), nh),
+                 L.adaptq_plan_create((C.c_void_p * (len(ctx) - nh))(*ctx[nh:]), len(ctx) - nh)]
+        if not all(plans):
+            raise RuntimeError(last_error())
+        torch.cuda.synchronize()
+        a.record(stream)
+        t0 = time.perf_counter()
+        for s in range(steps):
+            for pl, lo, hi in ((plans[0], 0, 1), (plans[1], 1, nl)):
+                ok(L.adaptq_plan_append_device(pl, dp(per[0, s, lo:hi]), dp(per[1, s, lo:hi]), 1,
+                                               n0 + s, sp))
+                ok(L.adaptq_plan_compute_device(pl, dp(per[2, s, lo:hi]), dp(od[lo:hi]), sp))
+        b.record(stream)
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) * 1e6
+        c3[name + "_plans"] = {"us_per_step": wall / steps,
+                               "gpu_us_per_step": a.elapsed_time(b) * 1e3 / steps,
+                               "calls_per_step": 4}
+        for pl in plans:
+            L.adaptq_plan_destroy(pl)
         free(ms)
     res["C3"] = c3
     del bulk, per
@@ -366,10 +395,20 @@ def main():
     assert plan, _lib.last_error()
     t_create = time.time() - t0
 
-    # bulk append in chunks of heads (synthetic data generated on the GPU)
+    # bulk append in chunks of heads (synthetic data generated on the GPU),
+    # after one untimed append on a throwaway context of the same shape (the
+    # first launch of a kernel also loads its code object)
+    warm = L.adaptq_create(dim, kb, vb, 128, 0, 0.0, 0)
+    wk = torch.zeros(128, dim, device=dev)
+    assert L.adaptq_plan_append_device(
+        wplan := L.adaptq_plan_create((C.c_void_p * 1)(warm), 1), C.c_void_p(wk.data_ptr()),
+        C.c_void_p(wk.data_ptr()), 128, 0, sptr) == 0, _lib.last_error()
+    torch.cuda.synchronize()
+    L.adaptq_plan_destroy(wplan)
+    L.adaptq_destroy(warm)
     g = torch.Generator(device=dev)
     g.manual_seed(42)
-    chunk = 256
+    chunk = 1024
     scales = torch.exp(0.5 * torch.randn(H, generator=g, device=dev))
     append_ms = 0.0
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

@@ -253,8 +253,10 @@ int adaptq_plan_append_device(adaptq_plan_t plan, const float *d_keys,
 /* One decode step for every context of the plan in one launch.
  * d_queries [n_ctx][dim] -> d_outs [n_ctx][dim], device memory, async on
  * `stream`.  Same results as adaptq_compute per context; contexts with an
- * empty ring get zeros.  Returns 0/-1 (ADAPTQ_ERR_UNSUPPORTED when a context
- * would take the sparse-V or hybrid branch: use adaptq_compute for those). */
+ * empty ring get zeros.  Every non-empty context must take the same branch
+ * (dense, sparse-V or hybrid; attention.cpp:480-660), which then runs as one
+ * batched launch sequence.  Returns 0/-1 (-1 with a message when the
+ * branches differ). */
 int adaptq_plan_compute_device(adaptq_plan_t plan, const float *d_queries,
                                float *d_outs, void *stream);
 

@@ -77,3 +77,57 @@ def test_plan_empty_rings_give_zeros():
     sync()
     assert np.all(do.download((H, dim)) == 0)
     L.adaptq_plan_destroy(plan)
+
+
+# Sparse-V (v_mass > 0) and hybrid (raw mirror) branches through one plan:
+# heads hold different numbers of tokens, outputs match the oracle per head.
+@pytest.mark.parametrize("dim,kb,vb,cap,vm,hyb,sizes", [
+    (64, 4, 2, 4096, 0.95, 0, [2048, 1500, 3000, 7]),
+    (128, 3, 2, 2048, 0.9, 0, [1025, 1280, 600]),
+    (64, 4, 2, 1024, 0.95, 512, [512, 300, 1, 64]),
+    (128, 16, 2, 256, 0.95, 256, [200, 256]),
+])
+def test_plan_compute_sparse_and_hybrid(oracle, dim, kb, vb, cap, vm, hyb, sizes):
+    print(f"plan branch dim={dim} k{kb}v{vb} v_mass={vm} hyb={hyb} sizes={sizes}", flush=True)
+    H = len(sizes)
+    rng = np.random.default_rng(dim + len(sizes))
+    heads = [GpuHead(dim, kb, vb, cap, 200 + i, vm, hyb) for i in range(H)]
+    refs = [oracle.head(dim, kb, vb, cap, 200 + i, vm, hyb) for i in range(H)]
+    for i, n in enumerate(sizes):
+        kv = rng.standard_normal((n, 2, dim)).astype(np.float32)
+        for t in range(n):
+            heads[i].append(kv[t, 0], kv[t, 1], t)
+            refs[i].append(kv[t, 0], kv[t, 1], t)
+    arr = (C.c_void_p * H)(*[h.h for h in heads])
+    plan = L.adaptq_plan_create(arr, H)
+    assert plan, err()
+    for _ in range(2):
+        q = (3 * rng.standard_normal((H, dim))).astype(np.float32)
+        dq, do = DeviceBuffer(q.nbytes), DeviceBuffer(q.nbytes)
+        dq.upload(q)
+        assert L.adaptq_plan_compute_device(plan, dq.ptr, do.ptr, None) == 0, err()
+        sync()
+        y = do.download((H, dim))
+        for i, o in enumerate(refs):
+            r = o.compute(q[i])[0]
+            assert rel_err(y[i], r) <= 1e-4, (i, rel_err(y[i], r))
+    L.adaptq_plan_destroy(plan)
+
+
+def test_plan_rejects_mixed_branches():
+    # head 0 keeps its raw mirror (hybrid branch), head 1 has evicted (sparse-V)
+    dim = 64
+    a, b = GpuHead(dim, 4, 2, 8, 1, 0.95, 8), GpuHead(dim, 4, 2, 8, 2, 0.95, 8)
+    x = np.ones(dim, np.float32)
+    for t in range(4):
+        a.append(x, x, t)
+    for t in range(9):
+        b.append(x, x, t)
+    arr = (C.c_void_p * 2)(a.h, b.h)
+    plan = L.adaptq_plan_create(arr, 2)
+    assert plan, err()
+    dq, do = DeviceBuffer(2 * dim * 4), DeviceBuffer(2 * dim * 4)
+    dq.upload(np.ones((2, dim), np.float32))
+    assert L.adaptq_plan_compute_device(plan, dq.ptr, do.ptr, None) == -1
+    assert "different branches" in err()
+    L.adaptq_plan_destroy(plan)
