@@ -111,7 +111,7 @@ def cpu_baseline(cfg, seconds=12.0, heads=8, seed=0):
     }
 
 
-def secondary(L, last_error, torch, np, stream, reps=20):
+def secondary(L, last_error, torch, np, stream, reps=20, which=("C1", "C2", "C3", "C4")):
     """BASELINE configs[0..3] timed on the GPU (not the headline): medians of
     `reps` HIP-event spans on `stream`, in µs, with the algorithmic bytes each
     span reads.  Every stack is created fresh, filled through the device
@@ -170,154 +170,158 @@ def secondary(L, last_error, torch, np, stream, reps=20):
 
     res = {}
 
-    # C1
-    rng = np.random.default_rng(42)
-    k = rng.standard_normal((2048, 4, 64), dtype=np.float32)
-    v = rng.standard_normal((2048, 4, 64), dtype=np.float32)
-    q = rng.standard_normal((4, 64), dtype=np.float32)
-    kd, vd = (torch.from_numpy(np.ascontiguousarray(x.transpose(1, 0, 2))).to(dev) for x in (k, v))
-    qd, od = torch.from_numpy(q).to(dev), torch.empty(4, 64, device=dev)
-    c1 = {}
-    for name, vm, hyb in (("dense", 0.0, 0), ("engine_defaults_sparse_v", 0.95, 512)):
-        ms = stack([(4, 64, 4, 2, 2048, 42, vm, hyb)])
-        ok(L.adaptq_mha_append_all_device(ms[0], dp(kd), dp(vd), 2048, 0, sp))
-        us = span(lambda: ok(L.adaptq_mha_compute_all_device(ms[0], dp(qd), dp(od), sp)))
-        c1[name] = rate(us, 4 * 2048 * decode_bytes_per_token(64, 4, 2))
-        free(ms)
-    res["C1"] = c1
+    if "C1" in which:
+        # C1
+        rng = np.random.default_rng(42)
+        k = rng.standard_normal((2048, 4, 64), dtype=np.float32)
+        v = rng.standard_normal((2048, 4, 64), dtype=np.float32)
+        q = rng.standard_normal((4, 64), dtype=np.float32)
+        kd, vd = (torch.from_numpy(np.ascontiguousarray(x.transpose(1, 0, 2))).to(dev) for x in (k, v))
+        qd, od = torch.from_numpy(q).to(dev), torch.empty(4, 64, device=dev)
+        c1 = {}
+        for name, vm, hyb in (("dense", 0.0, 0), ("engine_defaults_sparse_v", 0.95, 512)):
+            ms = stack([(4, 64, 4, 2, 2048, 42, vm, hyb)])
+            ok(L.adaptq_mha_append_all_device(ms[0], dp(kd), dp(vd), 2048, 0, sp))
+            us = span(lambda: ok(L.adaptq_mha_compute_all_device(ms[0], dp(qd), dp(od), sp)))
+            c1[name] = rate(us, 4 * 2048 * decode_bytes_per_token(64, 4, 2))
+            free(ms)
+        res["C1"] = c1
 
-    # C2
-    nl, nh, n = 24, 14, 512
-    rng = np.random.default_rng(42)
-    kv = rng.standard_normal((2, nl, nh, n, 64), dtype=np.float32)
-    q = rng.standard_normal((nl, nh, 64), dtype=np.float32)
-    for x in (kv, q):
-        x[..., [3, 17]] *= 20.0
-    kvd, qd = torch.from_numpy(kv).to(dev), torch.from_numpy(q).to(dev)
-    od = torch.empty(nl, nh, 64, device=dev)
-    packed_bytes = nh * n * (decode_bytes_per_token(64, 16, 2)
-                             + (nl - 1) * decode_bytes_per_token(64, 4, 2))
-    c2 = {}
-    for name, vm, hyb in (("packed", 0.0, 0), ("hybrid_fp32", 0.95, 512)):
-        ms = stack([(nh, 64, 16 if l == 0 else 4, 2, n, 42 ^ l, vm, hyb) for l in range(nl)])
-        for l, m in enumerate(ms):
-            ok(L.adaptq_mha_append_all_device(m, dp(kvd[0, l]), dp(kvd[1, l]), n, 0, sp))
-
-        def step():
+    if "C2" in which:
+        # C2
+        nl, nh, n = 24, 14, 512
+        rng = np.random.default_rng(42)
+        kv = rng.standard_normal((2, nl, nh, n, 64), dtype=np.float32)
+        q = rng.standard_normal((nl, nh, 64), dtype=np.float32)
+        for x in (kv, q):
+            x[..., [3, 17]] *= 20.0
+        kvd, qd = torch.from_numpy(kv).to(dev), torch.from_numpy(q).to(dev)
+        od = torch.empty(nl, nh, 64, device=dev)
+        packed_bytes = nh * n * (decode_bytes_per_token(64, 16, 2)
+                                 + (nl - 1) * decode_bytes_per_token(64, 4, 2))
+        c2 = {}
+        for name, vm, hyb in (("packed", 0.0, 0), ("hybrid_fp32", 0.95, 512)):
+            ms = stack([(nh, 64, 16 if l == 0 else 4, 2, n, 42 ^ l, vm, hyb) for l in range(nl)])
             for l, m in enumerate(ms):
-                ok(L.adaptq_mha_compute_all_device(m, dp(qd[l]), dp(od[l]), sp))
-        us = span(step)
-        c2[name] = rate(us, packed_bytes if hyb == 0 else nl * nh * n * 2 * 64 * 4)
-        if hyb == 0:
+                ok(L.adaptq_mha_append_all_device(m, dp(kvd[0, l]), dp(kvd[1, l]), n, 0, sp))
+
+            def step():
+                for l, m in enumerate(ms):
+                    ok(L.adaptq_mha_compute_all_device(m, dp(qd[l]), dp(od[l]), sp))
+            us = span(step)
+            c2[name] = rate(us, packed_bytes if hyb == 0 else nl * nh * n * 2 * 64 * 4)
+            if hyb == 0:
+                ctx = [L.adaptq_mha_head(m, h) for m in ms for h in range(nh)]
+                plans = [L.adaptq_plan_create((C.c_void_p * nh)(*ctx[:nh]), nh),
+                         L.adaptq_plan_create((C.c_void_p * (len(ctx) - nh))(*ctx[nh:]), len(ctx) - nh)]
+                if not all(plans):
+                    raise RuntimeError(last_error())
+
+                def step_plans():
+                    ok(L.adaptq_plan_compute_device(plans[0], dp(qd[0]), dp(od[0]), sp))
+                    ok(L.adaptq_plan_compute_device(plans[1], dp(qd[1:]), dp(od[1:]), sp))
+                c2["packed_two_plans"] = rate(span(step_plans), packed_bytes)
+                for p in plans:
+                    L.adaptq_plan_destroy(p)
+            free(ms)
+        res["C2"] = c2
+        del kvd
+
+    if "C3" in which:
+        # C3
+        nl, nh, n0, steps = 22, 4, 1024, 256
+        rng = np.random.default_rng(3)
+        t4 = lambda *shape: (rng.standard_t(4, size=shape) / np.sqrt(2.0)).astype(np.float32)
+        bulk = torch.from_numpy(t4(2, nl, nh, n0, 64)).to(dev)
+        per = torch.from_numpy(t4(3, steps, nl, nh, 64)).to(dev)  # k, v, q per step
+        od = torch.empty(nl, nh, 64, device=dev)
+        step_bytes = sum(nh * (n0 + s + 1) * (decode_bytes_per_token(64, 16, 2)
+                                             + (nl - 1) * decode_bytes_per_token(64, 3, 2))
+                         for s in range(steps))
+        c3 = {}
+        for name, vm, hyb in (("dense", 0.0, 0), ("engine_defaults_sparse_v", 0.95, 512)):
+            ms = stack([(nh, 64, 16 if l == 0 else 3, 2, 1280, l, vm, hyb) for l in range(nl)])
+
+            def bulk_append():
+                for l, m in enumerate(ms):
+                    ok(L.adaptq_mha_append_all_device(m, dp(bulk[0, l]), dp(bulk[1, l]), n0, 0, sp))
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            bulk_append()
+            b.record(stream)
+            torch.cuda.synchronize()
+            append_us = a.elapsed_time(b) * 1e3
+            a.record(stream)
+            t0 = time.perf_counter()
+            for s in range(steps):
+                for l, m in enumerate(ms):
+                    ok(L.adaptq_mha_append_all_device(m, dp(per[0, s, l]), dp(per[1, s, l]), 1,
+                                                      n0 + s, sp))
+                    ok(L.adaptq_mha_compute_all_device(m, dp(per[2, s, l]), dp(od[l]), sp))
+            b.record(stream)
+            torch.cuda.synchronize()
+            wall = (time.perf_counter() - t0) * 1e6
+            c3[name] = {"us_per_step": wall / steps, "gpu_us_per_step": a.elapsed_time(b) * 1e3 / steps,
+                        "bulk_append_us": append_us, "decode_bytes_256_steps": step_bytes,
+                        "calls_per_step": 2 * nl}
+            free(ms)
+
+            # the same steps through two plans (layer 0, layers 1-21): one append
+            # call and one decode call per plan and step
+            ms = stack([(nh, 64, 16 if l == 0 else 3, 2, 1280, l, vm, hyb) for l in range(nl)])
+            bulk_append()
             ctx = [L.adaptq_mha_head(m, h) for m in ms for h in range(nh)]
             plans = [L.adaptq_plan_create((C.c_void_p * nh)(*ctx[:nh]), nh),
                      L.adaptq_plan_create((C.c_void_p * (len(ctx) - nh))(*ctx[nh:]), len(ctx) - nh)]
             if not all(plans):
                 raise RuntimeError(last_error())
+            torch.cuda.synchronize()
+            a.record(stream)
+            t0 = time.perf_counter()
+            for s in range(steps):
+                for pl, lo, hi in ((plans[0], 0, 1), (plans[1], 1, nl)):
+                    ok(L.adaptq_plan_append_device(pl, dp(per[0, s, lo:hi]), dp(per[1, s, lo:hi]), 1,
+                                                   n0 + s, sp))
+                    ok(L.adaptq_plan_compute_device(pl, dp(per[2, s, lo:hi]), dp(od[lo:hi]), sp))
+            b.record(stream)
+            torch.cuda.synchronize()
+            wall = (time.perf_counter() - t0) * 1e6
+            c3[name + "_plans"] = {"us_per_step": wall / steps,
+                                   "gpu_us_per_step": a.elapsed_time(b) * 1e3 / steps,
+                                   "calls_per_step": 4}
+            for pl in plans:
+                L.adaptq_plan_destroy(pl)
+            free(ms)
+        res["C3"] = c3
+        del bulk, per
 
-            def step_plans():
-                ok(L.adaptq_plan_compute_device(plans[0], dp(qd[0]), dp(od[0]), sp))
-                ok(L.adaptq_plan_compute_device(plans[1], dp(qd[1:]), dp(od[1:]), sp))
-            c2["packed_two_plans"] = rate(span(step_plans), packed_bytes)
-            for p in plans:
-                L.adaptq_plan_destroy(p)
-        free(ms)
-    res["C2"] = c2
-    del kvd
-
-    # C3
-    nl, nh, n0, steps = 22, 4, 1024, 256
-    rng = np.random.default_rng(3)
-    t4 = lambda *shape: (rng.standard_t(4, size=shape) / np.sqrt(2.0)).astype(np.float32)
-    bulk = torch.from_numpy(t4(2, nl, nh, n0, 64)).to(dev)
-    per = torch.from_numpy(t4(3, steps, nl, nh, 64)).to(dev)  # k, v, q per step
-    od = torch.empty(nl, nh, 64, device=dev)
-    step_bytes = sum(nh * (n0 + s + 1) * (decode_bytes_per_token(64, 16, 2)
-                                         + (nl - 1) * decode_bytes_per_token(64, 3, 2))
-                     for s in range(steps))
-    c3 = {}
-    for name, vm, hyb in (("dense", 0.0, 0), ("engine_defaults_sparse_v", 0.95, 512)):
-        ms = stack([(nh, 64, 16 if l == 0 else 3, 2, 1280, l, vm, hyb) for l in range(nl)])
-
-        def bulk_append():
-            for l, m in enumerate(ms):
-                ok(L.adaptq_mha_append_all_device(m, dp(bulk[0, l]), dp(bulk[1, l]), n0, 0, sp))
+    if "C4" in which:
+        # C4
+        g = torch.Generator(device=dev)
+        g.manual_seed(7)
+        nh, cap, ntok, nq = 8, 32768, 40000, 64
+        kd = torch.randn(nh, ntok, 128, generator=g, device=dev)
+        vd = torch.randn(nh, ntok, 128, generator=g, device=dev)
+        qd = torch.randn(nq, nh, 128, generator=g, device=dev)
+        od = torch.empty_like(qd)
+        ms = stack([(nh, 128, 4, 4, cap, 7, 0.0, 0)])
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record(stream)
-        bulk_append()
+        ok(L.adaptq_mha_append_all_device(ms[0], dp(kd), dp(vd), ntok, 0, sp))
         b.record(stream)
         torch.cuda.synchronize()
-        append_us = a.elapsed_time(b) * 1e3
-        a.record(stream)
-        t0 = time.perf_counter()
-        for s in range(steps):
-            for l, m in enumerate(ms):
-                ok(L.adaptq_mha_append_all_device(m, dp(per[0, s, l]), dp(per[1, s, l]), 1,
-                                                  n0 + s, sp))
-                ok(L.adaptq_mha_compute_all_device(m, dp(per[2, s, l]), dp(od[l]), sp))
-        b.record(stream)
-        torch.cuda.synchronize()
-        wall = (time.perf_counter() - t0) * 1e6
-        c3[name] = {"us_per_step": wall / steps, "gpu_us_per_step": a.elapsed_time(b) * 1e3 / steps,
-                    "bulk_append_us": append_us, "decode_bytes_256_steps": step_bytes,
-                    "calls_per_step": 2 * nl}
+        app_us = a.elapsed_time(b) * 1e3
+        per_query = nh * cap * decode_bytes_per_token(128, 4, 4)
+        row = 128 * 4
+        us = span(lambda: ok(L.adaptq_ggml_attn_f32_device(ms[0], dp(qd), 128, nh, nq, row, nh * row,
+                                                           dp(od), row, nh * row, sp)))
+        us1 = span(lambda: ok(L.adaptq_mha_compute_all_device(ms[0], dp(qd[0]), dp(od[0]), sp)))
+        res["C4"] = {
+            "append_40000": rate(app_us, nh * ntok * append_bytes_per_token(128, 128, 4, 4)),
+            "queries_64_one_launch": dict(rate(us, nq * per_query), per_query_bytes=per_query),
+            "query_1": rate(us1, per_query),
+        }
         free(ms)
-
-        # the same steps through two plans (layer 0, layers 1-21): one append
-        # call and one decode call per plan and step
-        ms = stack([(nh, 64, 16 if l == 0 else 3, 2, 1280, l, vm, hyb) for l in range(nl)])
-        bulk_append()
-        ctx = [L.adaptq_mha_head(m, h) for m in ms for h in range(nh)]
-        plans = [L.adaptq_plan_create((C.c_void_p * nh)(*ctx[:nh]), nh),
-                 L.adaptq_plan_create((C.c_void_p * (len(ctx) - nh))(*ctx[nh:]), len(ctx) - nh)]
-        if not all(plans):
-            raise RuntimeError(last_error())
-        torch.cuda.synchronize()
-        a.record(stream)
-        t0 = time.perf_counter()
-        for s in range(steps):
-            for pl, lo, hi in ((plans[0], 0, 1), (plans[1], 1, nl)):
-                ok(L.adaptq_plan_append_device(pl, dp(per[0, s, lo:hi]), dp(per[1, s, lo:hi]), 1,
-                                               n0 + s, sp))
-                ok(L.adaptq_plan_compute_device(pl, dp(per[2, s, lo:hi]), dp(od[lo:hi]), sp))
-        b.record(stream)
-        torch.cuda.synchronize()
-        wall = (time.perf_counter() - t0) * 1e6
-        c3[name + "_plans"] = {"us_per_step": wall / steps,
-                               "gpu_us_per_step": a.elapsed_time(b) * 1e3 / steps,
-                               "calls_per_step": 4}
-        for pl in plans:
-            L.adaptq_plan_destroy(pl)
-        free(ms)
-    res["C3"] = c3
-    del bulk, per
-
-    # C4
-    g = torch.Generator(device=dev)
-    g.manual_seed(7)
-    nh, cap, ntok, nq = 8, 32768, 40000, 64
-    kd = torch.randn(nh, ntok, 128, generator=g, device=dev)
-    vd = torch.randn(nh, ntok, 128, generator=g, device=dev)
-    qd = torch.randn(nq, nh, 128, generator=g, device=dev)
-    od = torch.empty_like(qd)
-    ms = stack([(nh, 128, 4, 4, cap, 7, 0.0, 0)])
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record(stream)
-    ok(L.adaptq_mha_append_all_device(ms[0], dp(kd), dp(vd), ntok, 0, sp))
-    b.record(stream)
-    torch.cuda.synchronize()
-    app_us = a.elapsed_time(b) * 1e3
-    per_query = nh * cap * decode_bytes_per_token(128, 4, 4)
-    row = 128 * 4
-    us = span(lambda: ok(L.adaptq_ggml_attn_f32_device(ms[0], dp(qd), 128, nh, nq, row, nh * row,
-                                                       dp(od), row, nh * row, sp)))
-    us1 = span(lambda: ok(L.adaptq_mha_compute_all_device(ms[0], dp(qd[0]), dp(od[0]), sp)))
-    res["C4"] = {
-        "append_40000": rate(app_us, nh * ntok * append_bytes_per_token(128, 128, 4, 4)),
-        "queries_64_one_launch": dict(rate(us, nq * per_query), per_query_bytes=per_query),
-        "query_1": rate(us1, per_query),
-    }
-    free(ms)
     res["note"] = ("medians of %d HIP-event spans in us; bytes = algorithmic bytes read by "
                    "the span (C4 queries: 64 x the one-query bytes, so gb_per_s above the "
                    "HBM peak means K/V reuse through the caches)" % reps)
@@ -345,6 +349,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the timings of BASELINE configs[0..3]")
+    ap.add_argument("--only", default="",
+                    help="comma-separated BASELINE configs 1-4 (e.g. C1,C3): run only those "
+                         "secondary timings and print them (profiling runs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy 5 times (scales rocprof "
                          "FETCH_SIZE/WRITE_SIZE readings to bytes)")
@@ -371,6 +378,15 @@ def main():
     from adaptq_amd import _lib
     L = _lib.lib
     import ctypes as C
+
+    if args.only:
+        which = tuple(x.strip().upper() for x in args.only.split(",") if x.strip())
+        bad = [w for w in which if w not in ("C1", "C2", "C3", "C4")]
+        if bad:
+            sys.exit(f"--only: unknown config {bad}; choose from C1,C2,C3,C4")
+        res = secondary(L, _lib.last_error, torch, np, torch.cuda.current_stream(), which=which)
+        print(json.dumps({"secondary_only": res}))
+        return
 
     cfg = CFG5
     dim, n, kb, vb = cfg["dim"], cfg["ctx"], cfg["k_bits"], cfg["v_bits"]
