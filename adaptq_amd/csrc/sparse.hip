@@ -112,14 +112,32 @@ __device__ void rotate_query_exact(float *s_q, const float *q, int dim, int P,
 
 // dot(s_q, CB[codes of row]) with the reference's 8 FMA lanes (lane L takes
 // codes L, L+8, ...) summed pairwise (attention.cpp:83-136).
-// PT = 0: any padded size, codes read byte by byte.  PT = 64/128 with 2/4-bit
-// codes: the row is read as words; reference word w sits at stored word
-// w ^ (x >> 2) with its bytes permuted by b ^ (x & 3) (kperm_mask), and one
-// v_perm per word restores the reference byte order.
+// PT = 0: any padded size, codes read byte by byte.  PT = 64/128: the row is
+// read as words; 3-bit rows are in reference order; for 2/4-bit codes
+// reference word w sits at stored word w ^ (x >> 2) with its bytes permuted by
+// b ^ (x & 3) (kperm_mask), and one v_perm per word restores the reference
+// byte order.
 template <int PT, int KB>
 __device__ __forceinline__ float kdot_row(const uint8_t *row, int x, const float *s_q, int P) {
   float s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  if constexpr (PT != 0 && (KB == 2 || KB == 4)) {
+  if constexpr (PT != 0 && KB == 3) {
+    // 3-bit rows are unpermuted: 24-bit big-endian groups of 8 codes
+    constexpr int W = PT * 3 / 32;
+    const uint32_t *r32 = reinterpret_cast<const uint32_t *>(row);
+    uint32_t w[W];
+#pragma unroll
+    for (int i = 0; i < W; ++i) w[i] = r32[i];
+#pragma unroll
+    for (int g = 0; g < PT / 8; ++g) {
+      const int b0 = 3 * g;
+      const uint32_t w24 = (((w[b0 >> 2] >> (8 * (b0 & 3))) & 255u) << 16) |
+                           (((w[(b0 + 1) >> 2] >> (8 * ((b0 + 1) & 3))) & 255u) << 8) |
+                           ((w[(b0 + 2) >> 2] >> (8 * ((b0 + 2) & 3))) & 255u);
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        s[k] = fmaf(cbv<KB>((int)((w24 >> (21 - 3 * k)) & 7u)), s_q[8 * g + k], s[k]);
+    }
+  } else if constexpr (PT != 0 && (KB == 2 || KB == 4)) {
     constexpr int W = PT * KB / 32;
     const uint32_t *r32 = reinterpret_cast<const uint32_t *>(row);
     const uint32_t xw = (uint32_t)x >> 2;
@@ -775,7 +793,11 @@ hipError_t launch_decode_sparse(HeadDesc *const *descs, int n_items, const Decod
       else if (sh.padded == 128) AQ_LOGITS(128, 2);
       else AQ_LOGITS(0, 2);
       break;
-    case 3: AQ_LOGITS(0, 3); break;
+    case 3:
+      if (sh.padded == 64) AQ_LOGITS(64, 3);
+      else if (sh.padded == 128) AQ_LOGITS(128, 3);
+      else AQ_LOGITS(0, 3);
+      break;
     case 4:
       if (sh.padded == 64) AQ_LOGITS(64, 4);
       else if (sh.padded == 128) AQ_LOGITS(128, 4);

@@ -121,8 +121,9 @@ def secondary(L, last_error, torch, np, stream, reps=20, which=("C1", "C2", "C3"
           the sparse-V branch at n = 2048).
       C2: 24 layers x 14 heads d64, n = 512 (layer 0 K16/V2, others K4/V2,
           channels 3 and 17 x20): one decode step over all layers, packed
-          (hybrid 0; one launch per layer, and two plans) and hybrid FP32
-          (Engine defaults: every layer takes the raw-mirror branch).
+          (hybrid 0) and hybrid FP32 (Engine defaults: every layer takes the
+          raw-mirror branch), each with one call per layer and through two
+          plans (layer 0, layers 1-23).
       C3: 22 layers x 4 heads d64 (layer 0 K16/V2, others K3/V2), Student-t(4)
           / sqrt 2: 1024-token bulk append, then 256 steps of (append 1 +
           decode) for every layer; µs per step, host wall clock included;
@@ -209,20 +210,21 @@ def secondary(L, last_error, torch, np, stream, reps=20, which=("C1", "C2", "C3"
                 for l, m in enumerate(ms):
                     ok(L.adaptq_mha_compute_all_device(m, dp(qd[l]), dp(od[l]), sp))
             us = span(step)
-            c2[name] = rate(us, packed_bytes if hyb == 0 else nl * nh * n * 2 * 64 * 4)
-            if hyb == 0:
-                ctx = [L.adaptq_mha_head(m, h) for m in ms for h in range(nh)]
-                plans = [L.adaptq_plan_create((C.c_void_p * nh)(*ctx[:nh]), nh),
-                         L.adaptq_plan_create((C.c_void_p * (len(ctx) - nh))(*ctx[nh:]), len(ctx) - nh)]
-                if not all(plans):
-                    raise RuntimeError(last_error())
+            nbytes = packed_bytes if hyb == 0 else nl * nh * n * 2 * 64 * 4
+            c2[name] = rate(us, nbytes)
+            # the same step through two plans (layer 0, layers 1-23)
+            ctx = [L.adaptq_mha_head(m, h) for m in ms for h in range(nh)]
+            plans = [L.adaptq_plan_create((C.c_void_p * nh)(*ctx[:nh]), nh),
+                     L.adaptq_plan_create((C.c_void_p * (len(ctx) - nh))(*ctx[nh:]), len(ctx) - nh)]
+            if not all(plans):
+                raise RuntimeError(last_error())
 
-                def step_plans():
-                    ok(L.adaptq_plan_compute_device(plans[0], dp(qd[0]), dp(od[0]), sp))
-                    ok(L.adaptq_plan_compute_device(plans[1], dp(qd[1:]), dp(od[1:]), sp))
-                c2["packed_two_plans"] = rate(span(step_plans), packed_bytes)
-                for p in plans:
-                    L.adaptq_plan_destroy(p)
+            def step_plans():
+                ok(L.adaptq_plan_compute_device(plans[0], dp(qd[0]), dp(od[0]), sp))
+                ok(L.adaptq_plan_compute_device(plans[1], dp(qd[1:]), dp(od[1:]), sp))
+            c2[name + "_two_plans"] = rate(span(step_plans), nbytes)
+            for p in plans:
+                L.adaptq_plan_destroy(p)
             free(ms)
         res["C2"] = c2
         del kvd
