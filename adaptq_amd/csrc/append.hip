@@ -51,14 +51,38 @@ __device__ __forceinline__ void store_row(uint8_t *dst, const uint32_t (&w)[(NB 
 
 // Store a K row with its bytes in the slot's XOR order (kperm_mask): word i,
 // bytes permuted within the word by x & 3, goes to word position i ^ (x >> 2).
+// The words are put in stored order in registers (a conditional swap per bit
+// of x >> 2), so the row leaves as whole 16-byte stores.
 template <int NB>
 __device__ __forceinline__ void store_row_perm(uint8_t *dst, const uint32_t (&w)[NB / 4], int slot,
                                                uint32_t x) {
-  uint32_t *p = reinterpret_cast<uint32_t *>(dst + (size_t)slot * NB);
+  constexpr int NW = NB / 4;
   const uint32_t sel = 0x03020100u ^ ((x & 3u) * 0x01010101u);
   const uint32_t xw = x >> 2;
+  uint32_t o[NW];
 #pragma unroll
-  for (int i = 0; i < NB / 4; ++i) p[i ^ xw] = __builtin_amdgcn_perm(0u, w[i], sel);
+  for (int i = 0; i < NW; ++i) o[i] = __builtin_amdgcn_perm(0u, w[i], sel);
+  // o[i] <- o[i ^ xw]: one conditional swap level per bit of xw
+#pragma unroll
+  for (int b = 0; (1 << b) < NW; ++b) {
+    const bool f = (xw >> b) & 1u;
+#pragma unroll
+    for (int i = 0; i < NW; ++i)
+      if ((i & (1 << b)) == 0) {
+        const uint32_t a = o[i], c = o[i | (1 << b)];
+        o[i] = f ? c : a;
+        o[i | (1 << b)] = f ? a : c;
+      }
+  }
+  if constexpr (NB % 16 == 0) {
+    uint4 *p = reinterpret_cast<uint4 *>(dst + (size_t)slot * NB);
+#pragma unroll
+    for (int i = 0; i < NB / 16; ++i) p[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+  } else {
+    uint32_t *p = reinterpret_cast<uint32_t *>(dst + (size_t)slot * NB);
+#pragma unroll
+    for (int i = 0; i < NW; ++i) p[i] = o[i];
+  }
 }
 
 template <int P, int B>
