@@ -1169,14 +1169,37 @@ size_t decode_workspace_floats(int n_items, const DecodeShape &sh) {
   return (size_t)n_items * sp.splits * (sh.padded + 4);
 }
 
+// Items per launch: the grid's y dimension holds items (at most 65,535).
+constexpr int kMaxItemsPerLaunch = 65535;
+
+hipError_t launch_decode_items(HeadDesc *const *descs, int n_items, const DecodeShape &sh,
+                               const SplitPlan &sp, const float *d_q, float *d_out, float *d_ws,
+                               hipStream_t s);
+
 hipError_t launch_decode(HeadDesc *const *descs, int n_items, const DecodeShape &shape,
                          const float *d_q, float *d_out, float *d_ws, hipStream_t s) {
   if (n_items <= 0) return hipSuccess;
   DecodeShape sh = shape;
   if (sh.raw) sh.k_bits = sh.v_bits = 16;  // the mirror holds fp32 keys and values
+  const SplitPlan sp = decode_plan(n_items, sh);
+  // one split plan for all items; chunks of items take consecutive
+  // queries, outputs and workspace
+  for (int c0 = 0; c0 < n_items; c0 += kMaxItemsPerLaunch) {
+    const int cnt = n_items - c0 < kMaxItemsPerLaunch ? n_items - c0 : kMaxItemsPerLaunch;
+    const hipError_t e =
+        launch_decode_items(descs + c0, cnt, sh, sp, d_q + (size_t)c0 * sh.dim,
+                            d_out + (size_t)c0 * sh.dim,
+                            d_ws + (size_t)c0 * sp.splits * (sh.padded + 4), s);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+hipError_t launch_decode_items(HeadDesc *const *descs, int n_items, const DecodeShape &sh,
+                               const SplitPlan &sp, const float *d_q, float *d_out, float *d_ws,
+                               hipStream_t s) {
   const bool raw = sh.raw;
   const bool lut_ok = lut_eligible(sh);
-  const SplitPlan sp = decode_plan(n_items, sh);
   const dim3 grid(sp.splits, n_items);
   hipError_t e;
   if (lut_ok) {

@@ -784,46 +784,59 @@ hipError_t launch_decode_sparse(HeadDesc *const *descs, int n_items, const Decod
   const int sort_cap = keys_at(n);
   const float sp = sqrtf((float)sh.padded);
   const float isp = 1.0f / sp;
-  const dim3 g1((n + kThreads - 1) / kThreads, n_items);
-#define AQ_LOGITS(PT, KB_) \
-  sparse_logits_kernel<PT, KB_><<<g1, kThreads, 0, s>>>(descs, d_q, n, isp, sp, ws, stride)
-  switch (sh.k_bits) {
-    case 2:
-      if (sh.padded == 64) AQ_LOGITS(64, 2);
-      else if (sh.padded == 128) AQ_LOGITS(128, 2);
-      else AQ_LOGITS(0, 2);
-      break;
-    case 3:
-      if (sh.padded == 64) AQ_LOGITS(64, 3);
-      else if (sh.padded == 128) AQ_LOGITS(128, 3);
-      else AQ_LOGITS(0, 3);
-      break;
-    case 4:
-      if (sh.padded == 64) AQ_LOGITS(64, 4);
-      else if (sh.padded == 128) AQ_LOGITS(128, 4);
-      else AQ_LOGITS(0, 4);
-      break;
-    default: return hipErrorInvalidValue;
-  }
-#undef AQ_LOGITS
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  sparse_select_kernel<<<n_items, kSelThreads, 0, s>>>(descs, v_mass, ws, stride, sort_cap);
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
   const int splits = vsum_splits(n);
-  float *parts = ws + (size_t)n_items * stride;
-  const dim3 g3(splits, n_items);
-  switch (sh.v_bits) {
-    case 2: sparse_vsum_kernel<2><<<g3, kThreads, 0, s>>>(descs, ws, stride, kVChunk, splits, parts); break;
-    case 3: sparse_vsum_kernel<3><<<g3, kThreads, 0, s>>>(descs, ws, stride, kVChunk, splits, parts); break;
-    case 4: sparse_vsum_kernel<4><<<g3, kThreads, 0, s>>>(descs, ws, stride, kVChunk, splits, parts); break;
-    default: return hipErrorInvalidValue;
+  float *parts_all = ws + (size_t)n_items * stride;
+  // items go in the grid's y dimension (at most 65,535 per launch); chunks of
+  // items take consecutive queries, outputs and workspace
+  constexpr int kMaxItems = 65535;
+  for (int c0 = 0; c0 < n_items; c0 += kMaxItems) {
+    const int cnt = n_items - c0 < kMaxItems ? n_items - c0 : kMaxItems;
+    HeadDesc *const *dsc = descs + c0;
+    const float *q = d_q + (size_t)c0 * sh.dim;
+    float *out = d_out + (size_t)c0 * sh.dim;
+    float *w = ws + (size_t)c0 * stride;
+    float *parts = parts_all + (size_t)c0 * splits * sh.padded;
+    const dim3 g1((n + kThreads - 1) / kThreads, cnt);
+#define AQ_LOGITS(PT, KB_) \
+  sparse_logits_kernel<PT, KB_><<<g1, kThreads, 0, s>>>(dsc, q, n, isp, sp, w, stride)
+    switch (sh.k_bits) {
+      case 2:
+        if (sh.padded == 64) AQ_LOGITS(64, 2);
+        else if (sh.padded == 128) AQ_LOGITS(128, 2);
+        else AQ_LOGITS(0, 2);
+        break;
+      case 3:
+        if (sh.padded == 64) AQ_LOGITS(64, 3);
+        else if (sh.padded == 128) AQ_LOGITS(128, 3);
+        else AQ_LOGITS(0, 3);
+        break;
+      case 4:
+        if (sh.padded == 64) AQ_LOGITS(64, 4);
+        else if (sh.padded == 128) AQ_LOGITS(128, 4);
+        else AQ_LOGITS(0, 4);
+        break;
+      default: return hipErrorInvalidValue;
+    }
+#undef AQ_LOGITS
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    sparse_select_kernel<<<cnt, kSelThreads, 0, s>>>(dsc, v_mass, w, stride, sort_cap);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const dim3 g3(splits, cnt);
+    switch (sh.v_bits) {
+      case 2: sparse_vsum_kernel<2><<<g3, kThreads, 0, s>>>(dsc, w, stride, kVChunk, splits, parts); break;
+      case 3: sparse_vsum_kernel<3><<<g3, kThreads, 0, s>>>(dsc, w, stride, kVChunk, splits, parts); break;
+      case 4: sparse_vsum_kernel<4><<<g3, kThreads, 0, s>>>(dsc, w, stride, kVChunk, splits, parts); break;
+      default: return hipErrorInvalidValue;
+    }
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    sparse_finish_kernel<<<cnt, kThreads, 0, s>>>(dsc, kVChunk, splits, parts, out);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
   }
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  sparse_finish_kernel<<<n_items, kThreads, 0, s>>>(descs, kVChunk, splits, parts, d_out);
-  return hipGetLastError();
+  return hipSuccess;
 }
 
 }  // namespace aq

@@ -131,3 +131,42 @@ def test_plan_rejects_mixed_branches():
     assert L.adaptq_plan_compute_device(plan, dq.ptr, do.ptr, None) == -1
     assert "different branches" in err()
     L.adaptq_plan_destroy(plan)
+
+
+# More contexts than one launch's grid holds (items go in the grid's y
+# dimension, at most 65,535): the decode runs in chunks of items; sampled heads
+# on both sides of the chunk boundary match the oracle.
+@pytest.mark.parametrize("vm", [0.0, 0.95])
+def test_plan_more_items_than_one_grid(oracle, vm):
+    H, dim, cap, n = 65600, 64, 8, 3
+    print(f"plan of {H} contexts, v_mass={vm}", flush=True)
+    rng = np.random.default_rng(17)
+    hs = [L.adaptq_create(dim, 4, 2, cap, i, vm, 0) for i in range(H)]
+    assert all(hs), err()
+    try:
+        plan = L.adaptq_plan_create((C.c_void_p * H)(*hs), H)
+        assert plan, err()
+        k = rng.standard_normal((H, n, dim)).astype(np.float32)
+        v = rng.standard_normal((H, n, dim)).astype(np.float32)
+        q = rng.standard_normal((H, dim)).astype(np.float32)
+        dk, dv, dq, do = (DeviceBuffer(x.nbytes) for x in (k, v, q, q))
+        dk.upload(k)
+        dv.upload(v)
+        dq.upload(q)
+        assert L.adaptq_plan_append_device(plan, dk.ptr, dv.ptr, n, 0, None) == 0, err()
+        assert L.adaptq_plan_compute_device(plan, dq.ptr, do.ptr, None) == 0, err()
+        sync()
+        y = do.download((H, dim))
+        assert np.isfinite(y).all()
+        for h in (0, 65534, 65535, 65536, H - 1):
+            o = oracle.head(dim, 4, 2, cap, h, vm, 0)
+            for t in range(n):
+                o.append(k[h, t], v[h, t], t)
+            g = GpuHead.wrap(hs[h], dim)
+            for a, b in zip(g.read_slots(0, n), o.read_slots(0, n)):
+                assert same_bits(a, b), h
+            assert rel_err(y[h], o.compute(q[h])[0]) <= 1e-4, h
+        L.adaptq_plan_destroy(plan)
+    finally:
+        for x in hs:
+            L.adaptq_destroy(x)
