@@ -262,9 +262,13 @@ __device__ float serial_sum(const float *s, int m, float acc) {
 }
 
 // The reference's mass loop over quad sums q[0..m): while mass < v_mass, add
-// the next one.  mass never decreases (the sums are >= 0) and stays NaN once
-// NaN, so a predicated add over a batch takes exactly the quads the loop
-// takes.  Returns how many were taken; *mass is updated.
+// the next one.  Returns how many it takes; *mass is updated.  The sums are
+// >= 0, so the running mass never decreases (and stays NaN once NaN): the
+// number taken is the number of positions whose mass before them is still
+// below v_mass, counted beside a plain chain of adds.  Past the stop the
+// chain runs on to the end of its batch of 32, which leaves *mass at or above
+// v_mass (or NaN) as the reference's is, so the single-token loop that
+// follows runs exactly when the reference's does.
 __device__ int mass_scan(const float *q, int m, float v_mass, float *mass) {
   const float4 *q4 = reinterpret_cast<const float4 *>(q);
   float ms = *mass;
@@ -278,9 +282,8 @@ __device__ int mass_scan(const float *q, int m, float v_mass, float *mass) {
       const float e[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const bool go = ms < v_mass;
-        ms = go ? __fadd_rn(ms, e[c]) : ms;
-        taken += go ? 1 : 0;
+        taken += ms < v_mass ? 1 : 0;
+        ms = __fadd_rn(ms, e[c]);
       }
     }
   }
@@ -332,24 +335,20 @@ __device__ __forceinline__ float block_max(float m, SelectShared &sh) {
 
 // Exclusive scan of cnt[] (16 x kSelThreads 16-bit counts, digit-major) in
 // place: thread t scans entries 16t .. 16t+15, waves scan the thread totals,
-// the wave totals are added in order.
+// the wave totals are added in order.  Counts stay packed two to a word: every
+// prefix is below 2^16 (n <= kLdsSort), so adding base * 0x10001 to a word
+// carries nothing from the low half into the high one.
 __device__ __forceinline__ void scan_counts(SelectShared &sh) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   uint4 *c4 = reinterpret_cast<uint4 *>(sh.cnt) + 2 * tid;
   const uint4 a = c4[0], b = c4[1];
-  const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  uint32_t v[16];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    v[2 * i] = w[i] & 0xFFFFu;
-    v[2 * i + 1] = w[i] >> 16;
-  }
+  uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
   uint32_t run = 0;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const uint32_t t = v[i];
-    v[i] = run;
-    run += t;
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t lo = w[i] & 0xFFFFu, hi = w[i] >> 16;
+    w[i] = run | ((run + lo) << 16);
+    run += lo + hi;
   }
   uint32_t incl = run;
   for (int off = 1; off < 64; off <<= 1) {
@@ -360,11 +359,9 @@ __device__ __forceinline__ void scan_counts(SelectShared &sh) {
   __syncthreads();
   uint32_t base = incl - run;
   for (int k = 0; k < wave; ++k) base += sh.wsum[k];
-  uint32_t o[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) o[i] = (v[2 * i] + base) | ((v[2 * i + 1] + base) << 16);
-  c4[0] = make_uint4(o[0], o[1], o[2], o[3]);
-  c4[1] = make_uint4(o[4], o[5], o[6], o[7]);
+  const uint32_t b2 = base * 0x10001u;
+  c4[0] = make_uint4(w[0] + b2, w[1] + b2, w[2] + b2, w[3] + b2);
+  c4[1] = make_uint4(w[4] + b2, w[5] + b2, w[6] + b2, w[7] + b2);
   __syncthreads();
 }
 
@@ -379,7 +376,7 @@ __device__ __forceinline__ void scan_counts(SelectShared &sh) {
 //      runs the mass loop over them, then the single tokens
 //      (attention.cpp:454-472)
 //   5. per-token weights (p * vscale) * isp for the selected tokens, else 0,
-//      written over the logits at each token's index
+//      written over the logits in token order
 template <int E>
 __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, float *lg, int n, int s0,
                              SelectShared &sh) {
@@ -492,22 +489,30 @@ __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, fl
     int ii = 4 * mass_scan(sh.stage, n_quads, v_mass, &mass);
     for (; ii < n && mass < v_mass; ++ii) mass = __fadd_rn(mass, hi_p(sh.key[ii]));
     sh.cut = ii;
+    sh.last = ii > 0 ? ((uint64_t)sh.key[ii - 1] << 32) | sh.idx[ii - 1] : 0;
   }
   __syncthreads();
-  // sorted position r holds token idx[r] with probability hi_p(key[r]); the
-  // first cut positions are the selection
+  // The selection is the first cut keys of the sorted order, i.e. every key
+  // up to the last one taken (keys are distinct).  Each thread recomputes its
+  // own tokens' p (the logits are still in lg; expf and the product give the
+  // same bits as before) and writes their weights in token order.
   const int cut = sh.cut;
+  const uint64_t last = sh.last;
   const float isp = 1.0f / sqrtf((float)P);
-  float vs[E];
+  float lv[E], vs[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    const int r = p0 + e;
-    vs[e] = r < cut ? d->v_scale[ring_slot(s0, sh.idx[r], cap)] : 0.0f;
+    const int t = p0 + e;
+    lv[e] = t < n ? lg[t] : 0.0f;
+    vs[e] = t < n ? d->v_scale[ring_slot(s0, t, cap)] : 0.0f;
   }
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    const int r = p0 + e;
-    if (r < n) lg[sh.idx[r]] = r < cut ? __fmul_rn(__fmul_rn(hi_p(sh.key[r]), vs[e]), isp) : 0.0f;
+    const int t = p0 + e;
+    if (t < n) {
+      const float p = __fmul_rn(expf(lv[e] - mx), inv);
+      lg[t] = cut > 0 && make_key(p, t) <= last ? __fmul_rn(__fmul_rn(p, vs[e]), isp) : 0.0f;
+    }
   }
 }
 
