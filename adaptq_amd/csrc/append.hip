@@ -106,11 +106,16 @@ __device__ __forceinline__ uint32_t nan_word(int k) {
 // mixes heads: the descriptor and sign words are scalar loads and a sign flip
 // is one XOR with a scalar mask.  Otherwise lanes run over (head, token)
 // pairs in order (for few tokens per head).
+//
+// commit != 0 (the caller's guarantee: each head's tokens are all in one block,
+// i.e. UNIFORM with n_tok <= 128, or one token per head): this launch also
+// advances each head's ring state, once every thread of the head has read the
+// old one, and no commit_kernel follows.
 template <int P, int B, bool UNIFORM>
 __global__ __launch_bounds__(128) void append_kernel(HeadDesc *const *descs, int n_ctx,
                                                      int side, const float *__restrict__ src,
                                                      int n_tok, int dim, float inv_sqrt_p,
-                                                     float sqrt_p) {
+                                                     float sqrt_p, int commit) {
   // 4-bit codes: the bucket table of quantize_ss4, built before any lane leaves
   __shared__ Q4Entry s_q4[B == 4 ? kQ4Entries : 1];
   if constexpr (B == 4) {
@@ -121,7 +126,6 @@ __global__ __launch_bounds__(128) void append_kernel(HeadDesc *const *descs, int
   if constexpr (UNIFORM) {
     c = blockIdx.y;
     t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= n_tok) return;
   } else {
     const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= (long long)n_ctx * n_tok) return;
@@ -131,6 +135,17 @@ __global__ __launch_bounds__(128) void append_kernel(HeadDesc *const *descs, int
   const HeadDesc *d = descs[c];
   const RingState st = d->st;
   const int cap = d->cap;
+  if (commit) {
+    if constexpr (UNIFORM) {
+      __syncthreads();  // the block's threads all hold the old state
+      if (threadIdx.x == 0) descs[c]->st = ring_after(st, n_tok, cap, d->hyb);
+    } else {
+      descs[c]->st = ring_after(st, n_tok, cap, d->hyb);  // one token: this lane's head only
+    }
+  }
+  if constexpr (UNIFORM) {
+    if (t >= n_tok) return;
+  }
   const float *x = src + ((size_t)c * n_tok + t) * dim;
 
   // Token t survives the batch only if fewer than cap tokens follow it.
@@ -387,7 +402,7 @@ hipError_t launch_wide(HeadDesc *const *descs, int n_ctx, int side, int bits, co
 
 template <int P, bool U>
 hipError_t launch_side_as(HeadDesc *const *descs, int n_ctx, int side, int bits, const float *src,
-                          int n_tok, int dim, hipStream_t s) {
+                          int n_tok, int dim, int commit, hipStream_t s) {
   const float sp = sqrtf((float)P);
   const float isp = 1.0f / sp;
   dim3 grid;
@@ -398,22 +413,30 @@ hipError_t launch_side_as(HeadDesc *const *descs, int n_ctx, int side, int bits,
     grid = dim3((unsigned)((total + 127) / 128));
   }
   switch (bits) {
-    case 2: append_kernel<P, 2, U><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp); break;
-    case 3: append_kernel<P, 3, U><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp); break;
-    case 4: append_kernel<P, 4, U><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp); break;
-    case 16: append_kernel<P, 16, U><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp); break;
+    case 2: append_kernel<P, 2, U><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp, commit); break;
+    case 3: append_kernel<P, 3, U><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp, commit); break;
+    case 4: append_kernel<P, 4, U><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp, commit); break;
+    case 16: append_kernel<P, 16, U><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp, commit); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
 // Head-per-block launches once a head has at least a wave of tokens.
+bool head_per_block(int n_ctx, int n_tok) { return n_tok >= 64 && n_ctx <= 65535; }
+
+// The V-side launch can advance the ring states itself (see append_kernel)
+// when each head's tokens fall in one block.
+bool commit_in_kernel(int n_ctx, int n_tok) {
+  return n_tok == 1 || (head_per_block(n_ctx, n_tok) && n_tok <= 128);
+}
+
 template <int P>
 hipError_t launch_side(HeadDesc *const *descs, int n_ctx, int side, int bits, const float *src,
-                       int n_tok, int dim, hipStream_t s) {
-  if (n_tok >= 64 && n_ctx <= 65535)
-    return launch_side_as<P, true>(descs, n_ctx, side, bits, src, n_tok, dim, s);
-  return launch_side_as<P, false>(descs, n_ctx, side, bits, src, n_tok, dim, s);
+                       int n_tok, int dim, int commit, hipStream_t s) {
+  if (head_per_block(n_ctx, n_tok))
+    return launch_side_as<P, true>(descs, n_ctx, side, bits, src, n_tok, dim, commit, s);
+  return launch_side_as<P, false>(descs, n_ctx, side, bits, src, n_tok, dim, commit, s);
 }
 
 }  // namespace
@@ -423,25 +446,27 @@ hipError_t launch_append(HeadDesc *const *descs, int n_ctx, int dim, int padded,
                          hipStream_t s) {
   if (n_ctx <= 0 || n_tok <= 0) return hipSuccess;
   hipError_t e = hipSuccess;
+  const bool fold = padded <= 128 && commit_in_kernel(n_ctx, n_tok);
   for (int side = 0; side < 2 && e == hipSuccess; ++side) {
     const int bits = side == 0 ? k_bits : v_bits;
     const float *src = side == 0 ? keys : vals;
+    const int commit = fold && side == 1 ? 1 : 0;  // after the K side has read the state
     switch (padded) {
-      case 1: e = launch_side<1>(descs, n_ctx, side, bits, src, n_tok, dim, s); break;
-      case 2: e = launch_side<2>(descs, n_ctx, side, bits, src, n_tok, dim, s); break;
-      case 4: e = launch_side<4>(descs, n_ctx, side, bits, src, n_tok, dim, s); break;
-      case 8: e = launch_side<8>(descs, n_ctx, side, bits, src, n_tok, dim, s); break;
-      case 16: e = launch_side<16>(descs, n_ctx, side, bits, src, n_tok, dim, s); break;
-      case 32: e = launch_side<32>(descs, n_ctx, side, bits, src, n_tok, dim, s); break;
-      case 64: e = launch_side<64>(descs, n_ctx, side, bits, src, n_tok, dim, s); break;
-      case 128: e = launch_side<128>(descs, n_ctx, side, bits, src, n_tok, dim, s); break;
+      case 1: e = launch_side<1>(descs, n_ctx, side, bits, src, n_tok, dim, commit, s); break;
+      case 2: e = launch_side<2>(descs, n_ctx, side, bits, src, n_tok, dim, commit, s); break;
+      case 4: e = launch_side<4>(descs, n_ctx, side, bits, src, n_tok, dim, commit, s); break;
+      case 8: e = launch_side<8>(descs, n_ctx, side, bits, src, n_tok, dim, commit, s); break;
+      case 16: e = launch_side<16>(descs, n_ctx, side, bits, src, n_tok, dim, commit, s); break;
+      case 32: e = launch_side<32>(descs, n_ctx, side, bits, src, n_tok, dim, commit, s); break;
+      case 64: e = launch_side<64>(descs, n_ctx, side, bits, src, n_tok, dim, commit, s); break;
+      case 128: e = launch_side<128>(descs, n_ctx, side, bits, src, n_tok, dim, commit, s); break;
       case 256:
       case 512:
       case 1024: e = launch_wide(descs, n_ctx, side, bits, src, n_tok, dim, padded, s); break;
       default: return hipErrorInvalidValue;
     }
   }
-  if (e != hipSuccess) return e;
+  if (e != hipSuccess || fold) return e;
   commit_kernel<<<(n_ctx + 255) / 256, 256, 0, s>>>(descs, n_ctx, n_tok);
   return hipGetLastError();
 }

@@ -1073,6 +1073,16 @@ adaptq_plan_t adaptq_plan_create(const adaptq_ctx_t *ctxs, int n_ctx) {
     p->ctxs.push_back(c);
     list[i] = c->d_desc;
   }
+  {
+    // a context twice would take two slots from one ring state
+    std::vector<Ctx *> sorted(p->ctxs);
+    std::sort(sorted.begin(), sorted.end());
+    if (std::adjacent_find(sorted.begin(), sorted.end()) != sorted.end()) {
+      delete p;
+      set_error("adaptq_plan_create: a context appears more than once");
+      return nullptr;
+    }
+  }
   p->device = p->ctxs[0]->device;
   DeviceGuard g(p->device);
   if (hip_fail(p->d_list.ensure(sizeof(void *) * (size_t)n_ctx), fn) ||

@@ -235,8 +235,9 @@ int adaptq_snapshot_load(const adaptq_mha_t *layers, int n_layers, const char *p
 /* ---- Batched device-pointer path ----
  * Extension, no counterpart in the reference.  For callers whose data is
  * already in device memory (torch-ROCm tensors, serving loops) and for the
- * "all engines in one launch" decode: a plan binds n_ctx contexts that share
- * dim, k_bits, v_bits, capacity, v_mass and hybrid_thresh. */
+ * "all engines in one launch" decode: a plan binds n_ctx distinct contexts
+ * that share dim, k_bits, v_bits, capacity, v_mass and hybrid_thresh
+ * (NULL with a message otherwise). */
 typedef void *adaptq_plan_t;
 
 adaptq_plan_t adaptq_plan_create(const adaptq_ctx_t *ctxs, int n_ctx);

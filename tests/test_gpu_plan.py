@@ -170,3 +170,48 @@ def test_plan_more_items_than_one_grid(oracle, vm):
     finally:
         for x in hs:
             L.adaptq_destroy(x)
+
+
+def test_plan_rejects_duplicate_contexts():
+    a, b = GpuHead(64, 4, 2, 16, 1), GpuHead(64, 4, 2, 16, 2)
+    arr = (C.c_void_p * 3)(a.h, b.h, a.h)
+    assert not L.adaptq_plan_create(arr, 3)
+    assert "more than once" in err()
+
+
+# Single-token appends (decode steps) and 64..128-token appends advance the
+# ring state inside the V-side launch; longer ones with a separate kernel.
+# Every length keeps the ring equal to per-token host appends.
+@pytest.mark.parametrize("n_tok", [1, 2, 63, 64, 128, 129, 300])
+def test_plan_append_lengths_keep_ring_state(oracle, n_tok):
+    H, dim, cap = 5, 64, 200
+    rng = np.random.default_rng(n_tok)
+    heads = [GpuHead(dim, 4, 2, cap, 50 + i, 0.0, 96) for i in range(H)]
+    refs = [oracle.head(dim, 4, 2, cap, 50 + i, 0.0, 96) for i in range(H)]
+    plan = L.adaptq_plan_create((C.c_void_p * H)(*[h.h for h in heads]), H)
+    assert plan, err()
+    for step in range(3):
+        k = rng.standard_normal((H, n_tok, dim)).astype(np.float32)
+        v = rng.standard_normal((H, n_tok, dim)).astype(np.float32)
+        dk, dv = DeviceBuffer(k.nbytes), DeviceBuffer(v.nbytes)
+        dk.upload(k)
+        dv.upload(v)
+        assert L.adaptq_plan_append_device(plan, dk.ptr, dv.ptr, n_tok, 0, None) == 0, err()
+        sync()
+        for i in range(H):
+            for t in range(n_tok):
+                refs[i].append(k[i, t], v[i, t], t)
+    for g, o in zip(heads, refs):
+        gi, oi = g.info(), o.info()
+        assert (gi["head"], gi["size"]) == (oi["head"], oi["size"])
+        for x, y in zip(g.read_slots(0, oi["size"]), o.read_slots(0, oi["size"])):
+            assert same_bits(x, y)
+    q = rng.standard_normal((H, dim)).astype(np.float32)
+    dq, do = DeviceBuffer(q.nbytes), DeviceBuffer(q.nbytes)
+    dq.upload(q)
+    assert L.adaptq_plan_compute_device(plan, dq.ptr, do.ptr, None) == 0, err()
+    sync()
+    y = do.download((H, dim))
+    for i, o in enumerate(refs):
+        assert rel_err(y[i], o.compute(q[i])[0]) <= 1e-4
+    L.adaptq_plan_destroy(plan)
