@@ -104,7 +104,43 @@ struct DevBuf {
   }
 };
 
+// Pinned host memory that kernels read and write directly (device-visible
+// pointer dp).  Whoever reuses or frees it first waits for the kernels that
+// may still use it.
+struct PinnedBuf {
+  void *p = nullptr;
+  void *dp = nullptr;
+  size_t bytes = 0;
+  hipError_t ensure(size_t need) {
+    if (need <= bytes) return hipSuccess;
+    release();
+    const size_t want = std::max(need, (size_t)4096);
+    hipError_t e = hipHostMalloc(&p, want, hipHostMallocDefault);
+    if (e != hipSuccess) {
+      p = nullptr;
+      return e;
+    }
+    e = hipHostGetDevicePointer(&dp, p, 0);
+    if (e != hipSuccess) {
+      (void)hipHostFree(p);
+      p = dp = nullptr;
+      return e;
+    }
+    bytes = want;
+    return hipSuccess;
+  }
+  void release() {
+    if (p) (void)hipHostFree(p);
+    p = dp = nullptr;
+    bytes = 0;
+  }
+};
+
 constexpr int kStageTokens = 1024;
+// Flushes of up to this many tokens per head are read by the append kernel
+// straight from pinned host memory; larger ones go to the device in one
+// asynchronous copy first.
+constexpr int kDirectTokens = 64;
 
 struct Ctx {
   std::mutex mu;
@@ -117,7 +153,9 @@ struct Ctx {
   aq::HeadDesc **d_desc_list = nullptr;  // one entry: d_desc
   std::vector<float> stage_k, stage_v;
   int staged = 0;
-  DevBuf d_stage, d_io, d_ws, d_items;
+  DevBuf d_stage, d_ws, d_items;
+  PinnedBuf h_stage, h_io;  // staged rows for the append kernel; queries and outputs
+  bool pending = false;     // an append launch may still read h_stage
   int items_uploaded = 0;
 };
 
@@ -130,7 +168,9 @@ struct Mha {
   DevBuf d_rep;   // [reps][n_heads] the same pointers repeated (multi-query launches)
   int rep_n = 0;  // reps held in d_rep
   DevBuf d_ws, d_io, d_stage;
-  std::vector<float> pack_k, pack_v, pack_q;
+  PinnedBuf h_stage, h_io;
+  bool pending = false;  // an append launch may still read h_stage
+  std::vector<float> pack_q;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -140,11 +180,13 @@ void free_ctx(Ctx *c) {
   int cur = 0;
   (void)hipGetDevice(&cur);
   (void)hipSetDevice(c->device);
+  if (c->pending) (void)hipStreamSynchronize(lib_stream(c->device));
   if (c->slab) (void)hipFree(c->slab);
   c->d_stage.release();
-  c->d_io.release();
   c->d_ws.release();
   c->d_items.release();
+  c->h_stage.release();
+  c->h_io.release();
   (void)hipSetDevice(cur);
   delete c;
 }
@@ -272,28 +314,47 @@ struct DeviceGuard {
   }
 };
 
-// Quantise the staged tokens (caller holds c->mu).
-bool flush_locked(Ctx *c, const char *fn) {
-  if (c->staged == 0) return true;
+// Quantise the staged tokens (caller holds c->mu), on the library stream.
+// The rows go through pinned memory (the kernel reads small batches from it
+// directly) and the call does not wait for the kernel unless sync: the next
+// flush waits before it reuses the pinned rows, and compute waits at its end.
+// sync = true (inspection, snapshots, device-form calls on other streams)
+// waits for everything queued on the library stream.
+bool flush_locked(Ctx *c, const char *fn, bool sync = true) {
+  if (c->staged == 0 && !sync) return true;
   DeviceGuard g(c->device);
   hipStream_t s = lib_stream(c->device);
-  const size_t row = (size_t)c->dim * 4;
-  const size_t half = align256((size_t)c->staged * row);
-  if (hip_fail(c->d_stage.ensure(2 * half), fn)) return false;
-  float *dk = static_cast<float *>(c->d_stage.p);
-  float *dv = reinterpret_cast<float *>(static_cast<uint8_t *>(c->d_stage.p) + half);
-  hipError_t e = hipMemcpyAsync(dk, c->stage_k.data(), c->staged * row, hipMemcpyHostToDevice, s);
-  if (e == hipSuccess)
-    e = hipMemcpyAsync(dv, c->stage_v.data(), c->staged * row, hipMemcpyHostToDevice, s);
-  if (e == hipSuccess)
-    e = aq::launch_append(c->d_desc_list, 1, c->dim, c->padded, c->k_bits, c->v_bits, dk, dv,
-                          c->staged, s);
-  if (e == hipSuccess) e = hipStreamSynchronize(s);
-  if (hip_fail(e, fn)) return false;
-  c->st = aq::ring_after(c->st, c->staged, c->cap, c->hyb);
-  c->staged = 0;
-  c->stage_k.clear();
-  c->stage_v.clear();
+  if (c->staged > 0) {
+    if (c->pending) {
+      if (hip_fail(hipStreamSynchronize(s), fn)) return false;
+      c->pending = false;
+    }
+    const size_t n = (size_t)c->staged * c->dim;  // floats per side
+    if (hip_fail(c->h_stage.ensure(2 * n * 4), fn)) return false;
+    float *pk = static_cast<float *>(c->h_stage.p);
+    std::memcpy(pk, c->stage_k.data(), n * 4);
+    std::memcpy(pk + n, c->stage_v.data(), n * 4);
+    const float *dk = static_cast<const float *>(c->h_stage.dp);
+    hipError_t e = hipSuccess;
+    if (c->staged > kDirectTokens) {
+      if (hip_fail(c->d_stage.ensure(2 * n * 4), fn)) return false;
+      e = hipMemcpyAsync(c->d_stage.p, c->h_stage.p, 2 * n * 4, hipMemcpyHostToDevice, s);
+      dk = static_cast<const float *>(c->d_stage.p);
+    }
+    if (e == hipSuccess)
+      e = aq::launch_append(c->d_desc_list, 1, c->dim, c->padded, c->k_bits, c->v_bits, dk, dk + n,
+                            c->staged, s);
+    if (hip_fail(e, fn)) return false;
+    c->pending = true;
+    c->st = aq::ring_after(c->st, c->staged, c->cap, c->hyb);
+    c->staged = 0;
+    c->stage_k.clear();
+    c->stage_v.clear();
+  }
+  if (sync) {
+    if (hip_fail(hipStreamSynchronize(s), fn)) return false;
+    c->pending = false;
+  }
   return true;
 }
 
@@ -301,7 +362,7 @@ void append_locked(Ctx *c, const float *key, const float *val) {
   c->stage_k.insert(c->stage_k.end(), key, key + c->dim);
   c->stage_v.insert(c->stage_v.end(), val, val + c->dim);
   ++c->staged;
-  if (c->staged >= kStageTokens) flush_locked(c, "adaptq_append");
+  if (c->staged >= kStageTokens) flush_locked(c, "adaptq_append", false);
 }
 
 enum class Mode { Dense, Hybrid, Sparse };
@@ -314,8 +375,9 @@ Mode mode_of(const Ctx *c) {
 }
 
 // Synchronous decode of nq queries against one head (caller holds c->mu).
+// Queries and outputs pass through pinned memory the kernels read and write.
 int compute_locked(Ctx *c, const float *queries, int nq, float *outs, const char *fn) {
-  if (!flush_locked(c, fn)) return -1;
+  if (!flush_locked(c, fn, false)) return -1;
   const int n = c->st.size;
   if (n == 0) {
     std::memset(outs, 0, sizeof(float) * (size_t)nq * c->dim);
@@ -326,7 +388,7 @@ int compute_locked(Ctx *c, const float *queries, int nq, float *outs, const char
   const Mode mode = mode_of(c);
   aq::DecodeShape sh{c->dim, c->padded, c->k_bits, c->v_bits, mode == Mode::Hybrid, n};
   const size_t io = align256((size_t)nq * c->dim * 4);
-  if (hip_fail(c->d_io.ensure(2 * io), fn)) return -1;
+  if (hip_fail(c->h_io.ensure(2 * io), fn)) return -1;  // no kernel uses it between calls
   if (nq > c->items_uploaded) {
     if (hip_fail(c->d_items.ensure(sizeof(void *) * (size_t)nq), fn)) return -1;
     std::vector<aq::HeadDesc *> items((size_t)nq, c->d_desc);
@@ -337,21 +399,19 @@ int compute_locked(Ctx *c, const float *queries, int nq, float *outs, const char
   const size_t wsf = mode == Mode::Sparse ? aq::sparse_workspace_floats(nq, sh)
                                           : aq::decode_workspace_floats(nq, sh);
   if (hip_fail(c->d_ws.ensure(wsf * 4), fn)) return -1;
-  float *dq = static_cast<float *>(c->d_io.p);
-  float *dout = reinterpret_cast<float *>(static_cast<uint8_t *>(c->d_io.p) + io);
+  std::memcpy(c->h_io.p, queries, (size_t)nq * c->dim * 4);
+  const float *dq = static_cast<const float *>(c->h_io.dp);
+  float *dout = reinterpret_cast<float *>(static_cast<uint8_t *>(c->h_io.dp) + io);
   auto **items = static_cast<aq::HeadDesc **>(c->d_items.p);
-  hipError_t e = hipMemcpyAsync(dq, queries, (size_t)nq * c->dim * 4, hipMemcpyHostToDevice, s);
-  if (e == hipSuccess) {
-    if (mode == Mode::Sparse)
-      e = aq::launch_decode_sparse(items, nq, sh, c->v_mass, dq, dout,
-                                   static_cast<float *>(c->d_ws.p), s);
-    else
-      e = aq::launch_decode(items, nq, sh, dq, dout, static_cast<float *>(c->d_ws.p), s);
-  }
-  if (e == hipSuccess)
-    e = hipMemcpyAsync(outs, dout, (size_t)nq * c->dim * 4, hipMemcpyDeviceToHost, s);
+  hipError_t e =
+      mode == Mode::Sparse
+          ? aq::launch_decode_sparse(items, nq, sh, c->v_mass, dq, dout,
+                                     static_cast<float *>(c->d_ws.p), s)
+          : aq::launch_decode(items, nq, sh, dq, dout, static_cast<float *>(c->d_ws.p), s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
   if (hip_fail(e, fn)) return -1;
+  c->pending = false;
+  std::memcpy(outs, static_cast<uint8_t *>(c->h_io.p) + io, (size_t)nq * c->dim * 4);
   return n;
 }
 
@@ -365,6 +425,7 @@ void reset_locked(Ctx *c) {
   hipError_t e = aq::launch_reset_state(c->d_desc_list, 1, s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
   if (e != hipSuccess) hip_fail(e, "adaptq_reset");
+  else c->pending = false;
 }
 
 struct Plan {
@@ -385,44 +446,59 @@ struct HeadLocks {
 
 // Quantise the staged tokens of every head (caller holds all head locks).
 // When every head holds the same number of staged tokens -- the usual case,
-// one token per head per step -- they go to the device in one copy per side
-// and one append launch over all heads.
-bool flush_all_locked(Mha *m, const char *fn) {
+// one token per head per step -- they go out through one pinned buffer and one
+// append launch over all heads.  sync: as flush_locked.
+bool flush_all_locked(Mha *m, const char *fn, bool sync = true) {
   const int S = m->heads[0]->staged;
   bool uniform = S > 0;
   for (Ctx *c : m->heads) uniform = uniform && c->staged == S;
   if (!uniform) {
     for (Ctx *c : m->heads)
-      if (!flush_locked(c, fn)) return false;
+      if (c->staged > 0 && !flush_locked(c, fn, false)) return false;
+    if (sync) {
+      DeviceGuard g(m->device);
+      if (hip_fail(hipStreamSynchronize(lib_stream(m->device)), fn)) return false;
+      m->pending = false;
+      for (Ctx *c : m->heads) c->pending = false;
+    }
     return true;
   }
   const Ctx *c0 = m->heads[0];
   const int H = m->n_heads;
-  const size_t per = (size_t)S * c0->dim;
-  m->pack_k.resize(per * H);
-  m->pack_v.resize(per * H);
-  for (int h = 0; h < H; ++h) {
-    std::memcpy(m->pack_k.data() + per * h, m->heads[h]->stage_k.data(), per * 4);
-    std::memcpy(m->pack_v.data() + per * h, m->heads[h]->stage_v.data(), per * 4);
-  }
+  const size_t per = (size_t)S * c0->dim;  // floats per head and side
   DeviceGuard g(m->device);
   hipStream_t s = lib_stream(m->device);
-  const size_t half = align256(per * H * 4);
-  if (hip_fail(m->d_stage.ensure(2 * half), fn)) return false;
-  float *dk = static_cast<float *>(m->d_stage.p);
-  float *dv = reinterpret_cast<float *>(static_cast<uint8_t *>(m->d_stage.p) + half);
-  hipError_t e = hipMemcpyAsync(dk, m->pack_k.data(), per * H * 4, hipMemcpyHostToDevice, s);
-  if (e == hipSuccess) e = hipMemcpyAsync(dv, m->pack_v.data(), per * H * 4, hipMemcpyHostToDevice, s);
+  if (m->pending) {
+    if (hip_fail(hipStreamSynchronize(s), fn)) return false;
+    m->pending = false;
+  }
+  if (hip_fail(m->h_stage.ensure(2 * per * H * 4), fn)) return false;
+  float *pk = static_cast<float *>(m->h_stage.p), *pv = pk + per * H;
+  for (int h = 0; h < H; ++h) {
+    std::memcpy(pk + per * h, m->heads[h]->stage_k.data(), per * 4);
+    std::memcpy(pv + per * h, m->heads[h]->stage_v.data(), per * 4);
+  }
+  const float *dk = static_cast<const float *>(m->h_stage.dp);
+  hipError_t e = hipSuccess;
+  if (S > kDirectTokens) {
+    if (hip_fail(m->d_stage.ensure(2 * per * H * 4), fn)) return false;
+    e = hipMemcpyAsync(m->d_stage.p, m->h_stage.p, 2 * per * H * 4, hipMemcpyHostToDevice, s);
+    dk = static_cast<const float *>(m->d_stage.p);
+  }
   if (e == hipSuccess)
     e = aq::launch_append(static_cast<aq::HeadDesc **>(m->d_list.p), H, c0->dim, c0->padded,
-                          c0->k_bits, c0->v_bits, dk, dv, S, s);
-  if (e == hipSuccess) e = hipStreamSynchronize(s);
+                          c0->k_bits, c0->v_bits, dk, dk + per * H, S, s);
   if (hip_fail(e, fn)) return false;
+  m->pending = true;
   for (Ctx *c : m->heads) {
     c->st = aq::ring_after(c->st, S, c->cap, c->hyb);
     c->staged = 0;
     c->stage_k.clear();
     c->stage_v.clear();
+  }
+  if (sync) {
+    if (hip_fail(hipStreamSynchronize(s), fn)) return false;
+    m->pending = false;
   }
   return true;
 }
@@ -591,9 +667,15 @@ adaptq_mha_t adaptq_mha_create(int n_heads, int dim, int k_bits, int v_bits, int
 void adaptq_mha_destroy(adaptq_mha_t h) {
   if (!h) return;
   Mha *m = static_cast<Mha *>(h);
+  if (m->pending) {
+    DeviceGuard g(m->device);
+    (void)hipStreamSynchronize(lib_stream(m->device));
+  }
   for (Ctx *c : m->heads) free_ctx(c);
   {
     DeviceGuard g(m->device);
+    m->h_stage.release();
+    m->h_io.release();
     m->d_list.release();
     m->d_rep.release();
     m->d_ws.release();
@@ -689,7 +771,7 @@ int adaptq_mha_append_all(adaptq_mha_t h, const float *keys, const float *vals, 
     c->stage_v.insert(c->stage_v.end(), vals + (size_t)i * dim, vals + (size_t)(i + 1) * dim);
     ++c->staged;
   }
-  if (m->heads[0]->staged >= kStageTokens && !flush_all_locked(m, fn)) return -1;
+  if (m->heads[0]->staged >= kStageTokens && !flush_all_locked(m, fn, false)) return -1;
   clear_error();
   return 0;
 }
@@ -702,16 +784,16 @@ int adaptq_mha_compute_all(adaptq_mha_t h, const float *queries, float *outs) {
   Mha *m = static_cast<Mha *>(h);
   std::lock_guard<std::mutex> gm(m->mu);
   HeadLocks locks(m);
-  if (!flush_all_locked(m, fn)) return -1;
+  if (!flush_all_locked(m, fn, false)) return -1;
   const int H = m->n_heads, dim = m->heads[0]->dim;
   DeviceGuard g(m->device);
   hipStream_t s = lib_stream(m->device);
+  // queries and outputs through pinned memory the kernels read and write
   const size_t io = align256((size_t)H * dim * 4);
-  if (hip_fail(m->d_io.ensure(2 * io), fn)) return -1;
-  float *dq = static_cast<float *>(m->d_io.p);
-  float *dout = reinterpret_cast<float *>(static_cast<uint8_t *>(m->d_io.p) + io);
-  if (hip_fail(hipMemcpyAsync(dq, queries, (size_t)H * dim * 4, hipMemcpyHostToDevice, s), fn))
-    return -1;
+  if (hip_fail(m->h_io.ensure(2 * io), fn)) return -1;
+  std::memcpy(m->h_io.p, queries, (size_t)H * dim * 4);
+  const float *dq = static_cast<const float *>(m->h_io.dp);
+  float *dout = reinterpret_cast<float *>(static_cast<uint8_t *>(m->h_io.dp) + io);
   int n = launch_all_locked(m, dq, dout, s, fn);
   if (n == -2) {  // heads differ in size or branch: one head at a time
     n = 0;
@@ -721,13 +803,14 @@ int adaptq_mha_compute_all(adaptq_mha_t h, const float *queries, float *outs) {
       if (r < 0) return -1;
       if (i == 0) n = r;
     }
+    m->pending = false;  // compute_locked waited for the stream
     clear_error();
     return n;
   }
   if (n < 0) return -1;
-  hipError_t e = hipMemcpyAsync(outs, dout, (size_t)H * dim * 4, hipMemcpyDeviceToHost, s);
-  if (e == hipSuccess) e = hipStreamSynchronize(s);
-  if (hip_fail(e, fn)) return -1;
+  if (hip_fail(hipStreamSynchronize(s), fn)) return -1;
+  m->pending = false;
+  std::memcpy(outs, static_cast<uint8_t *>(m->h_io.p) + io, (size_t)H * dim * 4);
   clear_error();
   return n;
 }
@@ -1274,6 +1357,12 @@ bool read_ring(Ctx *c, std::vector<uint8_t> &kc, std::vector<uint8_t> &vc,
 // (mod cap), hybrid mirror empty.  Caller holds the head's lock.
 bool write_ring(Ctx *c, int n, const uint8_t *kc, const uint8_t *vc, int row_stride,
                 const float *ks, const float *vs, const char *fn) {
+  {
+    // appends still queued on the library stream would land after the copies
+    DeviceGuard g(c->device);
+    if (hip_fail(hipStreamSynchronize(lib_stream(c->device)), fn)) return false;
+    c->pending = false;
+  }
   const int cap = c->cap;
   std::vector<uint8_t> ak((size_t)cap * c->k_pb, 0), av((size_t)cap * c->v_pb, 0);
   std::vector<float> aks((size_t)cap, 1.0f), avs((size_t)cap, 1.0f);
