@@ -319,9 +319,10 @@ struct DeviceGuard {
 // directly) and the call does not wait for the kernel unless sync: the next
 // flush waits before it reuses the pinned rows, and compute waits at its end.
 // sync = true (inspection, snapshots, device-form calls on other streams)
-// waits for everything queued on the library stream.
+// also waits for work already queued for this context (c->pending: set by
+// any flush that touched it).
 bool flush_locked(Ctx *c, const char *fn, bool sync = true) {
-  if (c->staged == 0 && !sync) return true;
+  if (c->staged == 0 && !(sync && c->pending)) return true;
   DeviceGuard g(c->device);
   hipStream_t s = lib_stream(c->device);
   if (c->staged > 0) {
@@ -351,7 +352,7 @@ bool flush_locked(Ctx *c, const char *fn, bool sync = true) {
     c->stage_k.clear();
     c->stage_v.clear();
   }
-  if (sync) {
+  if (sync && c->pending) {
     if (hip_fail(hipStreamSynchronize(s), fn)) return false;
     c->pending = false;
   }
@@ -434,6 +435,28 @@ struct Plan {
   DevBuf d_list, d_ws;
 };
 
+// Before a plan launches on the caller's stream: queue every context's staged
+// host appends on the library stream, then wait for that stream once if any
+// work for these contexts is queued there.
+bool flush_plan(Plan *p, const char *fn) {
+  bool queued = false;
+  for (Ctx *c : p->ctxs) {
+    std::lock_guard<std::mutex> g(c->mu);
+    if (!flush_locked(c, fn, false)) return false;
+    queued = queued || c->pending;
+  }
+  if (!queued) return true;
+  {
+    DeviceGuard g(p->device);
+    if (hip_fail(hipStreamSynchronize(lib_stream(p->device)), fn)) return false;
+  }
+  for (Ctx *c : p->ctxs) {
+    std::lock_guard<std::mutex> g(c->mu);
+    c->pending = false;
+  }
+  return true;
+}
+
 // Locks every head of an MHA in index order (per-head calls take one head
 // lock only, so the order cannot deadlock against them).
 struct HeadLocks {
@@ -453,9 +476,12 @@ bool flush_all_locked(Mha *m, const char *fn, bool sync = true) {
   bool uniform = S > 0;
   for (Ctx *c : m->heads) uniform = uniform && c->staged == S;
   if (!uniform) {
-    for (Ctx *c : m->heads)
+    bool queued = m->pending;
+    for (Ctx *c : m->heads) {
       if (c->staged > 0 && !flush_locked(c, fn, false)) return false;
-    if (sync) {
+      queued = queued || c->pending;
+    }
+    if (sync && queued) {
       DeviceGuard g(m->device);
       if (hip_fail(hipStreamSynchronize(lib_stream(m->device)), fn)) return false;
       m->pending = false;
@@ -495,10 +521,12 @@ bool flush_all_locked(Mha *m, const char *fn, bool sync = true) {
     c->staged = 0;
     c->stage_k.clear();
     c->stage_v.clear();
+    c->pending = true;  // the launch writes this head's ring
   }
   if (sync) {
     if (hip_fail(hipStreamSynchronize(s), fn)) return false;
     m->pending = false;
+    for (Ctx *c : m->heads) c->pending = false;
   }
   return true;
 }
@@ -804,12 +832,14 @@ int adaptq_mha_compute_all(adaptq_mha_t h, const float *queries, float *outs) {
       if (i == 0) n = r;
     }
     m->pending = false;  // compute_locked waited for the stream
+    for (Ctx *c : m->heads) c->pending = false;
     clear_error();
     return n;
   }
   if (n < 0) return -1;
   if (hip_fail(hipStreamSynchronize(s), fn)) return -1;
   m->pending = false;
+  for (Ctx *c : m->heads) c->pending = false;
   std::memcpy(outs, static_cast<uint8_t *>(m->h_io.p) + io, (size_t)H * dim * 4);
   clear_error();
   return n;
@@ -1199,10 +1229,7 @@ int adaptq_plan_append_device(adaptq_plan_t h, const float *d_keys, const float 
   }
   Plan *p = static_cast<Plan *>(h);
   if (n_tokens == 0) return 0;
-  for (Ctx *c : p->ctxs) {
-    std::lock_guard<std::mutex> g(c->mu);
-    if (!flush_locked(c, fn)) return -1;
-  }
+  if (!flush_plan(p, fn)) return -1;
   DeviceGuard g(p->device);
   hipStream_t s = static_cast<hipStream_t>(stream);  // NULL = the HIP null stream
   const Ctx *c0 = p->ctxs[0];
@@ -1227,9 +1254,9 @@ int adaptq_plan_compute_device(adaptq_plan_t h, const float *d_queries, float *d
   int max_n = 0;
   bool have_mode = false;
   Mode mode = Mode::Dense;
+  if (!flush_plan(p, fn)) return -1;
   for (Ctx *c : p->ctxs) {
     std::lock_guard<std::mutex> g(c->mu);
-    if (!flush_locked(c, fn)) return -1;
     if (c->st.size > 0) {
       const Mode m = mode_of(c);
       if (have_mode && m != mode) {
