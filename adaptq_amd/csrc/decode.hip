@@ -1046,14 +1046,21 @@ __global__ __launch_bounds__(kThreads) void decode_generic_kernel(
   }
 }
 
-// Merge the splits of each item, normalise, undo the rotation.
+// Merge the splits of each item, normalise, undo the rotation.  The split
+// maxima, weights and sums are spread over the block (split s on thread
+// s mod kThreads); each dimension's weighted sum over the splits is shared by
+// kThreads / P thread groups, group g taking splits s = g (mod groups).
+constexpr int kMaxSplitWeights = 1024;  // plan_splits never makes more splits
+
 template <bool INVERSE_FWHT>
 __global__ __launch_bounds__(kThreads) void finalize_kernel(HeadDesc *const *item_desc, int P,
                                                             int n_splits,
                                                             const float *__restrict__ partials,
                                                             float *__restrict__ outs) {
   __shared__ float s_acc[kMaxPadded];
-  __shared__ float s_f[256];
+  __shared__ float s_f[kMaxSplitWeights];
+  __shared__ float s_red[kWaves];
+  __shared__ float s_grp[kThreads];
   const int item = blockIdx.x;
   const HeadDesc *d = item_desc[item];
   const int dim = d->dim;
@@ -1062,25 +1069,57 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(HeadDesc *const *ite
     for (int i = threadIdx.x; i < dim; i += blockDim.x) out[i] = 0.0f;
     return;
   }
-  const float *part = partials + (size_t)item * n_splits * (P + 4);
-  float M = -INFINITY;
-  for (int s = 0; s < n_splits; ++s) M = fmaxf(M, part[(size_t)s * (P + 4)]);
-  float L = 0.0f;
-  for (int s = 0; s < n_splits; ++s) {
-    const float ms = part[(size_t)s * (P + 4)];
-    const float f = ms == -INFINITY ? 0.0f : expf(ms - M);
-    if (threadIdx.x == 0 && s < 256) s_f[s] = f;
-    L += f * part[(size_t)s * (P + 4) + 1];
-  }
+  const size_t stride = (size_t)P + 4;
+  const float *part = partials + (size_t)item * n_splits * stride;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float m = -INFINITY;
+  for (int s = threadIdx.x; s < n_splits; s += kThreads) m = fmaxf(m, part[s * stride]);
+  m = wave_max(m);
+  if (lane == 0) s_red[wave] = m;
   __syncthreads();
-  for (int i = threadIdx.x; i < P; i += blockDim.x) {
+  float M = s_red[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_red[w]);
+  __syncthreads();
+  float l = 0.0f;
+  for (int s = threadIdx.x; s < n_splits; s += kThreads) {
+    const float ms = part[s * stride];
+    const float f = ms == -INFINITY ? 0.0f : expf(ms - M);
+    if (s < kMaxSplitWeights) s_f[s] = f;
+    l += f * part[s * stride + 1];
+  }
+  l = wave_sum(l);
+  if (lane == 0) s_red[wave] = l;
+  __syncthreads();
+  float L = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) L += s_red[w];
+  auto weight = [&](int s) -> float {
+    if (s < kMaxSplitWeights) return s_f[s];
+    const float ms = part[s * stride];
+    return ms == -INFINITY ? 0.0f : expf(ms - M);
+  };
+  const int groups = P < kThreads ? kThreads / P : 1;
+  if (groups > 1) {
+    // P divides kThreads (P is a power of two below it)
+    const int i = threadIdx.x % P, grp = threadIdx.x / P;
     float a = 0.0f;
-    for (int s = 0; s < n_splits; ++s) {
-      const float f = s < 256 ? s_f[s]
-                              : (part[(size_t)s * (P + 4)] == -INFINITY ? 0.0f : expf(part[(size_t)s * (P + 4)] - M));
-      a += f * part[(size_t)s * (P + 4) + 4 + i];
+#pragma unroll 4
+    for (int s = grp; s < n_splits; s += groups) a += weight(s) * part[s * stride + 4 + i];
+    s_grp[threadIdx.x] = a;
+    __syncthreads();
+    if (threadIdx.x < P) {
+      float t = 0.0f;
+      for (int q = 0; q < groups; ++q) t += s_grp[q * P + threadIdx.x];
+      s_acc[threadIdx.x] = t;
     }
-    s_acc[i] = a;
+  } else {
+    for (int i = threadIdx.x; i < P; i += kThreads) {
+      float a = 0.0f;
+#pragma unroll 4
+      for (int s = 0; s < n_splits; ++s) a += weight(s) * part[s * stride + 4 + i];
+      s_acc[i] = a;
+    }
   }
   __syncthreads();
   finish_item<INVERSE_FWHT>(s_acc, P, dim, L, d->signs, out);
