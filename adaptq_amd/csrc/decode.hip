@@ -1129,9 +1129,8 @@ struct SplitPlan {
   int splits, chunk;
 };
 
-SplitPlan plan_splits(int n_items, int max_n, int min_chunk = 256) {
+SplitPlan plan_splits(int n_items, int max_n, int min_chunk, int target_blocks) {
   SplitPlan sp;
-  const int target_blocks = 1024;
   int by_work = (max_n + min_chunk - 1) / min_chunk;
   if (by_work < 1) by_work = 1;
   int want = (target_blocks + n_items - 1) / n_items;
@@ -1208,7 +1207,13 @@ SplitPlan decode_plan(int n_items, const DecodeShape &sh) {
     sp.chunk = ((max_n + kTile - 1) / kTile) * kTile;
     return sp;
   }
-  return plan_splits(n_items, max_n, lut ? kLutWaves * kTile : 256);
+  // LUT kernel: about one 512-thread block per CU (256 CUs): each extra block
+  // repeats the query rotation and the K table build, and the splits add
+  // finalize work (measured: 4 heads x 131,072 tokens 48 -> 27 us, 64 heads x
+  // 8,192 tokens 35 -> 25 us, 8 heads x 32,768 tokens 28 -> 25 us against a
+  // target of 1,024 blocks; none of the sampled shapes slower).
+  if (lut) return plan_splits(n_items, max_n, kLutWaves * kTile, 256);
+  return plan_splits(n_items, max_n, 256, 1024);
 }
 
 }  // namespace
