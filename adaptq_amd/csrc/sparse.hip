@@ -19,10 +19,12 @@
 // reference's std::sort leaves their order unspecified.
 //
 // Kernels: one grid over (token blocks, items) computes the logits; one block
-// per item does softmax, a bitonic sort (in LDS up to 16384 tokens, else in
-// the workspace) and the cut, and turns the selection into per-token weights;
-// a grid over (token chunks, items) sums the weighted V rows; one block per
-// item adds the chunks and applies the inverse FWHT.
+// per item does softmax, the sort (a stable radix sort in LDS up to 16,384
+// tokens, a bitonic sort in the workspace above) and the cut, and turns the
+// selection into per-token weights; a grid over (token chunks, items) sums the
+// weighted V rows; one block per item adds the chunks and applies the inverse
+// FWHT.  Short rings at padded 64 (up to 3,072 tokens) run all four steps in
+// one block per item (sparse_fused_kernel).
 #include "launch.hpp"
 
 namespace aq {
@@ -111,14 +113,17 @@ __device__ void rotate_query_exact(float *s_q, const float *q, int dim, int P,
 }
 
 // dot(s_q, CB[codes of row]) with the reference's 8 FMA lanes (lane L takes
-// codes L, L+8, ...) summed pairwise (attention.cpp:83-136).
+// codes L, L+8, ...) summed pairwise (attention.cpp:83-136).  cbk is the K
+// codebook in LDS (a run-time index into a constant array is a memory load
+// per code).
 // PT = 0: any padded size, codes read byte by byte.  PT = 64/128: the row is
 // read as words; 3-bit rows are in reference order; for 2/4-bit codes
 // reference word w sits at stored word w ^ (x >> 2) with its bytes permuted by
 // b ^ (x & 3) (kperm_mask), and one v_perm per word restores the reference
 // byte order.
 template <int PT, int KB>
-__device__ __forceinline__ float kdot_row(const uint8_t *row, int x, const float *s_q, int P) {
+__device__ __forceinline__ float kdot_row(const uint8_t *row, int x, const float *s_q, int P,
+                                          const float *cbk) {
   float s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   if constexpr (PT != 0 && KB == 3) {
     // 3-bit rows are unpermuted: 24-bit big-endian groups of 8 codes
@@ -135,7 +140,7 @@ __device__ __forceinline__ float kdot_row(const uint8_t *row, int x, const float
                            ((w[(b0 + 2) >> 2] >> (8 * ((b0 + 2) & 3))) & 255u);
 #pragma unroll
       for (int k = 0; k < 8; ++k)
-        s[k] = fmaf(cbv<KB>((int)((w24 >> (21 - 3 * k)) & 7u)), s_q[8 * g + k], s[k]);
+        s[k] = fmaf(cbk[(w24 >> (21 - 3 * k)) & 7u], s_q[8 * g + k], s[k]);
     }
   } else if constexpr (PT != 0 && (KB == 2 || KB == 4)) {
     constexpr int W = PT * KB / 32;
@@ -155,13 +160,13 @@ __device__ __forceinline__ float kdot_row(const uint8_t *row, int x, const float
         const int byte = j >> 2;
         c = (int)((w[byte >> 2] >> (8 * (byte & 3) + 6 - 2 * (j & 3))) & 3u);
       }
-      s[j & 7] = fmaf(cbv<KB>(c), s_q[j], s[j & 7]);
+      s[j & 7] = fmaf(cbk[c], s_q[j], s[j & 7]);
     }
   } else {
     for (int j = 0; j < P; j += 8)
 #pragma unroll
       for (int L = 0; L < 8; ++L)
-        if (j + L < P) s[L] = fmaf(cbv<KB>(kcode_at<KB>(row, j + L, x)), s_q[j + L], s[L]);
+        if (j + L < P) s[L] = fmaf(cbk[kcode_at<KB>(row, j + L, x)], s_q[j + L], s[L]);
   }
   const float t0 = s[0] + s[4], t1 = s[1] + s[5], t2 = s[2] + s[6], t3 = s[3] + s[7];
   return (t0 + t1) + (t2 + t3);
@@ -174,17 +179,19 @@ __global__ __launch_bounds__(kThreads) void sparse_logits_kernel(HeadDesc *const
                                                                  float sqrt_p, float *ws,
                                                                  size_t ws_stride) {
   __shared__ float s_q[kMaxPadded];
+  __shared__ float s_cbk[16];
   const int item = blockIdx.y;
   const HeadDesc *d = item_desc[item];
   const int n = d->st.size, cap = d->cap, dim = d->dim, P = d->padded;
   if ((int)(blockIdx.x * blockDim.x) >= n) return;
+  if (threadIdx.x < (1 << KB)) s_cbk[threadIdx.x] = cbv<KB>(threadIdx.x);
   rotate_query_exact(s_q, queries + (size_t)item * dim, dim, P, d->signs, inv_sqrt_p, sqrt_p);
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const int slot = (int)(((long long)d->st.head - n + cap + i) % cap);
   const uint8_t *row = d->k_codes + (size_t)slot * d->k_pb;
   const int x = slot & kperm_mask(P, KB);
-  const float dot = kdot_row<PT, KB>(row, x, s_q, P);
+  const float dot = kdot_row<PT, KB>(row, x, s_q, P, s_cbk);
   const float attn_s = 1.0f / (sqrtf((float)dim) * (float)P);
   ws[(size_t)item * ws_stride + i] = __fmul_rn(__fmul_rn(dot, attn_s), d->k_scale[slot]);
 }
@@ -628,6 +635,154 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
   // (the weights in lg are read by sparse_vsum_kernel)
 }
 
+// Short rings at padded 64 (n <= kFusedMax): one block of kSelThreads per item
+// does it all.  The logits are sparse_logits_kernel's (same kdot_row and
+// roundings), the selection is select_small's, so the selected set and the
+// per-token weights are the multi-kernel path's bit for bit; then the block
+// sums the weighted V rows and applies the inverse FWHT, which saves three
+// launches and their global round trips (the V sum's rounding order differs
+// from the multi-kernel path's chunked sums, as both differ from the
+// reference's sorted order).  Measured against the four launches: 4 heads x
+// 2,048 tokens 56 -> 52 us, 256 heads x 2,048 tokens 75 -> 58 us, even at
+// 4,096 tokens; at padded 128 one block per item computing every logit is
+// slower than the logits kernel's many blocks (8 heads x 2,048 tokens 62 ->
+// 80 us), so padded 128 keeps the four launches.
+constexpr int kFusedMax = 3 * kSelThreads;
+
+// V row unit read by one lane of the fused kernel: a 32-bit word of 2- or
+// 4-bit codes (16 or 8 codes), or a 3-byte group of 8 3-bit codes.
+template <int VB>
+struct VWord {
+  static constexpr int bytes = VB == 3 ? 3 : 4;
+  static constexpr int codes = VB == 3 ? 8 : 32 / VB;
+};
+
+// Bit position of code c (0 = first) inside a unit as loaded: words are
+// little-endian with codes MSB-first in each byte; a 3-byte group is the
+// big-endian 24-bit value.
+template <int VB>
+__device__ __forceinline__ int vcode_shift(int c) {
+  if constexpr (VB == 2) return 8 * (c >> 2) + 6 - 2 * (c & 3);
+  else if constexpr (VB == 4) return 8 * (c >> 1) + 4 - 4 * (c & 1);
+  else return 21 - 3 * c;
+}
+
+template <int PT, int KB, int VB>
+__global__ __launch_bounds__(kSelThreads) void sparse_fused_kernel(
+    HeadDesc *const *item_desc, const float *__restrict__ queries, float v_mass, float inv_sqrt_p,
+    float sqrt_p, float *ws, size_t ws_stride, float *__restrict__ outs) {
+  __shared__ SelectShared sh;
+  __shared__ float s_q[PT];
+  __shared__ float s_cb[16];
+  __shared__ float s_cbk[16];
+  constexpr int UB = VWord<VB>::bytes, CPU = VWord<VB>::codes;
+  constexpr int U = PT * VB / 8 / UB;  // units per V row (4..16)
+  constexpr int TPI = 64 / U;          // tokens per wave step
+  constexpr int NW = kSelThreads / 64;
+  constexpr int UNR = 4;               // row loads in flight per lane
+  const int item = blockIdx.x, tid = threadIdx.x;
+  const HeadDesc *d = item_desc[item];
+  const int n = d->st.size, cap = d->cap, dim = d->dim;
+  float *out = outs + (size_t)item * dim;
+  if (n == 0) {
+    for (int i = tid; i < dim; i += blockDim.x) out[i] = 0.0f;
+    return;
+  }
+  if (tid < (1 << VB)) s_cb[tid] = cbv<VB>(tid);
+  if (tid < (1 << KB)) s_cbk[tid] = cbv<KB>(tid);
+  float *lg = ws + (size_t)item * ws_stride;
+  const int s0 = (int)(((long long)d->st.head - n + cap) % cap);
+  rotate_query_exact(s_q, queries + (size_t)item * dim, dim, PT, d->signs, inv_sqrt_p, sqrt_p);
+
+  // logits of the tokens select_small gives this thread (E per thread); each
+  // thread reads back only its own
+  const int E = n <= kSelThreads ? 1 : n <= 2 * kSelThreads ? 2 : 4;
+  const float attn_s = 1.0f / (sqrtf((float)dim) * (float)PT);
+  for (int e = 0; e < E; ++e) {
+    const int t = tid * E + e;
+    if (t < n) {
+      const int slot = ring_slot(s0, t, cap);
+      const uint8_t *row = d->k_codes + (size_t)slot * d->k_pb;
+      const float dot = kdot_row<PT, KB>(row, slot & kperm_mask(PT, KB), s_q, PT, s_cbk);
+      lg[t] = __fmul_rn(__fmul_rn(dot, attn_s), d->k_scale[slot]);
+    }
+  }
+  if (E == 1) select_small<1>(d, v_mass, lg, n, s0, sh);
+  else if (E == 2) select_small<2>(d, v_mass, lg, n, s0, sh);
+  else select_small<4>(d, v_mass, lg, n, s0, sh);
+  __syncthreads();
+  // the weights (each thread's own, in lg) into LDS over the sort keys
+  float *w_lds = reinterpret_cast<float *>(sh.key);
+  for (int e = 0; e < E; ++e) {
+    const int t = tid * E + e;
+    if (t < n) w_lds[t] = lg[t];
+  }
+  __syncthreads();
+
+  // weighted V rows: lane (sub, u) takes unit u of token wave * TPI + sub,
+  // then every NW * TPI tokens; UNR rows are requested before any is used
+  const int lane = tid & 63, wave = tid >> 6, sub = lane / U, u = lane % U;
+  const uint8_t *vsrc = d->v_codes;
+  const int vpb = d->v_pb;
+  float acc[CPU];
+#pragma unroll
+  for (int c = 0; c < CPU; ++c) acc[c] = 0.0f;
+  for (int t = wave * TPI + sub; t < n; t += NW * TPI * UNR) {
+    uint32_t bits[UNR];
+    float wt[UNR];
+#pragma unroll
+    for (int j = 0; j < UNR; ++j) {
+      const int tj = t + j * NW * TPI;
+      wt[j] = tj < n ? w_lds[tj] : 0.0f;
+      const uint8_t *row = vsrc + (size_t)ring_slot(s0, tj < n ? tj : n - 1, cap) * vpb;
+      if constexpr (UB == 4) {
+        bits[j] = reinterpret_cast<const uint32_t *>(row)[u];
+      } else {
+        const uint8_t *g = row + 3 * u;
+        bits[j] = ((uint32_t)g[0] << 16) | ((uint32_t)g[1] << 8) | (uint32_t)g[2];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < UNR; ++j)
+#pragma unroll
+      for (int c = 0; c < CPU; ++c)
+        acc[c] = fmaf(s_cb[(bits[j] >> vcode_shift<VB>(c)) & ((1u << VB) - 1u)], wt[j], acc[c]);
+  }
+  // the TPI token groups of a wave (lanes u + U * sub), then the waves in order
+#pragma unroll
+  for (int off = U; off < 64; off <<= 1)
+#pragma unroll
+    for (int c = 0; c < CPU; ++c) acc[c] += __shfl_xor(acc[c], off);
+  float *s_red = reinterpret_cast<float *>(sh.cnt);  // NW x PT floats
+  if (sub == 0) {
+#pragma unroll
+    for (int c = 0; c < CPU; ++c) s_red[wave * PT + u * CPU + c] = acc[c];
+  }
+  __syncthreads();
+  float *s_acc = sh.stage;
+  for (int j = tid; j < PT; j += blockDim.x) {
+    float a = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) a += s_red[w * PT + j];
+    s_acc[j] = a;
+  }
+  __syncthreads();
+  for (int len = 1; len < PT; len <<= 1) {
+    for (int k = tid; k < PT / 2; k += blockDim.x) {
+      const int jj = (k / len) * 2 * len + (k % len);
+      const float lo = s_acc[jj], hi = s_acc[jj + len];
+      s_acc[jj] = lo + hi;
+      s_acc[jj + len] = lo - hi;
+    }
+    __syncthreads();
+  }
+  const float scale = 1.0f / sqrtf((float)PT);
+  for (int i = tid; i < dim; i += blockDim.x) {
+    const float v = __fmul_rn(s_acc[i], scale);
+    out[i] = sign_plus(d->signs, i) ? v : -v;
+  }
+}
+
 // Codes per byte-aligned unit of a packed row and the unit's size in bytes:
 // 2-bit: 1 byte = 4 codes, 4-bit: 1 byte = 2 codes, 3-bit: 3 bytes = 8 codes.
 template <int VB>
@@ -801,6 +956,20 @@ hipError_t launch_decode_sparse(HeadDesc *const *descs, int n_items, const Decod
     float *out = d_out + (size_t)c0 * sh.dim;
     float *w = ws + (size_t)c0 * stride;
     float *parts = parts_all + (size_t)c0 * splits * sh.padded;
+    if (n <= kFusedMax && sh.padded == 64) {
+#define AQ_FUSED(PT, KB_, VB_)                                                                    \
+  if (sh.padded == PT && sh.k_bits == KB_ && sh.v_bits == VB_) {                                  \
+    sparse_fused_kernel<PT, KB_, VB_><<<cnt, kSelThreads, 0, s>>>(dsc, q, v_mass, isp, sp, w,      \
+                                                                   stride, out);                  \
+    const hipError_t fe = hipGetLastError();                                                      \
+    if (fe != hipSuccess) return fe;                                                              \
+    continue;                                                                                     \
+  }
+      AQ_FUSED(64, 2, 2) AQ_FUSED(64, 2, 3) AQ_FUSED(64, 2, 4)
+      AQ_FUSED(64, 3, 2) AQ_FUSED(64, 3, 3) AQ_FUSED(64, 3, 4)
+      AQ_FUSED(64, 4, 2) AQ_FUSED(64, 4, 3) AQ_FUSED(64, 4, 4)
+#undef AQ_FUSED
+    }
     const dim3 g1((n + kThreads - 1) / kThreads, cnt);
 #define AQ_LOGITS(PT, KB_) \
   sparse_logits_kernel<PT, KB_><<<g1, kThreads, 0, s>>>(dsc, q, n, isp, sp, w, stride)
