@@ -916,6 +916,9 @@ __global__ __launch_bounds__(kThreads) void decode_generic_kernel(
   constexpr int G = 8;
   __shared__ float s_q[kMaxPadded];
   __shared__ float s_part[kWaves][G];
+  // codebooks in LDS: a run-time index into the constant tables would be a
+  // memory load per code
+  __shared__ float s_cbk[16], s_cbv[16];
   const int item = blockIdx.y, split = blockIdx.x;
   const HeadDesc *d = item_desc[item];
   const ItemView iv = item_view<RAW>(d);
@@ -933,6 +936,12 @@ __global__ __launch_bounds__(kThreads) void decode_generic_kernel(
     return;
   }
   const float *q = queries + (size_t)item * dim;
+  if constexpr (KQ) {
+    if (threadIdx.x < (1 << KB)) s_cbk[threadIdx.x] = cbv<KB>(threadIdx.x);
+  }
+  if constexpr (VQ) {
+    if (threadIdx.x < (1 << VB)) s_cbv[threadIdx.x] = cbv<VB>(threadIdx.x);
+  }
   for (int i = threadIdx.x; i < P; i += blockDim.x) {
     float v = i < dim ? q[i] : 0.0f;
     if (KQ && !((d->signs[i >> 5] >> (i & 31)) & 1u)) v = -v;
@@ -974,7 +983,7 @@ __global__ __launch_bounds__(kThreads) void decode_generic_kernel(
         const uint8_t *row = iv.k_rows + (size_t)t * kstride;
         const int x = t & xmask;
         for (int i = threadIdx.x; i < own; i += kThreads)
-          pd[g] = fmaf(s_q[i], cbv<KB>(kcode_at<KB>(row, i, x)), pd[g]);
+          pd[g] = fmaf(s_q[i], s_cbk[kcode_at<KB>(row, i, x)], pd[g]);
       }
 #pragma unroll
       for (int g = 0; g < G; ++g) {
@@ -1029,7 +1038,7 @@ __global__ __launch_bounds__(kThreads) void decode_generic_kernel(
         const int i = threadIdx.x + r * kThreads;
         if (i >= own) break;
         float vv;
-        if constexpr (VQ) vv = cbv<VB>(code_at<VB>(row, i));
+        if constexpr (VQ) vv = s_cbv[code_at<VB>(row, i)];
         else vv = reinterpret_cast<const float *>(row)[i];
         acc[r] = fmaf(vv, wgt, acc[r]);
       }
