@@ -170,7 +170,6 @@ struct Mha {
   DevBuf d_ws, d_io, d_stage;
   PinnedBuf h_stage, h_io;
   bool pending = false;  // an append launch may still read h_stage
-  std::vector<float> pack_q;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -964,27 +963,28 @@ int adaptq_ggml_attn_f32(adaptq_mha_t h, const float *q, int head_dim, int n_hea
     return -1;
   std::lock_guard<std::mutex> gm(m->mu);
   HeadLocks locks(m);
-  if (!flush_all_locked(m, fn)) return -1;
+  // the decode runs on the library stream after the flush's launches
+  if (!flush_all_locked(m, fn, false)) return -1;
   const int H = m->n_heads, dim = head_dim;
   if (n_queries == 0) {
     clear_error();
     return m->heads[0]->st.size;
   }
-  // queries packed [query][head][dim]; outputs come back in the same order
+  DeviceGuard g(m->device);
+  hipStream_t s = lib_stream(m->device);
+  // queries packed [query][head][dim] into pinned memory the kernels read;
+  // outputs come back there in the same order
   const size_t rows = (size_t)n_queries * H;
-  m->pack_q.resize(2 * rows * dim);
-  float *pq = m->pack_q.data(), *po = pq + rows * dim;
+  const size_t io = align256(rows * dim * 4);
+  if (hip_fail(m->h_io.ensure(2 * io), fn)) return -1;  // no kernel uses it between calls
+  float *pq = static_cast<float *>(m->h_io.p);
+  float *po = reinterpret_cast<float *>(static_cast<uint8_t *>(m->h_io.p) + io);
   for (int j = 0; j < n_queries; ++j)
     for (int i = 0; i < H; ++i)
       std::memcpy(pq + ((size_t)j * H + i) * dim, row_at(q, (size_t)i, q_nb1, (size_t)j, q_nb2),
                   (size_t)dim * 4);
-  DeviceGuard g(m->device);
-  hipStream_t s = lib_stream(m->device);
-  const size_t io = align256(rows * dim * 4);
-  if (hip_fail(m->d_io.ensure(2 * io), fn)) return -1;
-  float *dq = static_cast<float *>(m->d_io.p);
-  float *dout = reinterpret_cast<float *>(static_cast<uint8_t *>(m->d_io.p) + io);
-  if (hip_fail(hipMemcpyAsync(dq, pq, rows * dim * 4, hipMemcpyHostToDevice, s), fn)) return -1;
+  const float *dq = static_cast<const float *>(m->h_io.dp);
+  float *dout = reinterpret_cast<float *>(static_cast<uint8_t *>(m->h_io.dp) + io);
   int n = launch_all_locked(m, dq, dout, s, fn, n_queries);
   if (n == -2) {  // heads differ in size or branch: head by head, all queries of a head at once
     std::vector<float> hq((size_t)n_queries * dim), ho((size_t)n_queries * dim);
@@ -999,10 +999,10 @@ int adaptq_ggml_attn_f32(adaptq_mha_t h, const float *q, int head_dim, int n_hea
     }
   } else {
     if (n < 0) return -1;
-    hipError_t e = hipMemcpyAsync(po, dout, rows * dim * 4, hipMemcpyDeviceToHost, s);
-    if (e == hipSuccess) e = hipStreamSynchronize(s);
-    if (hip_fail(e, fn)) return -1;
+    if (hip_fail(hipStreamSynchronize(s), fn)) return -1;
   }
+  m->pending = false;  // the stream has drained (compute_locked waits for it too)
+  for (Ctx *c : m->heads) c->pending = false;
   for (int j = 0; j < n_queries; ++j)
     for (int i = 0; i < H; ++i)
       std::memcpy(const_cast<float *>(row_at(dst, (size_t)i, d_nb1, (size_t)j, d_nb2)),
