@@ -141,12 +141,14 @@ def test_decode_hybrid(oracle, dim, kb, vb, hyb, n):
 # Sort in LDS (n <= 16384) and in the workspace (above); quad sums staged in
 # one and in several chunks (n/4 above 4096); peaked queries (qs 20: the cut
 # falls after a few quads) and flat ones; v_mass near 1 (the single-token tail
-# runs); ragged n.
+# runs); ragged n.  At padded 64 up to 3,072 tokens the one-block kernel runs
+# (1, 2 and 4 tokens per thread; a wrapped ring; 3-bit V at the size limit).
 @pytest.mark.parametrize("dim,kb,vb,cap,n,vm,qs", [
     (64, 4, 2, 2048, 2048, 0.95, 3), (128, 4, 4, 512, 700, 0.95, 3), (64, 3, 2, 600, 513, 0.7, 3),
     (128, 2, 3, 9000, 9000, 0.95, 3), (64, 4, 2, 100, 7, 0.5, 3), (64, 4, 2, 17000, 17001, 0.95, 3),
     (64, 2, 4, 3000, 2999, 0.95, 20), (128, 4, 2, 20000, 20000, 0.999, 1),
-    (64, 4, 3, 5000, 4998, 0.9999, 0.5),
+    (64, 4, 3, 5000, 4998, 0.9999, 0.5), (64, 4, 2, 1500, 2600, 0.95, 3),
+    (64, 3, 3, 3072, 3072, 0.9, 3),
 ])
 def test_decode_sparse_v(oracle, dim, kb, vb, cap, n, vm, qs):
     print(f"decode sparse dim={dim} k{kb}v{vb} n={n} v_mass={vm} qscale={qs}", flush=True)
