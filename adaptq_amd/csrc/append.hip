@@ -166,41 +166,14 @@ __device__ __forceinline__ void load_wave_rows(const float *wave_rows, int lane,
 // i.e. UNIFORM with n_tok <= 128, or one token per head): this launch also
 // advances each head's ring state, once every thread of the head has read the
 // old one, and no commit_kernel follows.
+// Encode token t of context c (ring state st as read before any commit) for
+// one side; the caller has placed the thread on (c, t).
 template <int P, int B, bool UNIFORM>
-__global__ __launch_bounds__(128) void append_kernel(HeadDesc *const *descs, int n_ctx,
-                                                     int side, const float *__restrict__ src,
-                                                     int n_tok, int dim, float inv_sqrt_p,
-                                                     float sqrt_p, int commit) {
-  // 4-bit codes: the bucket table of quantize_ss4, built before any lane leaves
-  __shared__ Q4Entry s_q4[B == 4 ? kQ4Entries : 1];
-  if constexpr (B == 4) {
-    for (int i = threadIdx.x; i < kQ4Entries; i += blockDim.x) s_q4[i] = q4s_entry(i);
-    __syncthreads();
-  }
-  int c, t;
-  if constexpr (UNIFORM) {
-    c = blockIdx.y;
-    t = blockIdx.x * blockDim.x + threadIdx.x;
-  } else {
-    const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (g >= (long long)n_ctx * n_tok) return;
-    c = (int)(g / n_tok);
-    t = (int)(g - (long long)c * n_tok);
-  }
-  const HeadDesc *d = descs[c];
-  const RingState st = d->st;
+__device__ __forceinline__ void encode_row(const HeadDesc *d, const RingState st, int c, int t,
+                                           int side, const float *__restrict__ src, int n_tok,
+                                           int dim, float inv_sqrt_p, float sqrt_p,
+                                           const Q4Entry *s_q4) {
   const int cap = d->cap;
-  if (commit) {
-    if constexpr (UNIFORM) {
-      __syncthreads();  // the block's threads all hold the old state
-      if (threadIdx.x == 0) descs[c]->st = ring_after(st, n_tok, cap, d->hyb);
-    } else {
-      descs[c]->st = ring_after(st, n_tok, cap, d->hyb);  // one token: this lane's head only
-    }
-  }
-  if constexpr (UNIFORM) {
-    if (t >= n_tok) return;
-  }
   const float *x = src + ((size_t)c * n_tok + t) * dim;
 
   // Token t survives the batch only if fewer than cap tokens follow it.
@@ -342,6 +315,67 @@ __global__ __launch_bounds__(128) void append_kernel(HeadDesc *const *descs, int
     if (!stored) store_row<Row<P, B>::bytes>(codes, w, slot);
     scales[slot] = norm;
   }
+}
+
+template <int P, int B, bool UNIFORM>
+__global__ __launch_bounds__(128) void append_kernel(HeadDesc *const *descs, int n_ctx,
+                                                     int side, const float *__restrict__ src,
+                                                     int n_tok, int dim, float inv_sqrt_p,
+                                                     float sqrt_p, int commit) {
+  // 4-bit codes: the bucket table of quantize_ss4, built before any lane leaves
+  __shared__ Q4Entry s_q4[B == 4 ? kQ4Entries : 1];
+  if constexpr (B == 4) {
+    for (int i = threadIdx.x; i < kQ4Entries; i += blockDim.x) s_q4[i] = q4s_entry(i);
+    __syncthreads();
+  }
+  int c, t;
+  if constexpr (UNIFORM) {
+    c = blockIdx.y;
+    t = blockIdx.x * blockDim.x + threadIdx.x;
+  } else {
+    const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= (long long)n_ctx * n_tok) return;
+    c = (int)(g / n_tok);
+    t = (int)(g - (long long)c * n_tok);
+  }
+  const HeadDesc *d = descs[c];
+  const RingState st = d->st;
+  const int cap = d->cap;
+  if (commit) {
+    if constexpr (UNIFORM) {
+      __syncthreads();  // the block's threads all hold the old state
+      if (threadIdx.x == 0) descs[c]->st = ring_after(st, n_tok, cap, d->hyb);
+    } else {
+      descs[c]->st = ring_after(st, n_tok, cap, d->hyb);  // one token: this lane's head only
+    }
+  }
+  if constexpr (UNIFORM) {
+    if (t >= n_tok) return;
+  }
+  encode_row<P, B, UNIFORM>(d, st, c, t, side, src, n_tok, dim, inv_sqrt_p, sqrt_p, s_q4);
+}
+
+// Both sides of one token per head in one launch (n_tok == 1, lanes over
+// heads): each lane encodes its head's K row, then its V row, and advances the
+// head's ring state, which no other lane reads.  Halves the launches of a
+// decode step's append.
+template <int P, int KB, int VB>
+__global__ __launch_bounds__(128) void append_kv_kernel(HeadDesc *const *descs, int n_ctx,
+                                                        const float *__restrict__ keys,
+                                                        const float *__restrict__ vals,
+                                                        int dim, float inv_sqrt_p, float sqrt_p) {
+  __shared__ Q4Entry s_q4[(KB == 4 || VB == 4) ? kQ4Entries : 1];
+  if constexpr (KB == 4 || VB == 4) {
+    for (int i = threadIdx.x; i < kQ4Entries; i += blockDim.x) s_q4[i] = q4s_entry(i);
+    __syncthreads();
+  }
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= n_ctx) return;
+  const HeadDesc *d = descs[c];
+  const RingState st = d->st;
+  descs[c]->st = ring_after(st, 1, d->cap, d->hyb);
+  encode_row<P, KB, false>(d, st, c, 0, 0, keys, 1, dim, inv_sqrt_p, sqrt_p, s_q4);
+  encode_row<P, VB, false>(d, st, c, 0, 1, vals, 1, dim, inv_sqrt_p, sqrt_p, s_q4);
 }
 
 // Same codec for padded dimensions above 128: identical float steps in the
@@ -510,6 +544,22 @@ hipError_t launch_append(HeadDesc *const *descs, int n_ctx, int dim, int padded,
                          int v_bits, const float *keys, const float *vals, int n_tok,
                          hipStream_t s) {
   if (n_ctx <= 0 || n_tok <= 0) return hipSuccess;
+  if (n_tok == 1 && (padded == 64 || padded == 128)) {
+    // one launch for both sides and the ring states
+    const float sp = sqrtf((float)padded), isp = 1.0f / sp;
+    const dim3 grid((unsigned)((n_ctx + 127) / 128));
+#define AQ_KV(P_, KB_, VB_)                                                                       \
+  if (padded == P_ && k_bits == KB_ && v_bits == VB_) {                                          \
+    append_kv_kernel<P_, KB_, VB_><<<grid, 128, 0, s>>>(descs, n_ctx, keys, vals, dim, isp, sp); \
+    return hipGetLastError();                                                                    \
+  }
+#define AQ_KV_V(P_, KB_) AQ_KV(P_, KB_, 2) AQ_KV(P_, KB_, 3) AQ_KV(P_, KB_, 4) AQ_KV(P_, KB_, 16)
+    AQ_KV_V(64, 2) AQ_KV_V(64, 3) AQ_KV_V(64, 4) AQ_KV_V(64, 16)
+    AQ_KV_V(128, 2) AQ_KV_V(128, 3) AQ_KV_V(128, 4) AQ_KV_V(128, 16)
+#undef AQ_KV_V
+#undef AQ_KV
+    return hipErrorInvalidValue;
+  }
   hipError_t e = hipSuccess;
   const bool fold = padded <= 128 && commit_in_kernel(n_ctx, n_tok);
   for (int side = 0; side < 2 && e == hipSuccess; ++side) {
