@@ -23,8 +23,8 @@
 // tokens, a bitonic sort in the workspace above) and the cut, and turns the
 // selection into per-token weights; a grid over (token chunks, items) sums the
 // weighted V rows; one block per item adds the chunks and applies the inverse
-// FWHT.  Short rings at padded 64 (up to 3,072 tokens) run all four steps in
-// one block per item (sparse_fused_kernel).
+// FWHT.  Short rings (up to 3,072 tokens) run the last three steps in one
+// block per item, at padded 64 the logits too (sparse_fused_kernel).
 #include "launch.hpp"
 
 namespace aq {
@@ -635,18 +635,18 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
   // (the weights in lg are read by sparse_vsum_kernel)
 }
 
-// Short rings at padded 64 (n <= kFusedMax): one block of kSelThreads per item
-// does it all.  The logits are sparse_logits_kernel's (same kdot_row and
+// Short rings (n <= kFusedMax): one block of kSelThreads per item does the
+// selection, the weighted V sum and the inverse FWHT, and at padded 64 the
+// logits too.  The logits are sparse_logits_kernel's (same kdot_row and
 // roundings), the selection is select_small's, so the selected set and the
-// per-token weights are the multi-kernel path's bit for bit; then the block
-// sums the weighted V rows and applies the inverse FWHT, which saves three
-// launches and their global round trips (the V sum's rounding order differs
-// from the multi-kernel path's chunked sums, as both differ from the
-// reference's sorted order).  Measured against the four launches: 4 heads x
-// 2,048 tokens 56 -> 52 us, 256 heads x 2,048 tokens 75 -> 58 us, even at
-// 4,096 tokens; at padded 128 one block per item computing every logit is
-// slower than the logits kernel's many blocks (8 heads x 2,048 tokens 62 ->
-// 80 us), so padded 128 keeps the four launches.
+// per-token weights are the multi-kernel path's bit for bit; the V sum's
+// rounding order differs from the multi-kernel path's chunked sums, as both
+// differ from the reference's sorted order.  Measured against the four
+// launches at padded 64: 4 heads x 2,048 tokens 56 -> 52 us, 256 heads x
+// 2,048 tokens 75 -> 58 us, even at 4,096 tokens.  At padded 128 one block
+// per item computing every logit is slower than the logits kernel's many
+// blocks (8 heads x 2,048 tokens 62 -> 80 us), so there the logits kernel
+// runs first (LOGITS_IN) and the fused kernel takes over from the selection.
 constexpr int kFusedMax = 3 * kSelThreads;
 
 // V row unit read by one lane of the fused kernel: a 32-bit word of 2- or
@@ -667,7 +667,7 @@ __device__ __forceinline__ int vcode_shift(int c) {
   else return 21 - 3 * c;
 }
 
-template <int PT, int KB, int VB>
+template <int PT, int KB, int VB, bool LOGITS_IN>
 __global__ __launch_bounds__(kSelThreads) void sparse_fused_kernel(
     HeadDesc *const *item_desc, const float *__restrict__ queries, float v_mass, float inv_sqrt_p,
     float sqrt_p, float *ws, size_t ws_stride, float *__restrict__ outs) {
@@ -692,19 +692,20 @@ __global__ __launch_bounds__(kSelThreads) void sparse_fused_kernel(
   if (tid < (1 << KB)) s_cbk[tid] = cbv<KB>(tid);
   float *lg = ws + (size_t)item * ws_stride;
   const int s0 = (int)(((long long)d->st.head - n + cap) % cap);
-  rotate_query_exact(s_q, queries + (size_t)item * dim, dim, PT, d->signs, inv_sqrt_p, sqrt_p);
-
-  // logits of the tokens select_small gives this thread (E per thread); each
-  // thread reads back only its own
   const int E = n <= kSelThreads ? 1 : n <= 2 * kSelThreads ? 2 : 4;
-  const float attn_s = 1.0f / (sqrtf((float)dim) * (float)PT);
-  for (int e = 0; e < E; ++e) {
-    const int t = tid * E + e;
-    if (t < n) {
-      const int slot = ring_slot(s0, t, cap);
-      const uint8_t *row = d->k_codes + (size_t)slot * d->k_pb;
-      const float dot = kdot_row<PT, KB>(row, slot & kperm_mask(PT, KB), s_q, PT, s_cbk);
-      lg[t] = __fmul_rn(__fmul_rn(dot, attn_s), d->k_scale[slot]);
+  if constexpr (!LOGITS_IN) {
+    // logits of the tokens select_small gives this thread (E per thread);
+    // each thread reads back only its own
+    rotate_query_exact(s_q, queries + (size_t)item * dim, dim, PT, d->signs, inv_sqrt_p, sqrt_p);
+    const float attn_s = 1.0f / (sqrtf((float)dim) * (float)PT);
+    for (int e = 0; e < E; ++e) {
+      const int t = tid * E + e;
+      if (t < n) {
+        const int slot = ring_slot(s0, t, cap);
+        const uint8_t *row = d->k_codes + (size_t)slot * d->k_pb;
+        const float dot = kdot_row<PT, KB>(row, slot & kperm_mask(PT, KB), s_q, PT, s_cbk);
+        lg[t] = __fmul_rn(__fmul_rn(dot, attn_s), d->k_scale[slot]);
+      }
     }
   }
   if (E == 1) select_small<1>(d, v_mass, lg, n, s0, sh);
@@ -956,11 +957,16 @@ hipError_t launch_decode_sparse(HeadDesc *const *descs, int n_items, const Decod
     float *out = d_out + (size_t)c0 * sh.dim;
     float *w = ws + (size_t)c0 * stride;
     float *parts = parts_all + (size_t)c0 * splits * sh.padded;
-    if (n <= kFusedMax && sh.padded == 64) {
+    const dim3 g1((n + kThreads - 1) / kThreads, cnt);
+    if (n <= kFusedMax && (sh.padded == 64 || sh.padded == 128)) {
+      // padded 128: the logits kernel's many blocks first, then the rest in
+      // one block per item
 #define AQ_FUSED(PT, KB_, VB_)                                                                    \
   if (sh.padded == PT && sh.k_bits == KB_ && sh.v_bits == VB_) {                                  \
-    sparse_fused_kernel<PT, KB_, VB_><<<cnt, kSelThreads, 0, s>>>(dsc, q, v_mass, isp, sp, w,      \
-                                                                   stride, out);                  \
+    if (PT == 128)                                                                                \
+      sparse_logits_kernel<PT, KB_><<<g1, kThreads, 0, s>>>(dsc, q, n, isp, sp, w, stride);        \
+    sparse_fused_kernel<PT, KB_, VB_, PT == 128><<<cnt, kSelThreads, 0, s>>>(dsc, q, v_mass, isp,  \
+                                                                              sp, w, stride, out); \
     const hipError_t fe = hipGetLastError();                                                      \
     if (fe != hipSuccess) return fe;                                                              \
     continue;                                                                                     \
@@ -968,9 +974,11 @@ hipError_t launch_decode_sparse(HeadDesc *const *descs, int n_items, const Decod
       AQ_FUSED(64, 2, 2) AQ_FUSED(64, 2, 3) AQ_FUSED(64, 2, 4)
       AQ_FUSED(64, 3, 2) AQ_FUSED(64, 3, 3) AQ_FUSED(64, 3, 4)
       AQ_FUSED(64, 4, 2) AQ_FUSED(64, 4, 3) AQ_FUSED(64, 4, 4)
+      AQ_FUSED(128, 2, 2) AQ_FUSED(128, 2, 3) AQ_FUSED(128, 2, 4)
+      AQ_FUSED(128, 3, 2) AQ_FUSED(128, 3, 3) AQ_FUSED(128, 3, 4)
+      AQ_FUSED(128, 4, 2) AQ_FUSED(128, 4, 3) AQ_FUSED(128, 4, 4)
 #undef AQ_FUSED
     }
-    const dim3 g1((n + kThreads - 1) / kThreads, cnt);
 #define AQ_LOGITS(PT, KB_) \
   sparse_logits_kernel<PT, KB_><<<g1, kThreads, 0, s>>>(dsc, q, n, isp, sp, w, stride)
     switch (sh.k_bits) {
