@@ -827,30 +827,47 @@ __global__ __launch_bounds__(kThreads) void sparse_vsum_kernel(HeadDesc *const *
   __syncthreads();
   const int t_end = t0 + chunk < n ? t0 + chunk : n;
   const uint8_t *vsrc = d->v_codes;
+  // UNR tokens per step, their weights and code units requested before any
+  // is used (rows of weight 0 still load: the step's loads stay in flight
+  // together)
+  constexpr int UNR = 4;
+  const int step = (kThreads / 64) * TPI;
   if (active) {
-    for (int t = t0 + wave * TPI + sub; t < t_end; t += (kThreads / 64) * TPI) {
-      const float wt = w[t];
-      if (wt == 0.0f) continue;
-      const uint8_t *row = vsrc + (size_t)ring_slot(s0, t, cap) * vpb;
+    for (int t = t0 + wave * TPI + sub; t < t_end; t += UNR * step) {
+      float wt[UNR];
+      uint32_t bits[UNR][kMaxAcc / CPU];
 #pragma unroll
-      for (int r = 0; r < kMaxAcc / CPU; ++r) {
-        if (r >= R) break;
-        const int u = u0 + 64 * r;
-        uint32_t bits;
-        if constexpr (UB == 1) {
-          bits = row[u];
-        } else {
-          // a row of fewer than 8 codes holds a partial group
-          const int b0 = 3 * u;
-          bits = ((uint32_t)row[b0] << 16) | ((b0 + 1 < vpb ? (uint32_t)row[b0 + 1] : 0u) << 8) |
-                 (b0 + 2 < vpb ? (uint32_t)row[b0 + 2] : 0u);
-        }
+      for (int j = 0; j < UNR; ++j) {
+        const int tj = t + j * step;
+        wt[j] = tj < t_end ? w[tj] : 0.0f;
+        const uint8_t *row = vsrc + (size_t)ring_slot(s0, tj < t_end ? tj : t_end - 1, cap) * vpb;
 #pragma unroll
-        for (int c = 0; c < CPU; ++c) {
-          const int code = (int)((bits >> (VB * (CPU - 1 - c))) & ((1u << VB) - 1u));
-          acc[r * CPU + c] = fmaf(s_cb[code], wt, acc[r * CPU + c]);
+        for (int r = 0; r < kMaxAcc / CPU; ++r) {
+          bits[j][r] = 0u;
+          if (r >= R) continue;
+          const int u = u0 + 64 * r;
+          if constexpr (UB == 1) {
+            bits[j][r] = row[u];
+          } else {
+            // a row of fewer than 8 codes holds a partial group
+            const int b0 = 3 * u;
+            bits[j][r] = ((uint32_t)row[b0] << 16) |
+                         ((b0 + 1 < vpb ? (uint32_t)row[b0 + 1] : 0u) << 8) |
+                         (b0 + 2 < vpb ? (uint32_t)row[b0 + 2] : 0u);
+          }
         }
       }
+#pragma unroll
+      for (int j = 0; j < UNR; ++j)
+#pragma unroll
+        for (int r = 0; r < kMaxAcc / CPU; ++r) {
+          if (r >= R) break;
+#pragma unroll
+          for (int c = 0; c < CPU; ++c) {
+            const int code = (int)((bits[j][r] >> (VB * (CPU - 1 - c))) & ((1u << VB) - 1u));
+            acc[r * CPU + c] = fmaf(s_cb[code], wt[j], acc[r * CPU + c]);
+          }
+        }
     }
   }
   // sum the TPI token groups of each wave (lanes u0 + U * sub), then the waves
@@ -890,10 +907,29 @@ __global__ __launch_bounds__(kThreads) void sparse_finish_kernel(HeadDesc *const
   }
   const int used = (n + chunk - 1) / chunk;
   const float *part = partials + (size_t)item * n_splits * P;
-  for (int j = threadIdx.x; j < P; j += blockDim.x) {
+  // the chunks' partial sums: kThreads / P thread groups (P < kThreads) take
+  // every groups-th chunk with several loads in flight, then add up in order
+  __shared__ float s_grp[kThreads];
+  const int groups = P < kThreads ? kThreads / P : 1;
+  if (groups > 1) {
+    const int j = threadIdx.x % P, grp = threadIdx.x / P;
     float a = 0.0f;
-    for (int sp = 0; sp < used; ++sp) a += part[(size_t)sp * P + j];
-    s_acc[j] = a;
+#pragma unroll 8
+    for (int sp = grp; sp < used; sp += groups) a += part[(size_t)sp * P + j];
+    s_grp[threadIdx.x] = a;
+    __syncthreads();
+    if (threadIdx.x < P) {
+      float t = 0.0f;
+      for (int g = 0; g < groups; ++g) t += s_grp[g * P + threadIdx.x];
+      s_acc[threadIdx.x] = t;
+    }
+  } else {
+    for (int j = threadIdx.x; j < P; j += blockDim.x) {
+      float a = 0.0f;
+#pragma unroll 8
+      for (int sp = 0; sp < used; ++sp) a += part[(size_t)sp * P + j];
+      s_acc[j] = a;
+    }
   }
   __syncthreads();
   for (int len = 1; len < P; len <<= 1) {
