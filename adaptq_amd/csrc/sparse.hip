@@ -25,6 +25,8 @@
 // weighted V rows; one block per item adds the chunks and applies the inverse
 // FWHT.  Short rings (up to 3,072 tokens) run the last three steps in one
 // block per item, at padded 64 the logits too (sparse_fused_kernel).
+#include <algorithm>
+
 #include "launch.hpp"
 
 namespace aq {
@@ -343,8 +345,8 @@ __device__ __forceinline__ float block_max(float m, SelectShared &sh) {
 // Exclusive scan of cnt[] (16 x kSelThreads 16-bit counts, digit-major) in
 // place: thread t scans entries 16t .. 16t+15, waves scan the thread totals,
 // the wave totals are added in order.  Counts stay packed two to a word: every
-// prefix is below 2^16 (n <= kLdsSort), so adding base * 0x10001 to a word
-// carries nothing from the low half into the high one.
+// prefix is below 2^16 (at most 65,535 keys), so adding base * 0x10001 to a
+// word carries nothing from the low half into the high one.
 __device__ __forceinline__ void scan_counts(SelectShared &sh) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   uint4 *c4 = reinterpret_cast<uint4 *>(sh.cnt) + 2 * tid;
@@ -523,6 +525,102 @@ __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, fl
   }
 }
 
+// Rings above kLdsSort and up to kRadixMax tokens sort in the workspace:
+// stable LSD radix sort, ascending, of n 32-bit keys with 32-bit payloads,
+// 4 bits a pass, passes skipped for digits every key shares.  Thread t owns
+// the contiguous run [t C, (t + 1) C) of the n keys (C = n / kSelThreads
+// rounded up, at most 64, so its digit counts fit the 8-bit fields), counts
+// its digits, and after the block-wide scan of the counts (scan_counts:
+// prefixes below 2^16) writes its keys in order to their places.  (a, ai)
+// hold the input, (b, bi) are scratch; returns true if the result is in b.
+constexpr int kRadixMax = 65535;
+
+__device__ bool radix_sort_global(uint32_t *a, uint32_t *ai, uint32_t *b, uint32_t *bi, int n,
+                                  SelectShared &sh) {
+  const int tid = threadIdx.x;
+  const int C = (n + kSelThreads - 1) / kSelThreads;
+  const int lo = min(tid * C, n), hi = min(lo + C, n);
+  // the run is read 8 keys at a time, so the loads of a batch are in flight
+  // together
+  constexpr int BT = 8;
+  uint32_t kor = 0, kand = 0xFFFFFFFFu;
+  for (int i0 = lo; i0 < hi; i0 += BT) {
+    uint32_t kk[BT];
+#pragma unroll
+    for (int j = 0; j < BT; ++j) kk[j] = i0 + j < hi ? a[i0 + j] : a[lo];
+#pragma unroll
+    for (int j = 0; j < BT; ++j) {
+      kor |= kk[j];
+      kand &= kk[j];
+    }
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    kor |= __shfl_xor(kor, off);
+    kand &= __shfl_xor(kand, off);
+  }
+  if ((tid & 63) == 0) {
+    sh.wsum[tid >> 6] = kor;
+    reinterpret_cast<uint32_t *>(sh.red)[tid >> 6] = kand;
+  }
+  __syncthreads();
+  uint32_t diff = 0;
+  {
+    uint32_t o = 0, an = 0xFFFFFFFFu;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) {
+      o |= sh.wsum[w];
+      an &= reinterpret_cast<uint32_t *>(sh.red)[w];
+    }
+    diff = o ^ an;
+  }
+  __syncthreads();
+  bool in_b = false;
+  for (int sft = 0; sft < 32; sft += 4) {
+    if (((diff >> sft) & 15u) == 0) continue;
+    const uint32_t *src = in_b ? b : a, *srci = in_b ? bi : ai;
+    uint32_t *dst = in_b ? a : b, *dsti = in_b ? ai : bi;
+    uint64_t c_lo = 0, c_hi = 0;
+    for (int i0 = lo; i0 < hi; i0 += BT) {
+      uint32_t kk[BT];
+#pragma unroll
+      for (int j = 0; j < BT; ++j) kk[j] = i0 + j < hi ? src[i0 + j] : 0u;
+#pragma unroll
+      for (int j = 0; j < BT; ++j) {
+        if (i0 + j >= hi) break;
+        const uint32_t dg = (kk[j] >> sft) & 15u;
+        if (dg < 8u) c_lo += (uint64_t)1 << ((dg & 7u) * 8u);
+        else c_hi += (uint64_t)1 << ((dg & 7u) * 8u);
+      }
+    }
+#pragma unroll
+    for (int dd = 0; dd < 16; ++dd)
+      sh.cnt[dd * kSelThreads + tid] =
+          (uint16_t)(((dd < 8 ? c_lo : c_hi) >> ((dd & 7) * 8)) & 255u);
+    __syncthreads();
+    scan_counts(sh);
+    // this thread's running offsets stay in its own LDS count entries
+    for (int i0 = lo; i0 < hi; i0 += BT) {
+      uint32_t kk[BT], pp[BT];
+#pragma unroll
+      for (int j = 0; j < BT; ++j) {
+        kk[j] = i0 + j < hi ? src[i0 + j] : 0u;
+        pp[j] = i0 + j < hi ? srci[i0 + j] : 0u;
+      }
+#pragma unroll
+      for (int j = 0; j < BT; ++j) {
+        if (i0 + j >= hi) break;
+        const uint32_t dg = (kk[j] >> sft) & 15u;
+        const uint32_t o = sh.cnt[dg * kSelThreads + tid];
+        sh.cnt[dg * kSelThreads + tid] = (uint16_t)(o + 1u);
+        dst[o] = kk[j];
+        dsti[o] = pp[j];
+      }
+    }
+    __syncthreads();
+    in_b = !in_b;
+  }
+  return in_b;
+}
+
 // One block of kSelThreads per item: the sparse-V selection as per-token
 // weights.  n <= kLdsSort: select_small.  Larger n: the same steps with the
 // logits and 64-bit sort keys in the workspace and a bitonic sort there.
@@ -585,10 +683,27 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
   __syncthreads();
   const float inv = s_bcast[0];
 
-  // 3. probabilities, sorted descending (ties: older first)
-  for (int i = tid; i < N; i += blockDim.x) keys[i] = i < n ? make_key(__fmul_rn(lg[i], inv), i) : kPadKey;
-  __syncthreads();
-  bitonic(keys, N);
+  // 3. probabilities, sorted descending (ties: older first): sort keys
+  // (key_hi, token) by a radix sort up to kRadixMax tokens, a bitonic sort of
+  // 64-bit keys above
+  const bool radix = n <= kRadixMax;
+  const uint32_t *kh = nullptr, *ki = nullptr;
+  if (radix) {
+    uint32_t *a = reinterpret_cast<uint32_t *>(lg + sort_cap), *ai = a + n, *b = ai + n, *bi = b + n;
+    for (int i = tid; i < n; i += blockDim.x) {
+      a[i] = key_hi(__fmul_rn(lg[i], inv));
+      ai[i] = (uint32_t)i;
+    }
+    __syncthreads();
+    const bool in_b = radix_sort_global(a, ai, b, bi, n, sh);
+    kh = in_b ? b : a;
+    ki = in_b ? bi : ai;
+  } else {
+    for (int i = tid; i < N; i += blockDim.x) keys[i] = i < n ? make_key(__fmul_rn(lg[i], inv), i) : kPadKey;
+    __syncthreads();
+    bitonic(keys, N);
+  }
+  auto skey = [&](int i) -> uint64_t { return radix ? ((uint64_t)kh[i] << 32) | ki[i] : keys[i]; };
 
   // 4. the cut: whole quads while mass < v_mass, then single tokens
   const int n_quads = n / 4;  // quads with ii + 3 < n
@@ -598,8 +713,9 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
   for (int base = 0; base < n_quads; base += kStage) {
     const int m = n_quads - base < kStage ? n_quads - base : kStage;
     for (int k = tid; k < m; k += blockDim.x) {
-      const uint64_t *q = keys + 4 * (base + k);
-      s_stage[k] = __fadd_rn(__fadd_rn(__fadd_rn(key_p(q[0]), key_p(q[1])), key_p(q[2])), key_p(q[3]));
+      const int q = 4 * (base + k);
+      s_stage[k] = __fadd_rn(__fadd_rn(__fadd_rn(key_p(skey(q)), key_p(skey(q + 1))), key_p(skey(q + 2))),
+                             key_p(skey(q + 3)));
     }
     __syncthreads();
     if (tid == 0 && open) {
@@ -613,9 +729,9 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
     __syncthreads();
   }
   if (tid == 0) {
-    for (; ii < n && mass < v_mass; ++ii) mass = __fadd_rn(mass, key_p(keys[ii]));
+    for (; ii < n && mass < v_mass; ++ii) mass = __fadd_rn(mass, key_p(skey(ii)));
     sh.cut = ii;
-    sh.last = ii > 0 ? keys[ii - 1] : 0;
+    sh.last = ii > 0 ? skey(ii - 1) : 0;
   }
   __syncthreads();
   const int cut = sh.cut;
@@ -958,7 +1074,11 @@ int pow2_at_least(int n) {
 // that follow are aligned), then 2 floats per sort key.
 int keys_at(int n) { return ((n + 32 + 1) / 2) * 2; }
 
-size_t item_stride(int n) { return (size_t)keys_at(n) + 2 * (size_t)pow2_at_least(n); }
+// Sort space: N = 2^k >= n 64-bit keys (bitonic), or two buffers of n
+// 32-bit keys and n 32-bit tokens (radix).
+size_t item_stride(int n) {
+  return (size_t)keys_at(n) + std::max(2 * (size_t)pow2_at_least(n), 4 * (size_t)n);
+}
 
 }  // namespace
 
