@@ -19,13 +19,14 @@
 // reference's std::sort leaves their order unspecified.
 //
 // Kernels: one grid over (token blocks, items) computes the logits; one block
-// per item does softmax, the sort (a stable radix sort in LDS up to 16,384
-// tokens, a bitonic sort in the workspace above) and the cut, and turns the
-// selection into per-token weights; a grid over (token chunks, items) sums the
+// per item does softmax, the sort (a stable radix sort in LDS up to 8,192
+// tokens; above, one device-wide rocPRIM radix sort of every item's keys
+// between that kernel and a cut kernel) and the cut, and turns the selection
+// into per-token weights; a grid over (token chunks, items) sums the
 // weighted V rows; one block per item adds the chunks and applies the inverse
 // FWHT.  Short rings (up to 3,072 tokens) run the last three steps in one
 // block per item, at padded 64 the logits too (sparse_fused_kernel).
-#include <algorithm>
+#include <rocprim/device/device_radix_sort.hpp>
 
 #include "launch.hpp"
 
@@ -35,7 +36,13 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kSelThreads = 1024;
-constexpr int kLdsSort = 16384;  // tokens sorted in LDS (radix); above, in the workspace
+// Rings up to kSelectInBlock tokens are selected inside the select kernel
+// (radix sort in LDS); longer ones sort device-wide between two kernels
+// (measured, 8 heads d128: 12,000 tokens 242 -> 198 us and 16,384 tokens
+// 264 -> 237 us sorted device-wide; at 8,192 tokens and below the in-block
+// sort is as fast or faster).
+constexpr int kSelectInBlock = 8192;
+constexpr int kLdsSort = kSelectInBlock;  // keys the select kernel sorts in LDS
 constexpr int kStage = 4096;    // floats per LDS staging chunk
 
 template <int B>
@@ -217,25 +224,6 @@ __device__ __forceinline__ float hi_p(uint32_t hi) {
 __device__ __forceinline__ float key_p(uint64_t k) { return hi_p((uint32_t)(k >> 32)); }
 __device__ __forceinline__ int key_i(uint64_t k) { return (int)(uint32_t)k; }
 
-// Bitonic sort of N (a power of two) keys ascending; each thread takes whole
-// compare-exchange pairs, so no lane idles on the upper halves.
-__device__ void bitonic(uint64_t *m, int N) {
-  for (int k = 2; k <= N; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      const int lj = __builtin_ctz((unsigned)j);
-      for (int pr = threadIdx.x; pr < N / 2; pr += blockDim.x) {
-        const int i = ((pr >> lj) << (lj + 1)) | (pr & (j - 1));
-        const uint64_t a = m[i], b = m[i + j];
-        const bool up = (i & k) == 0;
-        if (up ? b < a : a < b) {
-          m[i] = b;
-          m[i + j] = a;
-        }
-      }
-      __syncthreads();
-    }
-  }
-}
 
 // acc + s[0] + s[1] + ... + s[m-1], left to right, one lane.  s is 16-byte
 // aligned LDS; two register buffers alternate, so the reads of the next 32
@@ -525,132 +513,46 @@ __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, fl
   }
 }
 
-// Rings above kLdsSort and up to kRadixMax tokens sort in the workspace:
-// stable LSD radix sort, ascending, of n 32-bit keys with 32-bit payloads,
-// 4 bits a pass, passes skipped for digits every key shares.  Thread t owns
-// the contiguous run [t C, (t + 1) C) of the n keys (C = n / kSelThreads
-// rounded up, at most 64, so its digit counts fit the 8-bit fields), counts
-// its digits, and after the block-wide scan of the counts (scan_counts:
-// prefixes below 2^16) writes its keys in order to their places.  (a, ai)
-// hold the input, (b, bi) are scratch; returns true if the result is in b.
-constexpr int kRadixMax = 65535;
-
-__device__ bool radix_sort_global(uint32_t *a, uint32_t *ai, uint32_t *b, uint32_t *bi, int n,
-                                  SelectShared &sh) {
-  const int tid = threadIdx.x;
-  const int C = (n + kSelThreads - 1) / kSelThreads;
-  const int lo = min(tid * C, n), hi = min(lo + C, n);
-  // the run is read 8 keys at a time, so the loads of a batch are in flight
-  // together
-  constexpr int BT = 8;
-  uint32_t kor = 0, kand = 0xFFFFFFFFu;
-  for (int i0 = lo; i0 < hi; i0 += BT) {
-    uint32_t kk[BT];
-#pragma unroll
-    for (int j = 0; j < BT; ++j) kk[j] = i0 + j < hi ? a[i0 + j] : a[lo];
-#pragma unroll
-    for (int j = 0; j < BT; ++j) {
-      kor |= kk[j];
-      kand &= kk[j];
-    }
-  }
-  for (int off = 32; off > 0; off >>= 1) {
-    kor |= __shfl_xor(kor, off);
-    kand &= __shfl_xor(kand, off);
-  }
-  if ((tid & 63) == 0) {
-    sh.wsum[tid >> 6] = kor;
-    reinterpret_cast<uint32_t *>(sh.red)[tid >> 6] = kand;
-  }
-  __syncthreads();
-  uint32_t diff = 0;
-  {
-    uint32_t o = 0, an = 0xFFFFFFFFu;
-    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) {
-      o |= sh.wsum[w];
-      an &= reinterpret_cast<uint32_t *>(sh.red)[w];
-    }
-    diff = o ^ an;
-  }
-  __syncthreads();
-  bool in_b = false;
-  for (int sft = 0; sft < 32; sft += 4) {
-    if (((diff >> sft) & 15u) == 0) continue;
-    const uint32_t *src = in_b ? b : a, *srci = in_b ? bi : ai;
-    uint32_t *dst = in_b ? a : b, *dsti = in_b ? ai : bi;
-    uint64_t c_lo = 0, c_hi = 0;
-    for (int i0 = lo; i0 < hi; i0 += BT) {
-      uint32_t kk[BT];
-#pragma unroll
-      for (int j = 0; j < BT; ++j) kk[j] = i0 + j < hi ? src[i0 + j] : 0u;
-#pragma unroll
-      for (int j = 0; j < BT; ++j) {
-        if (i0 + j >= hi) break;
-        const uint32_t dg = (kk[j] >> sft) & 15u;
-        if (dg < 8u) c_lo += (uint64_t)1 << ((dg & 7u) * 8u);
-        else c_hi += (uint64_t)1 << ((dg & 7u) * 8u);
-      }
-    }
-#pragma unroll
-    for (int dd = 0; dd < 16; ++dd)
-      sh.cnt[dd * kSelThreads + tid] =
-          (uint16_t)(((dd < 8 ? c_lo : c_hi) >> ((dd & 7) * 8)) & 255u);
-    __syncthreads();
-    scan_counts(sh);
-    // this thread's running offsets stay in its own LDS count entries
-    for (int i0 = lo; i0 < hi; i0 += BT) {
-      uint32_t kk[BT], pp[BT];
-#pragma unroll
-      for (int j = 0; j < BT; ++j) {
-        kk[j] = i0 + j < hi ? src[i0 + j] : 0u;
-        pp[j] = i0 + j < hi ? srci[i0 + j] : 0u;
-      }
-#pragma unroll
-      for (int j = 0; j < BT; ++j) {
-        if (i0 + j >= hi) break;
-        const uint32_t dg = (kk[j] >> sft) & 15u;
-        const uint32_t o = sh.cnt[dg * kSelThreads + tid];
-        sh.cnt[dg * kSelThreads + tid] = (uint16_t)(o + 1u);
-        dst[o] = kk[j];
-        dsti[o] = pp[j];
-      }
-    }
-    __syncthreads();
-    in_b = !in_b;
-  }
-  return in_b;
-}
-
 // One block of kSelThreads per item: the sparse-V selection as per-token
-// weights.  n <= kLdsSort: select_small.  Larger n: the same steps with the
-// logits and 64-bit sort keys in the workspace and a bitonic sort there.
+// weights.  n <= kSelectInBlock: select_small, all of it.  Larger n (keys != null):
+// the first of three steps.  This kernel takes the max, the exponentials and
+// their left-to-right sum (inv = 1/sum is kept at lg[n]) and writes the sort
+// keys (slot << 32) | key_hi(p), with the token as payload, into the item's
+// slot of S entries in a launch-wide array (padding: key_hi = ~0, after
+// everything); one device-wide stable radix sort of all slots (rocPRIM) puts
+// each item's keys in order inside its slot, p descending, ties older first;
+// sparse_cut_kernel then takes the cut and writes the weights.  Items at or
+// below kSelectInBlock in a launch that sorts fill their slot with padding.
 // sparse_vsum_kernel then sums the weighted V rows over many blocks and
 // sparse_finish_kernel applies the inverse FWHT.  The V sum runs in token
 // order instead of the reference's sorted order, which changes only its
 // rounding; the selected set is the reference's.
 __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *const *item_desc,
                                                                     float v_mass, float *ws,
-                                                                    size_t ws_stride,
-                                                                    int sort_cap) {
+                                                                    size_t ws_stride, int S,
+                                                                    uint64_t *keys, uint32_t *toks) {
   __shared__ SelectShared sh;
   const int item = blockIdx.x;
   const int tid = threadIdx.x;
   const HeadDesc *d = item_desc[item];
-  const int n = d->st.size, cap = d->cap, P = d->padded;
+  const int n = d->st.size, cap = d->cap;
+  const uint64_t slot_hi = (uint64_t)item << 32;
+  if (keys && n <= kSelectInBlock) {
+    for (int i = tid; i < S; i += blockDim.x) {
+      keys[(size_t)item * S + i] = slot_hi | 0xFFFFFFFFu;
+      toks[(size_t)item * S + i] = 0u;
+    }
+  }
   if (n == 0) return;
   float *lg = ws + (size_t)item * ws_stride;
   const int s0 = (int)(((long long)d->st.head - n + cap) % cap);
-  if (n <= kLdsSort) {
+  if (n <= kSelectInBlock) {
     if (n <= kSelThreads) select_small<1>(d, v_mass, lg, n, s0, sh);
     else if (n <= 2 * kSelThreads) select_small<2>(d, v_mass, lg, n, s0, sh);
     else if (n <= 4 * kSelThreads) select_small<4>(d, v_mass, lg, n, s0, sh);
-    else if (n <= 8 * kSelThreads) select_small<8>(d, v_mass, lg, n, s0, sh);
-    else select_small<16>(d, v_mass, lg, n, s0, sh);
+    else select_small<8>(d, v_mass, lg, n, s0, sh);
     return;
   }
-  int N = 1;
-  while (N < n) N <<= 1;
-  uint64_t *keys = reinterpret_cast<uint64_t *>(lg + sort_cap);
   float *s_stage = sh.stage, *s_red = sh.red, *s_bcast = sh.bcast;
 
   // 1. max with the reference's starting value and NaN-skipping compare
@@ -682,28 +584,37 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
   if (tid == 0) s_bcast[0] = 1.0f / sv;
   __syncthreads();
   const float inv = s_bcast[0];
+  if (tid == 0) lg[n] = inv;
 
-  // 3. probabilities, sorted descending (ties: older first): sort keys
-  // (key_hi, token) by a radix sort up to kRadixMax tokens, a bitonic sort of
-  // 64-bit keys above
-  const bool radix = n <= kRadixMax;
-  const uint32_t *kh = nullptr, *ki = nullptr;
-  if (radix) {
-    uint32_t *a = reinterpret_cast<uint32_t *>(lg + sort_cap), *ai = a + n, *b = ai + n, *bi = b + n;
-    for (int i = tid; i < n; i += blockDim.x) {
-      a[i] = key_hi(__fmul_rn(lg[i], inv));
-      ai[i] = (uint32_t)i;
-    }
-    __syncthreads();
-    const bool in_b = radix_sort_global(a, ai, b, bi, n, sh);
-    kh = in_b ? b : a;
-    ki = in_b ? bi : ai;
-  } else {
-    for (int i = tid; i < N; i += blockDim.x) keys[i] = i < n ? make_key(__fmul_rn(lg[i], inv), i) : kPadKey;
-    __syncthreads();
-    bitonic(keys, N);
+  // 3. sort keys and tokens into the item's slot
+  for (int i = tid; i < S; i += blockDim.x) {
+    keys[(size_t)item * S + i] = slot_hi | (i < n ? key_hi(__fmul_rn(lg[i], inv)) : 0xFFFFFFFFu);
+    toks[(size_t)item * S + i] = (uint32_t)i;
   }
-  auto skey = [&](int i) -> uint64_t { return radix ? ((uint64_t)kh[i] << 32) | ki[i] : keys[i]; };
+}
+
+// The cut and the weights of an item above kSelectInBlock tokens, over its sorted
+// slot (keys: slot << 32 | key_hi, toks: tokens).
+__global__ __launch_bounds__(kSelThreads) void sparse_cut_kernel(HeadDesc *const *item_desc,
+                                                                 float v_mass, float *ws,
+                                                                 size_t ws_stride, int S,
+                                                                 const uint64_t *keys,
+                                                                 const uint32_t *toks) {
+  __shared__ float s_stage[kStage];
+  __shared__ float s_bcast[2];
+  __shared__ int s_cut;
+  __shared__ uint64_t s_last;
+  const int item = blockIdx.x;
+  const int tid = threadIdx.x;
+  const HeadDesc *d = item_desc[item];
+  const int n = d->st.size, cap = d->cap, P = d->padded;
+  if (n <= kSelectInBlock) return;  // select_small wrote its weights
+  float *lg = ws + (size_t)item * ws_stride;
+  const int s0 = (int)(((long long)d->st.head - n + cap) % cap);
+  const float inv = lg[n];
+  const uint64_t *kk = keys + (size_t)item * S;
+  const uint32_t *tt = toks + (size_t)item * S;
+  auto skey = [&](int i) -> uint64_t { return ((uint64_t)(uint32_t)kk[i] << 32) | tt[i]; };
 
   // 4. the cut: whole quads while mass < v_mass, then single tokens
   const int n_quads = n / 4;  // quads with ii + 3 < n
@@ -730,12 +641,12 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
   }
   if (tid == 0) {
     for (; ii < n && mass < v_mass; ++ii) mass = __fadd_rn(mass, key_p(skey(ii)));
-    sh.cut = ii;
-    sh.last = ii > 0 ? skey(ii - 1) : 0;
+    s_cut = ii;
+    s_last = ii > 0 ? skey(ii - 1) : 0;
   }
   __syncthreads();
-  const int cut = sh.cut;
-  const uint64_t last = sh.last;
+  const int cut = s_cut;
+  const uint64_t last = s_last;
 
   // 5. per-token weights in natural order: the selection is the cut first
   // keys of the sorted order, i.e. every key up to the last one taken (keys
@@ -747,8 +658,6 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
                 ? __fmul_rn(__fmul_rn(p, d->v_scale[ring_slot(s0, t, cap)]), isp)
                 : 0.0f;
   }
-
-  // (the weights in lg are read by sparse_vsum_kernel)
 }
 
 // Short rings (n <= kFusedMax): one block of kSelThreads per item does the
@@ -1064,20 +973,37 @@ __global__ __launch_bounds__(kThreads) void sparse_finish_kernel(HeadDesc *const
   }
 }
 
-int pow2_at_least(int n) {
-  int p = 1;
-  while (p < n) p <<= 1;
-  return p;
+// Per item: the logits, then the probabilities, then the weights (n floats),
+// and 1/sum at [n] for rings that sort outside the select kernel.
+size_t item_stride(int n) { return (size_t)n + 4; }
+
+// Items per launch: the grid holds items in one dimension (at most 65,535).
+constexpr int kMaxItems = 65535;
+
+// Launch-wide sort of rings above kSelectInBlock: chunk items' slots of S keys
+// (64-bit) and tokens (32-bit), in and out, then rocPRIM's scratch.
+struct SortSpace {
+  size_t keys_floats, toks_floats, temp_bytes, floats;
+};
+
+int item_bits(int cnt) {
+  int b = 0;
+  while ((1 << b) < cnt) ++b;
+  return b;
 }
 
-// Per item: logits/probabilities (keys_at floats, even so the 8-byte sort keys
-// that follow are aligned), then 2 floats per sort key.
-int keys_at(int n) { return ((n + 32 + 1) / 2) * 2; }
+size_t align64(size_t x) { return (x + 63) & ~(size_t)63; }
 
-// Sort space: N = 2^k >= n 64-bit keys (bitonic), or two buffers of n
-// 32-bit keys and n 32-bit tokens (radix).
-size_t item_stride(int n) {
-  return (size_t)keys_at(n) + std::max(2 * (size_t)pow2_at_least(n), 4 * (size_t)n);
+SortSpace sort_space(int cnt, int S) {
+  SortSpace sp{};
+  const size_t m = (size_t)cnt * S;
+  sp.keys_floats = align64(2 * m);
+  sp.toks_floats = align64(m);
+  (void)rocprim::radix_sort_pairs(nullptr, sp.temp_bytes, (const uint64_t *)nullptr,
+                                  (uint64_t *)nullptr, (const uint32_t *)nullptr,
+                                  (uint32_t *)nullptr, m, 0u, 32u + (unsigned)item_bits(cnt));
+  sp.floats = 2 * sp.keys_floats + 2 * sp.toks_floats + align64((sp.temp_bytes + 3) / 4);
+  return sp;
 }
 
 }  // namespace
@@ -1089,7 +1015,9 @@ int vsum_splits(int n) { return (n + kVChunk - 1) / kVChunk; }
 
 size_t sparse_workspace_floats(int n_items, const DecodeShape &sh) {
   const int n = sh.max_n > 0 ? sh.max_n : 1;
-  return (size_t)n_items * item_stride(n) + (size_t)n_items * vsum_splits(n) * sh.padded;
+  size_t f = align64((size_t)n_items * item_stride(n) + (size_t)n_items * vsum_splits(n) * sh.padded);
+  if (n > kSelectInBlock) f += sort_space(n_items < kMaxItems ? n_items : kMaxItems, n).floats;
+  return f;
 }
 
 hipError_t launch_decode_sparse(HeadDesc *const *descs, int n_items, const DecodeShape &sh,
@@ -1098,14 +1026,13 @@ hipError_t launch_decode_sparse(HeadDesc *const *descs, int n_items, const Decod
   if (n_items <= 0) return hipSuccess;
   const int n = sh.max_n > 0 ? sh.max_n : 1;
   const size_t stride = item_stride(n);
-  const int sort_cap = keys_at(n);
   const float sp = sqrtf((float)sh.padded);
   const float isp = 1.0f / sp;
   const int splits = vsum_splits(n);
   float *parts_all = ws + (size_t)n_items * stride;
+  float *sort_base = ws + align64((size_t)n_items * stride + (size_t)n_items * splits * sh.padded);
   // items go in the grid's y dimension (at most 65,535 per launch); chunks of
   // items take consecutive queries, outputs and workspace
-  constexpr int kMaxItems = 65535;
   for (int c0 = 0; c0 < n_items; c0 += kMaxItems) {
     const int cnt = n_items - c0 < kMaxItems ? n_items - c0 : kMaxItems;
     HeadDesc *const *dsc = descs + c0;
@@ -1158,9 +1085,30 @@ hipError_t launch_decode_sparse(HeadDesc *const *descs, int n_items, const Decod
 #undef AQ_LOGITS
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    sparse_select_kernel<<<cnt, kSelThreads, 0, s>>>(dsc, v_mass, w, stride, sort_cap);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (n <= kSelectInBlock) {
+      sparse_select_kernel<<<cnt, kSelThreads, 0, s>>>(dsc, v_mass, w, stride, 0, nullptr, nullptr);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    } else {
+      // slots of S = n keys per item; the chunk's layout as sized by
+      // sparse_workspace_floats (for the largest chunk)
+      const SortSpace ss = sort_space(cnt, n);
+      uint64_t *k_in = reinterpret_cast<uint64_t *>(sort_base);
+      uint64_t *k_out = reinterpret_cast<uint64_t *>(sort_base + ss.keys_floats);
+      uint32_t *t_in = reinterpret_cast<uint32_t *>(sort_base + 2 * ss.keys_floats);
+      uint32_t *t_out = reinterpret_cast<uint32_t *>(sort_base + 2 * ss.keys_floats + ss.toks_floats);
+      void *temp = sort_base + 2 * ss.keys_floats + 2 * ss.toks_floats;
+      sparse_select_kernel<<<cnt, kSelThreads, 0, s>>>(dsc, v_mass, w, stride, n, k_in, t_in);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      size_t temp_bytes = ss.temp_bytes;
+      e = rocprim::radix_sort_pairs(temp, temp_bytes, k_in, k_out, t_in, t_out, (size_t)cnt * n, 0u,
+                                    32u + (unsigned)item_bits(cnt), s);
+      if (e != hipSuccess) return e;
+      sparse_cut_kernel<<<cnt, kSelThreads, 0, s>>>(dsc, v_mass, w, stride, n, k_out, t_out);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
     const dim3 g3(splits, cnt);
     switch (sh.v_bits) {
       case 2: sparse_vsum_kernel<2><<<g3, kThreads, 0, s>>>(dsc, w, stride, kVChunk, splits, parts); break;
