@@ -557,7 +557,8 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
 
   // 1. max with the reference's starting value and NaN-skipping compare
   float mx = -1e30f;
-  for (int i = tid; i < n; i += blockDim.x)
+#pragma unroll 8
+  for (int i = tid; i < n; i += kSelThreads)
     if (lg[i] > mx) mx = lg[i];
   s_red[tid] = mx;
   __syncthreads();
@@ -587,7 +588,8 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
   if (tid == 0) lg[n] = inv;
 
   // 3. sort keys and tokens into the item's slot
-  for (int i = tid; i < S; i += blockDim.x) {
+#pragma unroll 8
+  for (int i = tid; i < S; i += kSelThreads) {
     keys[(size_t)item * S + i] = slot_hi | (i < n ? key_hi(__fmul_rn(lg[i], inv)) : 0xFFFFFFFFu);
     toks[(size_t)item * S + i] = (uint32_t)i;
   }
@@ -652,11 +654,23 @@ __global__ __launch_bounds__(kSelThreads) void sparse_cut_kernel(HeadDesc *const
   // keys of the sorted order, i.e. every key up to the last one taken (keys
   // are distinct); p_t is recomputed exactly as the key was made
   const float isp = 1.0f / sqrtf((float)P);
-  for (int t = tid; t < n; t += blockDim.x) {
-    const float p = __fmul_rn(lg[t], inv);
-    lg[t] = cut > 0 && make_key(p, t) <= last
-                ? __fmul_rn(__fmul_rn(p, d->v_scale[ring_slot(s0, t, cap)]), isp)
-                : 0.0f;
+  constexpr int BT = 8;  // tokens per thread whose loads are in flight together
+  for (int t0 = tid; t0 < n; t0 += BT * kSelThreads) {
+    float lv[BT], vs[BT];
+#pragma unroll
+    for (int j = 0; j < BT; ++j) {
+      const int t = t0 + j * kSelThreads;
+      lv[j] = t < n ? lg[t] : 0.0f;
+      vs[j] = t < n ? d->v_scale[ring_slot(s0, t, cap)] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < BT; ++j) {
+      const int t = t0 + j * kSelThreads;
+      if (t < n) {
+        const float p = __fmul_rn(lv[j], inv);
+        lg[t] = cut > 0 && make_key(p, t) <= last ? __fmul_rn(__fmul_rn(p, vs[j]), isp) : 0.0f;
+      }
+    }
   }
 }
 
