@@ -41,6 +41,7 @@ SIGNATURES = {
     "adaptq_flush": (C.c_int, [C.c_void_p]),
     "adaptq_ring_info": (C.c_int, [C.c_void_p, _ip, _ip, _ip, _ip, _ip, _ip]),
     "adaptq_read_slots": (C.c_int, [C.c_void_p, C.c_int, C.c_int, _u8, _u8, _f, _f]),
+    "adaptq_sparse_weights": (C.c_int, [C.c_void_p, _f, _f]),
     "adaptq_mha_head": (C.c_void_p, [C.c_void_p, C.c_int]),
     "adaptq_mha_append_all": (C.c_int, [C.c_void_p, _f, _f, C.c_int]),
     "adaptq_mha_compute_all": (C.c_int, [C.c_void_p, _f, _f]),

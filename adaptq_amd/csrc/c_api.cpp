@@ -14,6 +14,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -69,27 +70,224 @@ int next_pow2(int n) {
 
 bool valid_bits(int b) { return b == 16 || (b >= 2 && b <= 4); }
 
-// One library stream per device (default priority).
-std::mutex g_stream_mu;
-hipStream_t g_streams[64];
+// ---- Stream ordering ----
+//
+// Work on a context's ring is queued on two kinds of streams: the library's
+// own stream per device (host-form calls: flushes of staged rows, host
+// compute, reset) and callers' streams (the *_device entry points).  They are
+// ordered on the device, without the host waiting.  The library stream is a
+// blocking stream, so the HIP null stream (NULL, torch's default stream) and
+// it wait for each other's earlier work by themselves; for any other caller
+// stream:
+//   * after a device-form launch, an event is recorded on the caller's stream
+//     (one event per caller stream and device);
+//   * before library-stream work, the library stream waits on every caller
+//     event recorded since its previous such wait;
+//   * before a device-form launch, the caller's stream waits on an event
+//     recorded after the library stream's latest work, unless the host has
+//     already seen that work complete.
+// Library-stream submissions are numbered per device; `done` is the highest
+// number the host has seen complete, so host waits (outputs of host-form
+// calls, reuse of pinned staging memory, inspection) happen only when the
+// work they need may still be running.  Device-form calls on different
+// caller streams that touch the same contexts are ordered by the caller, as
+// for any stream-taking library call.
+constexpr int kMaxDevices = 64;
+constexpr int kMaxCallerStreams = 16;
 
-hipStream_t lib_stream(int dev) {
-  std::lock_guard<std::mutex> g(g_stream_mu);
-  if (dev < 0 || dev >= 64) return nullptr;
-  if (!g_streams[dev]) {
-    hipStream_t s = nullptr;
-    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return nullptr;
-    g_streams[dev] = s;
+struct DevSync {
+  std::mutex mu;
+  hipStream_t lib = nullptr;
+  hipEvent_t lib_ev = nullptr;
+  uint64_t enq = 0;        // library-stream submissions so far
+  uint64_t done = 0;       // submissions the host has seen complete
+  uint64_t lib_ev_at = 0;  // submission count when lib_ev was recorded
+  struct Caller {
+    hipStream_t s;
+    hipEvent_t ev;
+    bool fresh;  // recorded, not yet waited on by the library stream
+  };
+  Caller caller[kMaxCallerStreams];
+  int n_caller = 0;
+  int evict = 0;
+};
+
+DevSync g_dev[kMaxDevices];
+
+DevSync *dev_sync(int dev) { return dev >= 0 && dev < kMaxDevices ? &g_dev[dev] : nullptr; }
+
+// Caller holds d->mu; dev is the current device.
+hipError_t ensure_lib(DevSync *d) {
+  if (d->lib) return hipSuccess;
+  hipStream_t s = nullptr;
+  // blocking (synchronises with the null stream), default priority
+  hipError_t e = hipStreamCreateWithFlags(&s, hipStreamDefault);
+  if (e != hipSuccess) return e;
+  hipEvent_t ev = nullptr;
+  e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+  if (e != hipSuccess) {
+    (void)hipStreamDestroy(s);
+    return e;
   }
-  return g_streams[dev];
+  d->lib = s;
+  d->lib_ev = ev;
+  return hipSuccess;
 }
+
+// Caller holds d->mu: the library stream waits on every fresh caller event.
+hipError_t wait_callers(DevSync *d) {
+  bool any = false;
+  for (int i = 0; i < d->n_caller; ++i) {
+    DevSync::Caller &c = d->caller[i];
+    if (!c.fresh) continue;
+    const hipError_t e = hipStreamWaitEvent(d->lib, c.ev, 0);
+    if (e != hipSuccess) return e;
+    c.fresh = false;
+    any = true;
+  }
+  if (any) ++d->enq;  // the wait is library-stream work the host may need to see done
+  return hipSuccess;
+}
+
+// Before queueing library-stream work for a context on the current device:
+// returns the library stream, which now waits for callers' queued work.
+hipError_t lib_begin(int dev, hipStream_t *out) {
+  DevSync *d = dev_sync(dev);
+  if (!d) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> g(d->mu);
+  hipError_t e = ensure_lib(d);
+  if (e == hipSuccess) e = wait_callers(d);
+  *out = d->lib;
+  return e;
+}
+
+// After queueing library-stream work: its submission number.
+uint64_t lib_end(int dev) {
+  DevSync *d = dev_sync(dev);
+  std::lock_guard<std::mutex> g(d->mu);
+  return ++d->enq;
+}
+
+// The host waits until library-stream submission `upto` has completed.
+hipError_t lib_wait(int dev, uint64_t upto) {
+  DevSync *d = dev_sync(dev);
+  if (!d) return hipErrorInvalidDevice;
+  hipStream_t s;
+  uint64_t target;
+  {
+    std::lock_guard<std::mutex> g(d->mu);
+    if (d->done >= upto || !d->lib) return hipSuccess;
+    s = d->lib;
+    target = d->enq;
+  }
+  const hipError_t e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> g(d->mu);
+  if (d->done < target) d->done = target;
+  return hipSuccess;
+}
+
+// Everything queued for the device so far -- library stream and callers'
+// device-form launches -- has completed when this returns (inspection,
+// snapshots, destruction).
+hipError_t settle(int dev) {
+  DevSync *d = dev_sync(dev);
+  if (!d) return hipErrorInvalidDevice;
+  uint64_t target;
+  {
+    std::lock_guard<std::mutex> g(d->mu);
+    hipError_t e = ensure_lib(d);
+    if (e == hipSuccess) e = wait_callers(d);
+    if (e != hipSuccess) return e;
+    target = d->enq;
+  }
+  return lib_wait(dev, target);
+}
+
+// The legacy null stream (NULL or hipStreamLegacy) and the blocking library
+// stream order each other's work implicitly.
+bool is_null_stream(hipStream_t s) { return s == nullptr || s == hipStreamLegacy; }
+
+bool capturing(hipStream_t s) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(s, &st) == hipSuccess && st == hipStreamCaptureStatusActive;
+}
+
+// Before a device-form launch on caller stream s: s waits for the library
+// stream's work that may still be running.  Under graph capture the host
+// waits instead (an event from outside the capture cannot be waited on).
+hipError_t caller_begin(int dev, hipStream_t s) {
+  if (is_null_stream(s)) return hipSuccess;  // it waits for the blocking library stream
+  DevSync *d = dev_sync(dev);
+  if (!d) return hipErrorInvalidDevice;
+  uint64_t target = 0;
+  {
+    std::lock_guard<std::mutex> g(d->mu);
+    if (d->enq <= d->done) return hipSuccess;
+    if (!capturing(s)) {
+      if (d->lib_ev_at < d->enq) {
+        const hipError_t e = hipEventRecord(d->lib_ev, d->lib);
+        if (e != hipSuccess) return e;
+        d->lib_ev_at = d->enq;
+      }
+      return hipStreamWaitEvent(s, d->lib_ev, 0);
+    }
+    target = d->enq;
+  }
+  return lib_wait(dev, target);
+}
+
+// After a device-form launch on caller stream s: record it for the library
+// stream to wait on.  Launches captured into a graph run at replay, outside
+// this bookkeeping.
+hipError_t caller_end(int dev, hipStream_t s) {
+  if (is_null_stream(s)) return hipSuccess;  // later library-stream work waits for it
+  DevSync *d = dev_sync(dev);
+  if (!d) return hipErrorInvalidDevice;
+  if (capturing(s)) return hipSuccess;
+  std::lock_guard<std::mutex> g(d->mu);
+  DevSync::Caller *c = nullptr;
+  for (int i = 0; i < d->n_caller && !c; ++i)
+    if (d->caller[i].s == s) c = &d->caller[i];
+  if (!c) {
+    if (d->n_caller < kMaxCallerStreams) {
+      c = &d->caller[d->n_caller];
+      hipError_t e = hipEventCreateWithFlags(&c->ev, hipEventDisableTiming);
+      if (e != hipSuccess) return e;
+      ++d->n_caller;
+    } else {
+      // reuse the slot of another stream once the library stream has
+      // waited on what it recorded
+      c = &d->caller[d->evict];
+      d->evict = (d->evict + 1) % kMaxCallerStreams;
+      if (c->fresh) {
+        hipError_t e = ensure_lib(d);
+        if (e == hipSuccess) e = hipStreamWaitEvent(d->lib, c->ev, 0);
+        if (e != hipSuccess) return e;
+        ++d->enq;
+      }
+    }
+    c->s = s;
+    c->fresh = false;
+  }
+  const hipError_t e = hipEventRecord(c->ev, s);
+  if (e == hipSuccess) c->fresh = true;
+  return e;
+}
+
+// Any change to a context's host-visible ring state (staged rows, appends,
+// resets, loads) moves this counter; a plan whose contexts have not changed
+// since its last scan skips the scan.
+std::atomic<uint64_t> g_epoch{1};
+
+void bump_epoch() { g_epoch.fetch_add(1, std::memory_order_acq_rel); }
 
 struct DevBuf {
   void *p = nullptr;
   size_t bytes = 0;
   hipError_t ensure(size_t need) {
     if (need <= bytes) return hipSuccess;
-    if (p) (void)hipFree(p);
+    if (p) (void)hipFree(p);  // hipFree waits for the device: no kernel still uses it
     p = nullptr;
     bytes = 0;
     size_t want = std::max(need, (size_t)4096);
@@ -148,6 +346,7 @@ struct Ctx {
   int dim = 0, padded = 0, k_bits = 0, v_bits = 0, cap = 0, hyb = 0, k_pb = 0, v_pb = 0;
   float v_mass = 0.f;
   aq::RingState st{0, 0, 0, 0};
+  aq::HeadDesc hd{};  // host copy of the device descriptor's pointers and config
   void *slab = nullptr;
   aq::HeadDesc *d_desc = nullptr;
   aq::HeadDesc **d_desc_list = nullptr;  // one entry: d_desc
@@ -155,7 +354,7 @@ struct Ctx {
   int staged = 0;
   DevBuf d_stage, d_ws, d_items;
   PinnedBuf h_stage, h_io;  // staged rows for the append kernel; queries and outputs
-  bool pending = false;     // an append launch may still read h_stage
+  uint64_t stage_seq = 0;   // library-stream submission that last read h_stage
   int items_uploaded = 0;
 };
 
@@ -169,24 +368,36 @@ struct Mha {
   int rep_n = 0;  // reps held in d_rep
   DevBuf d_ws, d_io, d_stage;
   PinnedBuf h_stage, h_io;
-  bool pending = false;  // an append launch may still read h_stage
+  uint64_t stage_seq = 0;  // library-stream submission that last read h_stage
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+struct DeviceGuard {
+  int prev = -1;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (prev != dev) (void)hipSetDevice(dev);
+  }
+  ~DeviceGuard() {
+    int cur = -1;
+    (void)hipGetDevice(&cur);
+    if (prev >= 0 && cur != prev) (void)hipSetDevice(prev);
+  }
+};
+
 void free_ctx(Ctx *c) {
   if (!c) return;
-  int cur = 0;
-  (void)hipGetDevice(&cur);
-  (void)hipSetDevice(c->device);
-  if (c->pending) (void)hipStreamSynchronize(lib_stream(c->device));
-  if (c->slab) (void)hipFree(c->slab);
-  c->d_stage.release();
-  c->d_ws.release();
-  c->d_items.release();
-  c->h_stage.release();
-  c->h_io.release();
-  (void)hipSetDevice(cur);
+  {
+    DeviceGuard g(c->device);
+    (void)settle(c->device);  // no queued kernel may still use the slab or the pinned rows
+    if (c->slab) (void)hipFree(c->slab);
+    c->d_stage.release();
+    c->d_ws.release();
+    c->d_items.release();
+    c->h_stage.release();
+    c->h_io.release();
+  }
   delete c;
 }
 
@@ -202,7 +413,7 @@ Ctx *create_ctx(int dim, int k_bits, int v_bits, int capacity, uint64_t seed, fl
     set_errorf(fn, "host allocation failed");
     return nullptr;
   }
-  if (hipGetDevice(&c->device) != hipSuccess) {
+  if (hipGetDevice(&c->device) != hipSuccess || c->device < 0 || c->device >= kMaxDevices) {
     delete c;
     set_errorf(fn, "no HIP device available");
     return nullptr;
@@ -259,7 +470,7 @@ Ctx *create_ctx(int dim, int k_bits, int v_bits, int capacity, uint64_t seed, fl
     return nullptr;
   }
   uint8_t *base = static_cast<uint8_t *>(c->slab);
-  aq::HeadDesc h{};
+  aq::HeadDesc &h = c->hd;
   h.k_codes = base + o_kc;
   h.v_codes = base + o_vc;
   h.k_scale = reinterpret_cast<float *>(base + o_ks);
@@ -300,61 +511,42 @@ Ctx *create_ctx(int dim, int k_bits, int v_bits, int capacity, uint64_t seed, fl
   return c;
 }
 
-struct DeviceGuard {
-  int prev = -1;
-  explicit DeviceGuard(int dev) {
-    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
-    if (prev != dev) (void)hipSetDevice(dev);
-  }
-  ~DeviceGuard() {
-    int cur = -1;
-    (void)hipGetDevice(&cur);
-    if (prev >= 0 && cur != prev) (void)hipSetDevice(prev);
-  }
-};
-
 // Quantise the staged tokens (caller holds c->mu), on the library stream.
 // The rows go through pinned memory (the kernel reads small batches from it
-// directly) and the call does not wait for the kernel unless sync: the next
-// flush waits before it reuses the pinned rows, and compute waits at its end.
-// sync = true (inspection, snapshots, device-form calls on other streams)
-// also waits for work already queued for this context (c->pending: set by
-// any flush that touched it).
-bool flush_locked(Ctx *c, const char *fn, bool sync = true) {
-  if (c->staged == 0 && !(sync && c->pending)) return true;
+// directly) and the call does not wait for the kernel: the next flush waits
+// before it reuses the pinned rows, and compute waits for its own outputs.
+// host_wait = true (inspection, snapshots) also waits until every queued
+// launch of the device has completed, callers' device-form launches included.
+bool flush_locked(Ctx *c, const char *fn, bool host_wait = false) {
+  if (c->staged == 0 && !host_wait) return true;
   DeviceGuard g(c->device);
-  hipStream_t s = lib_stream(c->device);
   if (c->staged > 0) {
-    if (c->pending) {
-      if (hip_fail(hipStreamSynchronize(s), fn)) return false;
-      c->pending = false;
-    }
+    if (hip_fail(lib_wait(c->device, c->stage_seq), fn)) return false;  // pinned rows reused
     const size_t n = (size_t)c->staged * c->dim;  // floats per side
     if (hip_fail(c->h_stage.ensure(2 * n * 4), fn)) return false;
     float *pk = static_cast<float *>(c->h_stage.p);
     std::memcpy(pk, c->stage_k.data(), n * 4);
     std::memcpy(pk + n, c->stage_v.data(), n * 4);
     const float *dk = static_cast<const float *>(c->h_stage.dp);
-    hipError_t e = hipSuccess;
-    if (c->staged > kDirectTokens) {
-      if (hip_fail(c->d_stage.ensure(2 * n * 4), fn)) return false;
-      e = hipMemcpyAsync(c->d_stage.p, c->h_stage.p, 2 * n * 4, hipMemcpyHostToDevice, s);
+    hipStream_t s;
+    hipError_t e = lib_begin(c->device, &s);
+    if (e == hipSuccess && c->staged > kDirectTokens) {
+      e = c->d_stage.ensure(2 * n * 4);
+      if (e == hipSuccess)
+        e = hipMemcpyAsync(c->d_stage.p, c->h_stage.p, 2 * n * 4, hipMemcpyHostToDevice, s);
       dk = static_cast<const float *>(c->d_stage.p);
     }
     if (e == hipSuccess)
       e = aq::launch_append(c->d_desc_list, 1, c->dim, c->padded, c->k_bits, c->v_bits, dk, dk + n,
                             c->staged, s);
     if (hip_fail(e, fn)) return false;
-    c->pending = true;
+    c->stage_seq = lib_end(c->device);
     c->st = aq::ring_after(c->st, c->staged, c->cap, c->hyb);
     c->staged = 0;
     c->stage_k.clear();
     c->stage_v.clear();
   }
-  if (sync && c->pending) {
-    if (hip_fail(hipStreamSynchronize(s), fn)) return false;
-    c->pending = false;
-  }
+  if (host_wait && hip_fail(settle(c->device), fn)) return false;
   return true;
 }
 
@@ -362,7 +554,8 @@ void append_locked(Ctx *c, const float *key, const float *val) {
   c->stage_k.insert(c->stage_k.end(), key, key + c->dim);
   c->stage_v.insert(c->stage_v.end(), val, val + c->dim);
   ++c->staged;
-  if (c->staged >= kStageTokens) flush_locked(c, "adaptq_append", false);
+  bump_epoch();
+  if (c->staged >= kStageTokens) flush_locked(c, "adaptq_append");
 }
 
 enum class Mode { Dense, Hybrid, Sparse };
@@ -377,14 +570,13 @@ Mode mode_of(const Ctx *c) {
 // Synchronous decode of nq queries against one head (caller holds c->mu).
 // Queries and outputs pass through pinned memory the kernels read and write.
 int compute_locked(Ctx *c, const float *queries, int nq, float *outs, const char *fn) {
-  if (!flush_locked(c, fn, false)) return -1;
+  if (!flush_locked(c, fn)) return -1;
   const int n = c->st.size;
   if (n == 0) {
     std::memset(outs, 0, sizeof(float) * (size_t)nq * c->dim);
     return 0;
   }
   DeviceGuard g(c->device);
-  hipStream_t s = lib_stream(c->device);
   const Mode mode = mode_of(c);
   aq::DecodeShape sh{c->dim, c->padded, c->k_bits, c->v_bits, mode == Mode::Hybrid, n};
   const size_t io = align256((size_t)nq * c->dim * 4);
@@ -403,57 +595,108 @@ int compute_locked(Ctx *c, const float *queries, int nq, float *outs, const char
   const float *dq = static_cast<const float *>(c->h_io.dp);
   float *dout = reinterpret_cast<float *>(static_cast<uint8_t *>(c->h_io.dp) + io);
   auto **items = static_cast<aq::HeadDesc **>(c->d_items.p);
-  hipError_t e =
-      mode == Mode::Sparse
-          ? aq::launch_decode_sparse(items, nq, sh, c->v_mass, dq, dout,
-                                     static_cast<float *>(c->d_ws.p), s)
-          : aq::launch_decode(items, nq, sh, dq, dout, static_cast<float *>(c->d_ws.p), s);
-  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  hipStream_t s;
+  hipError_t e = lib_begin(c->device, &s);
+  if (e == hipSuccess)
+    e = mode == Mode::Sparse
+            ? aq::launch_decode_sparse(items, nq, sh, c->v_mass, dq, dout,
+                                       static_cast<float *>(c->d_ws.p), s)
+            : aq::launch_decode(items, nq, sh, dq, dout, static_cast<float *>(c->d_ws.p), s);
+  if (e == hipSuccess) e = lib_wait(c->device, lib_end(c->device));
   if (hip_fail(e, fn)) return -1;
-  c->pending = false;
   std::memcpy(outs, static_cast<uint8_t *>(c->h_io.p) + io, (size_t)nq * c->dim * 4);
   return n;
 }
 
+// Empties the ring (caller holds c->mu).  The state reset is queued on the
+// library stream after every queued launch of the device; nothing waits.
 void reset_locked(Ctx *c) {
   c->staged = 0;
   c->stage_k.clear();
   c->stage_v.clear();
   c->st = aq::RingState{0, 0, 0, 0};
+  bump_epoch();
   DeviceGuard g(c->device);
-  hipStream_t s = lib_stream(c->device);
-  hipError_t e = aq::launch_reset_state(c->d_desc_list, 1, s);
-  if (e == hipSuccess) e = hipStreamSynchronize(s);
-  if (e != hipSuccess) hip_fail(e, "adaptq_reset");
-  else c->pending = false;
+  hipStream_t s;
+  hipError_t e = lib_begin(c->device, &s);
+  if (e == hipSuccess) e = aq::launch_reset_state(c->d_desc_list, 1, s);
+  if (e == hipSuccess) (void)lib_end(c->device);
+  else hip_fail(e, "adaptq_reset");
 }
 
+// A plan binds contexts for batched device-pointer calls.  It caches the
+// branch and the largest ring size of its contexts together with the epoch
+// they were read at; while no context has changed since (g_epoch), the
+// plan's calls read neither the contexts nor their locks.
 struct Plan {
   std::vector<Ctx *> ctxs;
   int device = 0;
   DevBuf d_list, d_ws;
+  std::mutex mu;          // one call on the plan at a time
+  uint64_t seen = 0;      // epoch the cache below was read at (0: never)
+  int max_n = 0;          // largest ring size
+  Mode mode = Mode::Dense;
+  bool mixed = false;     // non-empty contexts take different branches
 };
 
-// Before a plan launches on the caller's stream: queue every context's staged
-// host appends on the library stream, then wait for that stream once if any
-// work for these contexts is queued there.
-bool flush_plan(Plan *p, const char *fn) {
-  bool queued = false;
+// Scan of the plan's contexts (caller holds p->mu): flushes staged host
+// appends (library stream) and caches branch and largest ring size.
+bool plan_scan(Plan *p, const char *fn) {
+  if (p->seen != 0 && g_epoch.load(std::memory_order_acquire) == p->seen) return true;
+  const uint64_t e0 = g_epoch.load(std::memory_order_acquire);
+  int max_n = 0;
+  bool have = false, mixed = false;
+  Mode mode = Mode::Dense;
   for (Ctx *c : p->ctxs) {
     std::lock_guard<std::mutex> g(c->mu);
-    if (!flush_locked(c, fn, false)) return false;
-    queued = queued || c->pending;
+    if (!flush_locked(c, fn)) return false;
+    if (c->st.size > 0) {
+      const Mode m = mode_of(c);
+      if (have && m != mode) mixed = true;
+      mode = m;
+      have = true;
+    }
+    max_n = std::max(max_n, c->st.size);
   }
-  if (!queued) return true;
-  {
-    DeviceGuard g(p->device);
-    if (hip_fail(hipStreamSynchronize(lib_stream(p->device)), fn)) return false;
-  }
-  for (Ctx *c : p->ctxs) {
-    std::lock_guard<std::mutex> g(c->mu);
-    c->pending = false;
-  }
+  p->max_n = max_n;
+  p->mode = mode;
+  p->mixed = mixed;
+  p->seen = e0;
   return true;
+}
+
+// The batched decode of a plan on stream s (caller holds p->mu and has
+// scanned).  d_ws: workspace of at least ws_floats floats.
+int plan_launch_decode(Plan *p, const float *d_queries, float *d_outs, float *d_ws,
+                       hipStream_t s, const char *fn) {
+  if (p->mixed) {
+    set_error(
+        "adaptq_plan_compute_device: contexts take different branches (dense, sparse-V, "
+        "hybrid); use one plan per branch or adaptq_compute");
+    return -1;
+  }
+  const Ctx *c0 = p->ctxs[0];
+  const int n_items = (int)p->ctxs.size();
+  aq::DecodeShape sh{c0->dim, c0->padded, c0->k_bits, c0->v_bits, p->mode == Mode::Hybrid,
+                     p->max_n};
+  auto **items = static_cast<aq::HeadDesc **>(p->d_list.p);
+  hipError_t e = caller_begin(p->device, s);
+  if (e == hipSuccess)
+    e = p->mode == Mode::Sparse && p->max_n > 0
+            ? aq::launch_decode_sparse(items, n_items, sh, c0->v_mass, d_queries, d_outs, d_ws, s)
+            : aq::launch_decode(items, n_items, sh, d_queries, d_outs, d_ws, s);
+  if (e == hipSuccess) e = caller_end(p->device, s);
+  if (hip_fail(e, fn)) return -1;
+  return 0;
+}
+
+size_t plan_ws_floats(const Plan *p) {
+  const Ctx *c0 = p->ctxs[0];
+  const int n_items = (int)p->ctxs.size();
+  aq::DecodeShape sh{c0->dim, c0->padded, c0->k_bits, c0->v_bits, p->mode == Mode::Hybrid,
+                     p->max_n};
+  return p->mode == Mode::Sparse && p->max_n > 0 ? aq::sparse_workspace_floats(n_items, sh)
+                                                 : aq::decode_workspace_floats(n_items, sh);
 }
 
 // Locks every head of an MHA in index order (per-head calls take one head
@@ -469,34 +712,30 @@ struct HeadLocks {
 // Quantise the staged tokens of every head (caller holds all head locks).
 // When every head holds the same number of staged tokens -- the usual case,
 // one token per head per step -- they go out through one pinned buffer and one
-// append launch over all heads.  sync: as flush_locked.
-bool flush_all_locked(Mha *m, const char *fn, bool sync = true) {
+// append launch over all heads.  host_wait: as flush_locked.
+bool flush_all_locked(Mha *m, const char *fn, bool host_wait = false) {
   const int S = m->heads[0]->staged;
   bool uniform = S > 0;
-  for (Ctx *c : m->heads) uniform = uniform && c->staged == S;
+  bool any = false;
+  for (Ctx *c : m->heads) {
+    uniform = uniform && c->staged == S;
+    any = any || c->staged > 0;
+  }
+  DeviceGuard g(m->device);
+  if (!any) {
+    if (host_wait && hip_fail(settle(m->device), fn)) return false;
+    return true;
+  }
   if (!uniform) {
-    bool queued = m->pending;
-    for (Ctx *c : m->heads) {
-      if (c->staged > 0 && !flush_locked(c, fn, false)) return false;
-      queued = queued || c->pending;
-    }
-    if (sync && queued) {
-      DeviceGuard g(m->device);
-      if (hip_fail(hipStreamSynchronize(lib_stream(m->device)), fn)) return false;
-      m->pending = false;
-      for (Ctx *c : m->heads) c->pending = false;
-    }
+    for (Ctx *c : m->heads)
+      if (c->staged > 0 && !flush_locked(c, fn)) return false;
+    if (host_wait && hip_fail(settle(m->device), fn)) return false;
     return true;
   }
   const Ctx *c0 = m->heads[0];
   const int H = m->n_heads;
   const size_t per = (size_t)S * c0->dim;  // floats per head and side
-  DeviceGuard g(m->device);
-  hipStream_t s = lib_stream(m->device);
-  if (m->pending) {
-    if (hip_fail(hipStreamSynchronize(s), fn)) return false;
-    m->pending = false;
-  }
+  if (hip_fail(lib_wait(m->device, m->stage_seq), fn)) return false;  // pinned rows reused
   if (hip_fail(m->h_stage.ensure(2 * per * H * 4), fn)) return false;
   float *pk = static_cast<float *>(m->h_stage.p), *pv = pk + per * H;
   for (int h = 0; h < H; ++h) {
@@ -504,29 +743,26 @@ bool flush_all_locked(Mha *m, const char *fn, bool sync = true) {
     std::memcpy(pv + per * h, m->heads[h]->stage_v.data(), per * 4);
   }
   const float *dk = static_cast<const float *>(m->h_stage.dp);
-  hipError_t e = hipSuccess;
-  if (S > kDirectTokens) {
-    if (hip_fail(m->d_stage.ensure(2 * per * H * 4), fn)) return false;
-    e = hipMemcpyAsync(m->d_stage.p, m->h_stage.p, 2 * per * H * 4, hipMemcpyHostToDevice, s);
+  hipStream_t s;
+  hipError_t e = lib_begin(m->device, &s);
+  if (e == hipSuccess && S > kDirectTokens) {
+    e = m->d_stage.ensure(2 * per * H * 4);
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(m->d_stage.p, m->h_stage.p, 2 * per * H * 4, hipMemcpyHostToDevice, s);
     dk = static_cast<const float *>(m->d_stage.p);
   }
   if (e == hipSuccess)
     e = aq::launch_append(static_cast<aq::HeadDesc **>(m->d_list.p), H, c0->dim, c0->padded,
                           c0->k_bits, c0->v_bits, dk, dk + per * H, S, s);
   if (hip_fail(e, fn)) return false;
-  m->pending = true;
+  m->stage_seq = lib_end(m->device);
   for (Ctx *c : m->heads) {
     c->st = aq::ring_after(c->st, S, c->cap, c->hyb);
     c->staged = 0;
     c->stage_k.clear();
     c->stage_v.clear();
-    c->pending = true;  // the launch writes this head's ring
   }
-  if (sync) {
-    if (hip_fail(hipStreamSynchronize(s), fn)) return false;
-    m->pending = false;
-    for (Ctx *c : m->heads) c->pending = false;
-  }
+  if (host_wait && hip_fail(settle(m->device), fn)) return false;
   return true;
 }
 
@@ -694,9 +930,9 @@ adaptq_mha_t adaptq_mha_create(int n_heads, int dim, int k_bits, int v_bits, int
 void adaptq_mha_destroy(adaptq_mha_t h) {
   if (!h) return;
   Mha *m = static_cast<Mha *>(h);
-  if (m->pending) {
+  {
     DeviceGuard g(m->device);
-    (void)hipStreamSynchronize(lib_stream(m->device));
+    (void)settle(m->device);  // no queued kernel may still use the heads or pinned rows
   }
   for (Ctx *c : m->heads) free_ctx(c);
   {
@@ -763,7 +999,26 @@ int adaptq_mha_compute_batch(adaptq_mha_t h, int head_idx, const float *queries,
 void adaptq_mha_reset(adaptq_mha_t h) {
   if (!require_handle(h, "adaptq_mha_reset")) return;
   Mha *m = static_cast<Mha *>(h);
-  for (Ctx *c : m->heads) adaptq_reset(c);
+  {
+    std::lock_guard<std::mutex> gm(m->mu);
+    HeadLocks locks(m);
+    for (Ctx *c : m->heads) {
+      c->staged = 0;
+      c->stage_k.clear();
+      c->stage_v.clear();
+      c->st = aq::RingState{0, 0, 0, 0};
+    }
+    bump_epoch();
+    // one state reset for every head, queued after the device's queued launches
+    DeviceGuard g(m->device);
+    hipStream_t s;
+    hipError_t e = lib_begin(m->device, &s);
+    if (e == hipSuccess)
+      e = aq::launch_reset_state(static_cast<aq::HeadDesc **>(m->d_list.p), m->n_heads, s);
+    if (e == hipSuccess) (void)lib_end(m->device);
+    if (hip_fail(e, "adaptq_mha_reset")) return;
+  }
+  clear_error();
 }
 
 size_t adaptq_mha_total_kv_bytes(adaptq_mha_t h) {
@@ -798,7 +1053,8 @@ int adaptq_mha_append_all(adaptq_mha_t h, const float *keys, const float *vals, 
     c->stage_v.insert(c->stage_v.end(), vals + (size_t)i * dim, vals + (size_t)(i + 1) * dim);
     ++c->staged;
   }
-  if (m->heads[0]->staged >= kStageTokens && !flush_all_locked(m, fn, false)) return -1;
+  bump_epoch();
+  if (m->heads[0]->staged >= kStageTokens && !flush_all_locked(m, fn)) return -1;
   clear_error();
   return 0;
 }
@@ -811,16 +1067,17 @@ int adaptq_mha_compute_all(adaptq_mha_t h, const float *queries, float *outs) {
   Mha *m = static_cast<Mha *>(h);
   std::lock_guard<std::mutex> gm(m->mu);
   HeadLocks locks(m);
-  if (!flush_all_locked(m, fn, false)) return -1;
+  if (!flush_all_locked(m, fn)) return -1;
   const int H = m->n_heads, dim = m->heads[0]->dim;
   DeviceGuard g(m->device);
-  hipStream_t s = lib_stream(m->device);
   // queries and outputs through pinned memory the kernels read and write
   const size_t io = align256((size_t)H * dim * 4);
-  if (hip_fail(m->h_io.ensure(2 * io), fn)) return -1;
+  if (hip_fail(m->h_io.ensure(2 * io), fn)) return -1;  // no kernel uses it between calls
   std::memcpy(m->h_io.p, queries, (size_t)H * dim * 4);
   const float *dq = static_cast<const float *>(m->h_io.dp);
   float *dout = reinterpret_cast<float *>(static_cast<uint8_t *>(m->h_io.dp) + io);
+  hipStream_t s;
+  if (hip_fail(lib_begin(m->device, &s), fn)) return -1;
   int n = launch_all_locked(m, dq, dout, s, fn);
   if (n == -2) {  // heads differ in size or branch: one head at a time
     n = 0;
@@ -830,15 +1087,11 @@ int adaptq_mha_compute_all(adaptq_mha_t h, const float *queries, float *outs) {
       if (r < 0) return -1;
       if (i == 0) n = r;
     }
-    m->pending = false;  // compute_locked waited for the stream
-    for (Ctx *c : m->heads) c->pending = false;
     clear_error();
     return n;
   }
   if (n < 0) return -1;
-  if (hip_fail(hipStreamSynchronize(s), fn)) return -1;
-  m->pending = false;
-  for (Ctx *c : m->heads) c->pending = false;
+  if (hip_fail(lib_wait(m->device, lib_end(m->device)), fn)) return -1;
   std::memcpy(outs, static_cast<uint8_t *>(m->h_io.p) + io, (size_t)H * dim * 4);
   clear_error();
   return n;
@@ -862,11 +1115,15 @@ int adaptq_mha_append_all_device(adaptq_mha_t h, const float *d_keys, const floa
   if (!flush_all_locked(m, fn)) return -1;
   const Ctx *c0 = m->heads[0];
   DeviceGuard g(m->device);
-  hipError_t e = aq::launch_append(static_cast<aq::HeadDesc **>(m->d_list.p), m->n_heads, c0->dim,
-                                   c0->padded, c0->k_bits, c0->v_bits, d_keys, d_vals, n_tokens,
-                                   static_cast<hipStream_t>(stream));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = caller_begin(m->device, s);
+  if (e == hipSuccess)
+    e = aq::launch_append(static_cast<aq::HeadDesc **>(m->d_list.p), m->n_heads, c0->dim,
+                          c0->padded, c0->k_bits, c0->v_bits, d_keys, d_vals, n_tokens, s);
+  if (e == hipSuccess) e = caller_end(m->device, s);
   if (hip_fail(e, fn)) return -1;
   for (Ctx *c : m->heads) c->st = aq::ring_after(c->st, n_tokens, c->cap, c->hyb);
+  bump_epoch();
   return 0;
 }
 
@@ -881,12 +1138,15 @@ int adaptq_mha_compute_all_device(adaptq_mha_t h, const float *d_queries, float 
   HeadLocks locks(m);
   if (!flush_all_locked(m, fn)) return -1;
   DeviceGuard g(m->device);
-  const int n = launch_all_locked(m, d_queries, d_outs, static_cast<hipStream_t>(stream), fn);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (hip_fail(caller_begin(m->device, s), fn)) return -1;
+  const int n = launch_all_locked(m, d_queries, d_outs, s, fn);
   if (n == -2) {
     set_error("adaptq_mha_compute_all_device: heads differ in ring size or branch; "
               "use adaptq_mha_compute_all");
     return -1;
   }
+  if (n >= 0 && hip_fail(caller_end(m->device, s), fn)) return -1;
   return n;
 }
 
@@ -946,6 +1206,7 @@ int adaptq_ggml_append_f32(adaptq_mha_t h, const float *k, const float *v, int h
       c->stage_v.insert(c->stage_v.end(), vr, vr + head_dim);
       ++c->staged;
     }
+    bump_epoch();
     if (m->heads[0]->staged >= kStageTokens && !flush_all_locked(m, fn)) return -1;
   }
   clear_error();
@@ -964,14 +1225,13 @@ int adaptq_ggml_attn_f32(adaptq_mha_t h, const float *q, int head_dim, int n_hea
   std::lock_guard<std::mutex> gm(m->mu);
   HeadLocks locks(m);
   // the decode runs on the library stream after the flush's launches
-  if (!flush_all_locked(m, fn, false)) return -1;
+  if (!flush_all_locked(m, fn)) return -1;
   const int H = m->n_heads, dim = head_dim;
   if (n_queries == 0) {
     clear_error();
     return m->heads[0]->st.size;
   }
   DeviceGuard g(m->device);
-  hipStream_t s = lib_stream(m->device);
   // queries packed [query][head][dim] into pinned memory the kernels read;
   // outputs come back there in the same order
   const size_t rows = (size_t)n_queries * H;
@@ -985,6 +1245,8 @@ int adaptq_ggml_attn_f32(adaptq_mha_t h, const float *q, int head_dim, int n_hea
                   (size_t)dim * 4);
   const float *dq = static_cast<const float *>(m->h_io.dp);
   float *dout = reinterpret_cast<float *>(static_cast<uint8_t *>(m->h_io.dp) + io);
+  hipStream_t s;
+  if (hip_fail(lib_begin(m->device, &s), fn)) return -1;
   int n = launch_all_locked(m, dq, dout, s, fn, n_queries);
   if (n == -2) {  // heads differ in size or branch: head by head, all queries of a head at once
     std::vector<float> hq((size_t)n_queries * dim), ho((size_t)n_queries * dim);
@@ -999,10 +1261,8 @@ int adaptq_ggml_attn_f32(adaptq_mha_t h, const float *q, int head_dim, int n_hea
     }
   } else {
     if (n < 0) return -1;
-    if (hip_fail(hipStreamSynchronize(s), fn)) return -1;
+    if (hip_fail(lib_wait(m->device, lib_end(m->device)), fn)) return -1;
   }
-  m->pending = false;  // the stream has drained (compute_locked waits for it too)
-  for (Ctx *c : m->heads) c->pending = false;
   for (int j = 0; j < n_queries; ++j)
     for (int i = 0; i < H; ++i)
       std::memcpy(const_cast<float *>(row_at(dst, (size_t)i, d_nb1, (size_t)j, d_nb2)),
@@ -1035,13 +1295,16 @@ int adaptq_ggml_append_f32_device(adaptq_mha_t h, const float *d_k, const float 
   if (hip_fail(m->d_stage.ensure(2 * half), fn)) return -1;
   float *dk = static_cast<float *>(m->d_stage.p);
   float *dv = reinterpret_cast<float *>(static_cast<uint8_t *>(m->d_stage.p) + half);
-  hipError_t e = aq::launch_gather_rows(dk, d_k, H, n_tokens, head_dim, k_nb1, k_nb2, s);
+  hipError_t e = caller_begin(m->device, s);
+  if (e == hipSuccess) e = aq::launch_gather_rows(dk, d_k, H, n_tokens, head_dim, k_nb1, k_nb2, s);
   if (e == hipSuccess) e = aq::launch_gather_rows(dv, d_v, H, n_tokens, head_dim, v_nb1, v_nb2, s);
   if (e == hipSuccess)
     e = aq::launch_append(static_cast<aq::HeadDesc **>(m->d_list.p), H, c0->dim, c0->padded,
                           c0->k_bits, c0->v_bits, dk, dv, n_tokens, s);
+  if (e == hipSuccess) e = caller_end(m->device, s);
   if (hip_fail(e, fn)) return -1;
   for (Ctx *c : m->heads) c->st = aq::ring_after(c->st, n_tokens, c->cap, c->hyb);
+  bump_epoch();
   return 0;
 }
 
@@ -1068,7 +1331,8 @@ int adaptq_ggml_attn_f32_device(adaptq_mha_t h, const float *d_q, int head_dim, 
   float *dq = static_cast<float *>(m->d_io.p);
   float *dout = reinterpret_cast<float *>(static_cast<uint8_t *>(m->d_io.p) + io);
   // queries as [query][head][dim]
-  if (hip_fail(aq::launch_gather_rows(dq, d_q, n_queries, H, head_dim, q_nb2, q_nb1, s), fn))
+  if (hip_fail(caller_begin(m->device, s), fn) ||
+      hip_fail(aq::launch_gather_rows(dq, d_q, n_queries, H, head_dim, q_nb2, q_nb1, s), fn))
     return -1;
   const int n = launch_all_locked(m, dq, dout, s, fn, n_queries);
   if (n == -2) {
@@ -1077,7 +1341,8 @@ int adaptq_ggml_attn_f32_device(adaptq_mha_t h, const float *d_q, int head_dim, 
     return -1;
   }
   if (n < 0) return -1;
-  if (hip_fail(aq::launch_scatter_rows(d_dst, dout, n_queries, H, head_dim, d_nb2, d_nb1, s), fn))
+  if (hip_fail(aq::launch_scatter_rows(d_dst, dout, n_queries, H, head_dim, d_nb2, d_nb1, s), fn) ||
+      hip_fail(caller_end(m->device, s), fn))
     return -1;
   return n;
 }
@@ -1086,7 +1351,7 @@ int adaptq_flush(adaptq_ctx_t h) {
   if (!require_handle(h, "adaptq_flush")) return -1;
   Ctx *c = static_cast<Ctx *>(h);
   std::lock_guard<std::mutex> g(c->mu);
-  return flush_locked(c, "adaptq_flush") ? 0 : -1;
+  return flush_locked(c, "adaptq_flush", true) ? 0 : -1;
 }
 
 int adaptq_ring_info(adaptq_ctx_t h, int *head, int *size, int *capacity, int *padded_dim,
@@ -1113,23 +1378,22 @@ int adaptq_read_slots(adaptq_ctx_t h, int first_slot, int count, uint8_t *k_code
     set_error("adaptq_read_slots: slot range out of bounds");
     return -1;
   }
-  if (!flush_locked(c, "adaptq_read_slots")) return -1;
+  // every queued launch of the device (callers' included) completes first
+  if (!flush_locked(c, "adaptq_read_slots", true)) return -1;
   if (count == 0) return 0;
   DeviceGuard g2(c->device);
-  hipStream_t s = lib_stream(c->device);
-  aq::HeadDesc hd;
-  hipError_t e = hipMemcpy(&hd, c->d_desc, sizeof(hd), hipMemcpyDeviceToHost);
+  const aq::HeadDesc &hd = c->hd;
+  hipError_t e = hipSuccess;
   if (e == hipSuccess && k_codes)
-    e = hipMemcpyAsync(k_codes, hd.k_codes + (size_t)first_slot * c->k_pb, (size_t)count * c->k_pb,
-                       hipMemcpyDeviceToHost, s);
+    e = hipMemcpy(k_codes, hd.k_codes + (size_t)first_slot * c->k_pb, (size_t)count * c->k_pb,
+                  hipMemcpyDeviceToHost);
   if (e == hipSuccess && v_codes)
-    e = hipMemcpyAsync(v_codes, hd.v_codes + (size_t)first_slot * c->v_pb, (size_t)count * c->v_pb,
-                       hipMemcpyDeviceToHost, s);
+    e = hipMemcpy(v_codes, hd.v_codes + (size_t)first_slot * c->v_pb, (size_t)count * c->v_pb,
+                  hipMemcpyDeviceToHost);
   if (e == hipSuccess && k_scale)
-    e = hipMemcpyAsync(k_scale, hd.k_scale + first_slot, (size_t)count * 4, hipMemcpyDeviceToHost, s);
+    e = hipMemcpy(k_scale, hd.k_scale + first_slot, (size_t)count * 4, hipMemcpyDeviceToHost);
   if (e == hipSuccess && v_scale)
-    e = hipMemcpyAsync(v_scale, hd.v_scale + first_slot, (size_t)count * 4, hipMemcpyDeviceToHost, s);
-  if (e == hipSuccess) e = hipStreamSynchronize(s);
+    e = hipMemcpy(v_scale, hd.v_scale + first_slot, (size_t)count * 4, hipMemcpyDeviceToHost);
   if (hip_fail(e, "adaptq_read_slots")) return -1;
   // K rows stored in XOR byte order go back to the reference's order
   const int xmask = aq::kperm_mask(c->padded, c->k_bits);
@@ -1143,6 +1407,29 @@ int adaptq_read_slots(adaptq_ctx_t h, int first_slot, int count, uint8_t *k_code
     }
   }
   return 0;
+}
+
+int adaptq_sparse_weights(adaptq_ctx_t h, const float *query, float *weights) {
+  const char *fn = "adaptq_sparse_weights";
+  if (!require_handle(h, fn) || !require_pointer(query, fn, "query") ||
+      !require_pointer(weights, fn, "weights"))
+    return -1;
+  Ctx *c = static_cast<Ctx *>(h);
+  std::lock_guard<std::mutex> g(c->mu);
+  if (!flush_locked(c, fn)) return -1;
+  if (c->st.size == 0) return 0;
+  if (mode_of(c) != Mode::Sparse) {
+    set_errorf(fn, "the context does not take the sparse-V branch");
+    return -1;
+  }
+  std::vector<float> out((size_t)c->dim);
+  const int n = compute_locked(c, query, 1, out.data(), fn);
+  if (n < 0) return -1;
+  // every sparse-V launch leaves item 0's per-token weights (ring order) at
+  // the start of the workspace, and compute_locked has waited for it
+  DeviceGuard g2(c->device);
+  if (hip_fail(hipMemcpy(weights, c->d_ws.p, (size_t)n * 4, hipMemcpyDeviceToHost), fn)) return -1;
+  return n;
 }
 
 adaptq_ctx_t adaptq_mha_head(adaptq_mha_t h, int head_idx) {
@@ -1229,18 +1516,43 @@ int adaptq_plan_append_device(adaptq_plan_t h, const float *d_keys, const float 
   }
   Plan *p = static_cast<Plan *>(h);
   if (n_tokens == 0) return 0;
-  if (!flush_plan(p, fn)) return -1;
+  std::lock_guard<std::mutex> gp(p->mu);
+  if (!plan_scan(p, fn)) return -1;
   DeviceGuard g(p->device);
   hipStream_t s = static_cast<hipStream_t>(stream);  // NULL = the HIP null stream
   const Ctx *c0 = p->ctxs[0];
-  hipError_t e = aq::launch_append(static_cast<aq::HeadDesc **>(p->d_list.p), (int)p->ctxs.size(),
-                                   c0->dim, c0->padded, c0->k_bits, c0->v_bits, d_keys, d_vals,
-                                   n_tokens, s);
+  hipError_t e = caller_begin(p->device, s);
+  if (e == hipSuccess)
+    e = aq::launch_append(static_cast<aq::HeadDesc **>(p->d_list.p), (int)p->ctxs.size(), c0->dim,
+                          c0->padded, c0->k_bits, c0->v_bits, d_keys, d_vals, n_tokens, s);
+  if (e == hipSuccess) e = caller_end(p->device, s);
   if (hip_fail(e, fn)) return -1;
+  // Every context takes the same n_tokens: update the host ring states and
+  // the plan's cache in one pass, without the contexts' locks (calls that
+  // touch the same contexts must not overlap a plan call).
+  int max_n = 0;
+  bool have = false, mixed = false;
+  Mode mode = Mode::Dense;
   for (Ctx *c : p->ctxs) {
-    std::lock_guard<std::mutex> g2(c->mu);
     c->st = aq::ring_after(c->st, n_tokens, c->cap, c->hyb);
+    if (c->st.size > 0) {
+      const Mode m = mode_of(c);
+      if (have && m != mode) mixed = true;
+      mode = m;
+      have = true;
+    }
+    max_n = std::max(max_n, c->st.size);
   }
+  p->max_n = max_n;
+  p->mode = mode;
+  p->mixed = mixed;
+  // the states changed: other plans over these contexts must rescan; this
+  // plan's cache stays valid unless someone else moved the epoch meanwhile
+  uint64_t expect = p->seen;
+  if (g_epoch.compare_exchange_strong(expect, expect + 1, std::memory_order_acq_rel))
+    p->seen = expect + 1;
+  else
+    bump_epoch();
   return 0;
 }
 
@@ -1251,41 +1563,12 @@ int adaptq_plan_compute_device(adaptq_plan_t h, const float *d_queries, float *d
       !require_pointer(d_outs, fn, "d_outs"))
     return -1;
   Plan *p = static_cast<Plan *>(h);
-  int max_n = 0;
-  bool have_mode = false;
-  Mode mode = Mode::Dense;
-  if (!flush_plan(p, fn)) return -1;
-  for (Ctx *c : p->ctxs) {
-    std::lock_guard<std::mutex> g(c->mu);
-    if (c->st.size > 0) {
-      const Mode m = mode_of(c);
-      if (have_mode && m != mode) {
-        set_error(
-            "adaptq_plan_compute_device: contexts take different branches (dense, sparse-V, "
-            "hybrid); use one plan per branch or adaptq_compute");
-        return -1;
-      }
-      mode = m;
-      have_mode = true;
-    }
-    max_n = std::max(max_n, c->st.size);
-  }
-  const Ctx *c0 = p->ctxs[0];
-  const int n_items = (int)p->ctxs.size();
-  aq::DecodeShape sh{c0->dim, c0->padded, c0->k_bits, c0->v_bits, mode == Mode::Hybrid, max_n};
+  std::lock_guard<std::mutex> gp(p->mu);
+  if (!plan_scan(p, fn)) return -1;
   DeviceGuard g(p->device);
-  const size_t wsf = mode == Mode::Sparse ? aq::sparse_workspace_floats(n_items, sh)
-                                          : aq::decode_workspace_floats(n_items, sh);
-  if (hip_fail(p->d_ws.ensure(wsf * 4), fn)) return -1;
-  hipStream_t s = static_cast<hipStream_t>(stream);  // NULL = the HIP null stream
-  auto **items = static_cast<aq::HeadDesc **>(p->d_list.p);
-  float *ws = static_cast<float *>(p->d_ws.p);
-  const hipError_t e = mode == Mode::Sparse && max_n > 0
-                           ? aq::launch_decode_sparse(items, n_items, sh, c0->v_mass, d_queries,
-                                                      d_outs, ws, s)
-                           : aq::launch_decode(items, n_items, sh, d_queries, d_outs, ws, s);
-  if (hip_fail(e, fn)) return -1;
-  return 0;
+  if (!p->mixed && hip_fail(p->d_ws.ensure(plan_ws_floats(p) * 4), fn)) return -1;
+  return plan_launch_decode(p, d_queries, d_outs, static_cast<float *>(p->d_ws.p),
+                            static_cast<hipStream_t>(stream), fn);
 }
 
 }  // extern "C"
@@ -1357,8 +1640,8 @@ bool read_ring(Ctx *c, std::vector<uint8_t> &kc, std::vector<uint8_t> &vc,
   vs.assign((size_t)n, 0.f);
   if (n == 0) return true;
   DeviceGuard g(c->device);
-  aq::HeadDesc hd;
-  hipError_t e = hipMemcpy(&hd, c->d_desc, sizeof(hd), hipMemcpyDeviceToHost);
+  const aq::HeadDesc &hd = c->hd;
+  hipError_t e = hipSuccess;
   std::vector<uint8_t> ak((size_t)cap * c->k_pb), av((size_t)cap * c->v_pb);
   std::vector<float> aks((size_t)cap), avs((size_t)cap);
   if (e == hipSuccess) e = hipMemcpy(ak.data(), hd.k_codes, ak.size(), hipMemcpyDeviceToHost);
@@ -1385,10 +1668,9 @@ bool read_ring(Ctx *c, std::vector<uint8_t> &kc, std::vector<uint8_t> &vc,
 bool write_ring(Ctx *c, int n, const uint8_t *kc, const uint8_t *vc, int row_stride,
                 const float *ks, const float *vs, const char *fn) {
   {
-    // appends still queued on the library stream would land after the copies
+    // appends still queued (library stream or callers') would land after the copies
     DeviceGuard g(c->device);
-    if (hip_fail(hipStreamSynchronize(lib_stream(c->device)), fn)) return false;
-    c->pending = false;
+    if (hip_fail(settle(c->device), fn)) return false;
   }
   const int cap = c->cap;
   std::vector<uint8_t> ak((size_t)cap * c->k_pb, 0), av((size_t)cap * c->v_pb, 0);
@@ -1405,8 +1687,8 @@ bool write_ring(Ctx *c, int n, const uint8_t *kc, const uint8_t *vc, int row_str
   }
   aq::RingState st{cap > 0 ? n % cap : 0, n, 0, 0};
   DeviceGuard g(c->device);
-  aq::HeadDesc hd;
-  hipError_t e = hipMemcpy(&hd, c->d_desc, sizeof(hd), hipMemcpyDeviceToHost);
+  const aq::HeadDesc &hd = c->hd;
+  hipError_t e = hipSuccess;
   if (e == hipSuccess && cap > 0) e = hipMemcpy(hd.k_codes, ak.data(), ak.size(), hipMemcpyHostToDevice);
   if (e == hipSuccess && cap > 0) e = hipMemcpy(hd.v_codes, av.data(), av.size(), hipMemcpyHostToDevice);
   if (e == hipSuccess && cap > 0) e = hipMemcpy(hd.k_scale, aks.data(), aks.size() * 4, hipMemcpyHostToDevice);
@@ -1417,6 +1699,7 @@ bool write_ring(Ctx *c, int n, const uint8_t *kc, const uint8_t *vc, int row_str
   c->staged = 0;
   c->stage_k.clear();
   c->stage_v.clear();
+  bump_epoch();
   return true;
 }
 
@@ -1470,7 +1753,7 @@ int adaptq_snapshot_save(const adaptq_mha_t *layers, int n_layers, const char *p
     Mha *m = static_cast<Mha *>(layers[l]);
     std::lock_guard<std::mutex> gm(m->mu);
     HeadLocks locks(m);
-    if (!flush_all_locked(m, fn)) return -1;
+    if (!flush_all_locked(m, fn, true)) return -1;
     for (int h = 0; h < H; ++h) {
       Ctx *c = m->heads[h];
       if (!read_ring(c, kc, vc, ks, vs, fn)) return -1;

@@ -270,12 +270,21 @@ __device__ void write_partial(float *part, float m, float l, const float *acc_ld
   for (int i = threadIdx.x; i < P; i += blockDim.x) part[4 + i] = acc_lds[i];
 }
 
+// The reference seeds the running maximum of every softmax at -1e30
+// (attention.cpp:496, :566, and compute_avx2): logits at or below it get
+// weight expf(l - (-1e30)) = 0.  In base-2 units (quantised K) the seed is
+// -1e30 * log2 e.
+constexpr float kMaxSeed = -1e30f;
+constexpr float kMaxSeed2 = -1.44269504e30f;
+
 // Normalise acc (in LDS, P entries) by 1/L, undo the rotation (inverse FWHT
 // and signs, fwht.cpp:106-134) when V is quantised, and write dim outputs.
+// guard (the hybrid branch, attention.cpp:513): a zero or non-finite L
+// normalises by 1/n instead; elsewhere the reference divides by L as is.
 template <bool INVERSE_FWHT>
 __device__ void finish_item(float *s_acc, int P, int dim, float L, const uint32_t *signs,
-                            float *out) {
-  const float invL = 1.0f / L;
+                            float *out, bool guard = false, int n = 1) {
+  const float invL = guard && !(L > 0.0f && isfinite(L)) ? 1.0f / (float)n : 1.0f / L;
   for (int i = threadIdx.x; i < P; i += blockDim.x) s_acc[i] *= invL;
   __syncthreads();
   if (INVERSE_FWHT) {
@@ -736,7 +745,7 @@ __global__ __launch_bounds__(kLutThreads, (KB == 2 || KB == 4) ? 4 : 2) void dec
   float acc[D];
 #pragma unroll
   for (int i = 0; i < D; ++i) acc[i] = 0.0f;
-  float m_run = -INFINITY, l_run = 0.0f;
+  float m_run = KQ ? kMaxSeed2 : kMaxSeed, l_run = 0.0f;
 
   // The loop body holds the V phase of tile i and the K phase of tile i+1.
   float logit = tile_logit(kc, ksc, base);
@@ -861,7 +870,7 @@ __global__ __launch_bounds__(kLutThreads, (KB == 2 || KB == 4) ? 4 : 2) void dec
       s_q[i] = a;
     }
     __syncthreads();
-    finish_item<VQ && !RAW>(s_q, P, dim, L, signs, outs + (size_t)item * dim);
+    finish_item<VQ && !RAW>(s_q, P, dim, L, signs, outs + (size_t)item * dim, RAW, n);
     return;
   }
   for (int i = threadIdx.x; i < P; i += blockDim.x) {
@@ -969,7 +978,7 @@ __global__ __launch_bounds__(kThreads) void decode_generic_kernel(
   float acc[kMaxPadded / kThreads];
 #pragma unroll
   for (int r = 0; r < kMaxPadded / kThreads; ++r) acc[r] = 0.0f;
-  float m_run = -INFINITY, l_run = 0.0f;
+  float m_run = kMaxSeed, l_run = 0.0f;
 
   for (int t0 = t_begin; t0 < t_end; t0 += G) {
     if constexpr (KQ) {
@@ -1065,7 +1074,7 @@ template <bool INVERSE_FWHT>
 __global__ __launch_bounds__(kThreads) void finalize_kernel(HeadDesc *const *item_desc, int P,
                                                             int n_splits,
                                                             const float *__restrict__ partials,
-                                                            float *__restrict__ outs) {
+                                                            float *__restrict__ outs, int guard) {
   __shared__ float s_acc[kMaxPadded];
   __shared__ float s_f[kMaxSplitWeights];
   __shared__ float s_red[kWaves];
@@ -1131,7 +1140,7 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(HeadDesc *const *ite
     }
   }
   __syncthreads();
-  finish_item<INVERSE_FWHT>(s_acc, P, dim, L, d->signs, out);
+  finish_item<INVERSE_FWHT>(s_acc, P, dim, L, d->signs, out, guard != 0, d->st.size);
 }
 
 struct SplitPlan {
@@ -1280,9 +1289,10 @@ hipError_t launch_decode_items(HeadDesc *const *descs, int n_items, const Decode
   if (e != hipSuccess) return e;
   const bool fwht = !raw && sh.v_bits != 16;
   if (fwht)
-    finalize_kernel<true><<<n_items, kThreads, 0, s>>>(descs, sh.padded, sp.splits, d_ws, d_out);
+    finalize_kernel<true><<<n_items, kThreads, 0, s>>>(descs, sh.padded, sp.splits, d_ws, d_out, 0);
   else
-    finalize_kernel<false><<<n_items, kThreads, 0, s>>>(descs, sh.padded, sp.splits, d_ws, d_out);
+    finalize_kernel<false><<<n_items, kThreads, 0, s>>>(descs, sh.padded, sp.splits, d_ws, d_out,
+                                                        raw ? 1 : 0);
   return hipGetLastError();
 }
 

@@ -28,6 +28,7 @@
 // block per item, at padded 64 the logits too (sparse_fused_kernel).
 #include <rocprim/device/device_radix_sort.hpp>
 
+#include "expf_ref.hpp"
 #include "launch.hpp"
 
 namespace aq {
@@ -365,7 +366,8 @@ __device__ __forceinline__ void scan_counts(SelectShared &sh) {
 // Selection for n <= kLdsSort tokens.  Thread t owns tokens E t .. E t + E - 1
 // in registers.  Steps:
 //   1. max of the logits (the reference's start value -1e30 and compare)
-//   2. e = expf(l - max) into LDS; thread 0 adds them left to right
+//   2. e = expf(l - max) into LDS (expf_ref: the reference's libm expf, bit
+//      for bit); thread 0 adds them left to right
 //      (attention.cpp:422-426); p = e * (1/sum)
 //   3. stable LSD radix sort of the 32-bit keys, 4 bits a pass, skipping
 //      digits every key shares: order p descending, ties older first
@@ -392,7 +394,7 @@ __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, fl
   float *ef = reinterpret_cast<float *>(sh.key);
 #pragma unroll
   for (int e = 0; e < E; ++e)
-    if (p0 + e < n) ef[p0 + e] = expf(ev[e] - mx);
+    if (p0 + e < n) ef[p0 + e] = expf_ref(ev[e] - mx);
   __syncthreads();
   if (tid == 0) sh.bcast[0] = 1.0f / serial_sum(ef, n, 0.0f);
   __syncthreads();
@@ -507,7 +509,7 @@ __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, fl
   for (int e = 0; e < E; ++e) {
     const int t = p0 + e;
     if (t < n) {
-      const float p = __fmul_rn(expf(lv[e] - mx), inv);
+      const float p = __fmul_rn(expf_ref(lv[e] - mx), inv);
       lg[t] = cut > 0 && make_key(p, t) <= last ? __fmul_rn(__fmul_rn(p, vs[e]), isp) : 0.0f;
     }
   }
@@ -574,7 +576,7 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
   for (int base = 0; base < n; base += kStage) {
     const int m = n - base < kStage ? n - base : kStage;
     for (int i = tid; i < m; i += blockDim.x) {
-      const float e = expf(lg[base + i] - mx);
+      const float e = expf_ref(lg[base + i] - mx);
       lg[base + i] = e;
       s_stage[i] = e;
     }

@@ -42,56 +42,19 @@ def append_bytes_per_token(dim, p, kb, vb):
     return 8 * dim + pb(p, kb) + pb(p, vb) + 8
 
 
-def cpu_baseline(cfg, seconds=12.0, heads=8, seed=0):
-    """The reference's own decode (oracle/_ref: core/*.cpp, attention.cpp built
-    from /root/reference) on this host: `heads` heads of the bench shape, each
-    filled with cfg['ctx'] tokens, then compute() repeated for ~seconds, first
-    on one thread (the reference's execution model), then on one thread per
-    head.  Returns the multi-thread figure with the single-thread one attached.
-    Where the reference build is absent, the CPU restatement (oracle/) is timed
-    instead and reported as kind "port"."""
-    import numpy as np
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    # test infrastructure: the checker/baseline only
-    from bind import Oracle, Ref, REF_SO, fptr
-    if os.path.exists(REF_SO):
-        L, kind = Ref().lib, "reference"
-        create, append, compute = L.adaptq_create, L.adaptq_append, L.adaptq_compute
-    else:
-        L, kind = Oracle().lib, "port"
-        create, append, compute = L.orc_head_create, L.orc_head_append, L.orc_head_compute
-    dim, n = cfg["dim"], cfg["ctx"]
-    rng = np.random.default_rng(seed)
-    hs = []
-    for h in range(heads):
-        c = create(dim, cfg["k_bits"], cfg["v_bits"], n, 1000 + h, 0.0, 0)
-        kv = rng.standard_normal((n, 2, dim)).astype(np.float32)
-        for t in range(n):
-            append(c, fptr(kv[t, 0]), fptr(kv[t, 1]), t)
-        hs.append(c)
-    q = rng.standard_normal((heads, dim)).astype(np.float32)
-    out = np.zeros((heads, dim), np.float32)
-
-    def run(idx, budget, counts):
-        t0 = time.perf_counter()
-        k = 0
-        while time.perf_counter() - t0 < budget:
-            compute(hs[idx], fptr(q[idx]), fptr(out[idx]))
-            k += 1
-        counts[idx] = (k, time.perf_counter() - t0)
-
-    counts = {}
-    run(0, seconds / 3, counts)
-    single = counts[0][0] * n / counts[0][1]
-    counts = {}
-    threads = [threading.Thread(target=run, args=(i, 2 * seconds / 3, counts)) for i in range(heads)]
-    for t in threads:
-        t.start()
-    for t in threads:
-        t.join()
-    multi = sum(k * n / dt for k, dt in counts.values())
-    for c in hs:
-        (L.adaptq_destroy if kind == "reference" else L.orc_head_destroy)(c)
+def host_cpus():
+    """CPUs this process may use: the affinity mask, capped by a cgroup v2 CPU
+    quota if one is set (a container may see many cores but run on a share)."""
+    aff = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, period = f.read().split()[:2]
+            if q != "max":
+                quota = float(q) / float(period)
+    except (OSError, ValueError):
+        pass
+    usable = aff if quota is None else max(1, min(aff, int(quota)))
     model = "unknown"
     try:
         with open("/proc/cpuinfo") as f:
@@ -101,14 +64,257 @@ def cpu_baseline(cfg, seconds=12.0, heads=8, seed=0):
                     break
     except OSError:
         pass
+    return {"usable": usable, "affinity": aff, "cgroup_quota": quota, "model": model}
+
+
+class _CpuRef:
+    """The reference's own append/compute (oracle/_ref: core/*.cpp, cache/,
+    attention/attention.cpp built in place from /root/reference) through its C
+    ABI, looped in C by the test harness (oracle/ref_shim.cpp).  Without the
+    reference build, the CPU restatement (oracle/) stands in, looped from
+    Python, and the figures are marked kind "port"."""
+
+    def __init__(self):
+        import numpy as np
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        # test infrastructure: the baseline only
+        from bind import Oracle, Ref, REF_SO, fptr
+        self.np, self.fptr = np, fptr
+        if os.path.exists(REF_SO):
+            self.L, self.kind = Ref().lib, "reference"
+        else:
+            self.L, self.kind = Oracle().lib, "port"
+
+    def create(self, dim, kb, vb, cap, seed, vm=0.0, hyb=0):
+        if self.kind == "reference":
+            return self.L.adaptq_create(dim, kb, vb, cap, seed, vm, hyb)
+        return self.L.orc_head_create(dim, kb, vb, cap, seed, vm, hyb)
+
+    def destroy(self, h):
+        (self.L.adaptq_destroy if self.kind == "reference" else self.L.orc_head_destroy)(h)
+
+    def reset(self, h):
+        (self.L.adaptq_reset if self.kind == "reference" else self.L.orc_head_reset)(h)
+
+    def append_rows(self, h, k, v):
+        """k, v: contiguous float32 [n][dim]."""
+        n, dim = k.shape
+        if self.kind == "reference":
+            self.L.refx_append_rows(h, self.fptr(k), self.fptr(v), n, dim)
+        else:
+            for t in range(n):
+                self.L.orc_head_append(h, self.fptr(k[t]), self.fptr(v[t]), t)
+
+    def compute(self, h, q, out, reps=1):
+        if self.kind == "reference":
+            return self.L.refx_compute_reps(h, self.fptr(q), self.fptr(out), reps)
+        r = 0
+        for _ in range(reps):
+            r = self.L.orc_head_compute(h, self.fptr(q), self.fptr(out))
+        return r
+
+
+def _timed_threads(work, n_threads, seconds):
+    """Run work(i) repeatedly on n_threads threads for about `seconds`;
+    returns the units done per second (work returns its units)."""
+    done = [0.0] * n_threads
+    t_end = [0.0] * n_threads
+    t0 = time.perf_counter()
+
+    def run(i):
+        units = 0.0
+        while time.perf_counter() - t0 < seconds:
+            units += work(i)
+        done[i] = units
+        t_end[i] = time.perf_counter()
+
+    ts = [threading.Thread(target=run, args=(i,)) for i in range(n_threads)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    return sum(done) / (max(t_end) - t0)
+
+
+def cpu_baseline(cfg, seconds=12.0, seed=0):
+    """The reference's CPU path on this host, on a bounded sample of the bench
+    workload: heads of the bench shape (d128 K4/V2, 8,192 tokens, v_mass 0,
+    hybrid 0), one per thread.  Append: reset, then the 8,192 rows again and
+    again; decode: compute() again and again over a full ring.  Each is timed
+    on one thread (the reference's execution model: the Engine walks heads
+    serially) and on one thread per usable CPU (independent heads; the
+    reference's C ABI allows concurrent calls on different handles).
+    `seconds` is split over the four timings."""
+    np = __import__("numpy")
+    ref = _CpuRef()
+    cpus = host_cpus()
+    T = cpus["usable"]
+    dim, n, kb, vb = cfg["dim"], cfg["ctx"], cfg["k_bits"], cfg["v_bits"]
+    rng = np.random.default_rng(seed)
+    heads = [ref.create(dim, kb, vb, n, 1000 + h) for h in range(T)]
+    kv = [rng.standard_normal((2, n, dim), dtype=np.float32) for _ in range(min(T, 4))]
+    q = rng.standard_normal((T, dim)).astype(np.float32)
+    outs = np.zeros((T, dim), np.float32)
+
+    def append_work(i):
+        ref.reset(heads[i])
+        x = kv[i % len(kv)]
+        ref.append_rows(heads[i], x[0], x[1])
+        return float(n)
+
+    def decode_work(i):
+        reps = 8
+        ref.compute(heads[i], q[i], outs[i], reps)
+        return float(reps * n)
+
+    quarter = seconds / 4
+    app1 = _timed_threads(append_work, 1, quarter)
+    appT = _timed_threads(append_work, T, quarter)  # also leaves every ring full
+    dec1 = _timed_threads(decode_work, 1, quarter)
+    decT = _timed_threads(decode_work, T, quarter)
+    for h in heads:
+        ref.destroy(h)
+    db, ab = decode_bytes_per_token(dim, kb, vb), append_bytes_per_token(dim, dim, kb, vb)
     return {
-        "value": multi, "unit": "token*heads/s", "cores": heads, "kind": kind,
-        "sample": f"{heads} heads x {n} tokens, d{dim} K{cfg['k_bits']}/V{cfg['v_bits']}, "
-                  f"v_mass=0, hybrid=0; compute() repeated ~{seconds:.0f}s "
-                  f"(1/3 on 1 thread, 2/3 on {heads} threads); CPU: {model}",
-        "single_thread_value": single,
-        "gb_per_s": multi * decode_bytes_per_token(dim, cfg["k_bits"], cfg["v_bits"]) / 1e9,
+        "value": decT, "unit": "token*heads/s", "cores": T, "threads": T, "kind": ref.kind,
+        "sample": f"{T} heads (one per thread) x {n} tokens, d{dim} K{kb}/V{vb}, v_mass=0, "
+                  f"hybrid=0; append = reset + {n} rows, decode = compute() over the full "
+                  f"ring, each repeated ~{quarter:.1f}s on 1 thread and ~{quarter:.1f}s on "
+                  f"{T} threads",
+        "cpu_model": cpus["model"], "affinity_cpus": cpus["affinity"],
+        "cgroup_cpu_quota": cpus["cgroup_quota"],
+        "decode": {"token_heads_per_s": decT, "gb_per_s": decT * db / 1e9,
+                   "single_thread_token_heads_per_s": dec1,
+                   "single_thread_gb_per_s": dec1 * db / 1e9},
+        "append": {"token_heads_per_s": appT, "gb_per_s": appT * ab / 1e9,
+                   "single_thread_token_heads_per_s": app1,
+                   "single_thread_gb_per_s": app1 * ab / 1e9},
     }
+
+
+def cpu_configs(threads):
+    """The reference's CPU path on BASELINE configs[0..3] (same shapes and
+    data distributions as the GPU secondary timings; data from numpy): per
+    config, the append and the decode step, timed once on one thread (the
+    Engine's serial walk over heads) and once with the heads spread over
+    `threads` threads.  Returns µs per operation."""
+    np = __import__("numpy")
+    from concurrent.futures import ThreadPoolExecutor
+    ref = _CpuRef()
+    res = {}
+    pool = ThreadPoolExecutor(max_workers=threads)
+
+    def spread(fn, items):
+        """fn over items, each thread taking one contiguous share."""
+        items = list(items)
+        shares = [items[i::threads] for i in range(threads)]
+        list(pool.map(lambda sh: [fn(x) for x in sh], shares))
+
+    def both(fn, items):
+        items = list(items)
+        t0 = time.perf_counter()
+        for it in items:
+            fn(it)
+        one = (time.perf_counter() - t0) * 1e6
+        t0 = time.perf_counter()
+        spread(fn, items)
+        many = (time.perf_counter() - t0) * 1e6
+        return {"us_1_thread": one, f"us_{threads}_threads": many}
+
+    # C1: 4 heads d64 K4/V2, 2,048 tokens; dense and Engine defaults
+    rng = np.random.default_rng(42)
+    K = rng.standard_normal((4, 2048, 64), dtype=np.float32)
+    V = rng.standard_normal((4, 2048, 64), dtype=np.float32)
+    q = rng.standard_normal((4, 64), dtype=np.float32)
+    out = np.zeros((4, 64), np.float32)
+    c1 = {}
+    for name, vm, hyb in (("dense", 0.0, 0), ("engine_defaults_sparse_v", 0.95, 512)):
+        hs = [ref.create(64, 4, 2, 2048, 42 + h, vm, hyb) for h in range(4)]
+        c1[name + "_append_2048"] = both(lambda h: ref.append_rows(hs[h], K[h], V[h]), range(4))
+        c1[name + "_decode"] = both(lambda h: ref.compute(hs[h], q[h], out[h]), range(4))
+        for x in hs:
+            ref.destroy(x)
+    res["C1"] = c1
+
+    # C2: 24 layers x 14 heads d64, 512 tokens, layer 0 K16/V2, channels 3/17 x20
+    nl, nh, n = 24, 14, 512
+    kv = rng.standard_normal((2, nl, nh, n, 64), dtype=np.float32)
+    q = rng.standard_normal((nl, nh, 64), dtype=np.float32)
+    for x in (kv, q):
+        x[..., [3, 17]] *= 20.0
+    out = np.zeros((nl, nh, 64), np.float32)
+    c2 = {}
+    units = [(l, h) for l in range(nl) for h in range(nh)]
+    for name, vm, hyb in (("packed", 0.0, 0), ("hybrid_fp32", 0.95, 512)):
+        hs = {(l, h): ref.create(64, 16 if l == 0 else 4, 2, n, (42 ^ l) + h, vm, hyb)
+              for l, h in units}
+        c2[name + "_append_512"] = both(lambda u: ref.append_rows(hs[u], kv[0][u], kv[1][u]), units)
+        c2[name + "_decode_step"] = both(lambda u: ref.compute(hs[u], q[u], out[u]), units)
+        for x in hs.values():
+            ref.destroy(x)
+    res["C2"] = c2
+
+    # C3: 22 layers x 4 heads d64 (layer 0 K16/V2, others K3/V2), Student-t(4)/sqrt 2:
+    # 1,024-token bulk append, then 256 steps of (append one token + decode)
+    nl, nh, n0, steps = 22, 4, 1024, 256
+    t4 = lambda *shape: (rng.standard_t(4, size=shape) / np.sqrt(2.0)).astype(np.float32)
+    bulk = t4(2, nl, nh, n0, 64)
+    per = t4(3, nl, nh, steps, 64)
+    units = [(l, h) for l in range(nl) for h in range(nh)]
+    c3 = {}
+    for name, vm, hyb in (("dense", 0.0, 0), ("engine_defaults_sparse_v", 0.95, 512)):
+        hs = {(l, h): ref.create(64, 16 if l == 0 else 3, 2, 1280, l * 7 + h, vm, hyb)
+              for l, h in units}
+        c3[name + "_bulk_append_1024"] = both(lambda u: ref.append_rows(hs[u], bulk[0][u], bulk[1][u]),
+                                              units)
+        def steps_of(u):
+            hh, l, h = hs[u], u[0], u[1]
+            res_o = np.zeros(64, np.float32)
+            for s_ in range(steps):
+                ref.append_rows(hh, per[0, l, h, s_:s_ + 1], per[1, l, h, s_:s_ + 1])
+                ref.compute(hh, per[2, l, h, s_], res_o)
+        t0 = time.perf_counter()
+        for u in units:
+            steps_of(u)
+        one = (time.perf_counter() - t0) * 1e6 / steps
+        # the same 256 steps again on fresh rings, heads over the threads
+        for x in hs.values():
+            ref.destroy(x)
+        hs = {(l, h): ref.create(64, 16 if l == 0 else 3, 2, 1280, l * 7 + h, vm, hyb)
+              for l, h in units}
+        spread(lambda u: ref.append_rows(hs[u], bulk[0][u], bulk[1][u]), units)
+        t0 = time.perf_counter()
+        spread(steps_of, units)
+        many = (time.perf_counter() - t0) * 1e6 / steps
+        c3[name + "_per_step"] = {"us_1_thread": one, f"us_{threads}_threads": many}
+        for x in hs.values():
+            ref.destroy(x)
+    res["C3"] = c3
+
+    # C4: 8 heads d128 K4/V4, capacity 32,768, 40,000 tokens (7,232 evictions), 64 queries
+    nh, cap, ntok, nq = 8, 32768, 40000, 64
+    K = rng.standard_normal((nh, ntok, 128), dtype=np.float32)
+    V = rng.standard_normal((nh, ntok, 128), dtype=np.float32)
+    Q = rng.standard_normal((nq, nh, 128), dtype=np.float32)
+    out = np.zeros((nh, 128), np.float32)
+    c4 = {}
+    for name, vm, hyb in (("dense", 0.0, 0), ("engine_defaults_sparse_v", 0.95, 512)):
+        hs = [ref.create(128, 4, 4, cap, 7 + h, vm, hyb) for h in range(nh)]
+        c4[name + "_append_40000"] = both(lambda h: ref.append_rows(hs[h], K[h], V[h]), range(nh))
+        if vm == 0.0:
+            def q64(h):
+                for j in range(nq):
+                    ref.compute(hs[h], Q[j, h], out[h])
+            c4["dense_queries_64"] = both(q64, range(nh))
+        c4[name + "_query_1"] = both(lambda h: ref.compute(hs[h], Q[0, h], out[h]), range(nh))
+        for x in hs:
+            ref.destroy(x)
+    res["C4"] = c4
+    pool.shutdown()
+    res["kind"] = ref.kind
+    res["note"] = ("µs per operation over all heads of the config, reference CPU path, "
+                   "1 thread (serial over heads) and %d threads (heads spread)" % threads)
+    return res
 
 
 def secondary(L, last_error, torch, np, stream, reps=20, which=("C1", "C2", "C3", "C4")):
@@ -365,6 +571,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-configs", action="store_true",
+                    help="skip the reference CPU timings of BASELINE configs[0..3]")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the timings of BASELINE configs[0..3]")
     ap.add_argument("--only", default="",
@@ -471,13 +679,26 @@ def main():
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(args.steps)]
     torch.cuda.synchronize()
+    failed = 0
     t_wall = time.perf_counter()
     for a, b in evs:
         a.record(stream)
-        L.adaptq_plan_compute_device(plan, qp, op, sptr)
+        failed += L.adaptq_plan_compute_device(plan, qp, op, sptr) != 0
         b.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_wall
+    if failed:
+        sys.exit(f"bench: {failed} of {args.steps} timed decode calls failed: {_lib.last_error()}")
+    # Every output is finite and inside the bound any decode of these rings
+    # obeys: out_j = sum_t p_t vscale_t (H CB[c_t])_j / p, |(H y)_j| <= p max|CB|,
+    # so |out_j| <= max|CB_V| * max_t ||v_t||; an N(0, s^2) row of 128 entries
+    # has norm below 2 s sqrt(128) with overwhelming probability.
+    out_ok = bool(torch.isfinite(out).all().item())
+    out_max = float(out.abs().max().item())
+    out_bound = 1.5104 * float(scales.max().item()) * 2.0 * (dim ** 0.5)
+    if not out_ok or out_max > out_bound:
+        sys.exit(f"bench: decode outputs fail the check (finite={out_ok}, max |out| {out_max:.3g} "
+                 f"> bound {out_bound:.3g})")
     kern_ms = [a.elapsed_time(b) for a, b in evs]
     ms = float(np.mean(kern_ms))
     ms_per_step = wall * 1e3 / args.steps
@@ -492,6 +713,12 @@ def main():
     # the headline stack stays resident (~9 GB) while the secondary configs run
     sec = None if args.no_secondary else secondary(L, _lib.last_error, torch, np, stream)
     cpu = None if args.no_cpu else cpu_baseline(cfg, args.cpu_seconds)
+    append_rate = append_tokens / (append_ms * 1e-3)
+    if cpu is not None:
+        cpu["decode"]["gpu_over_cpu"] = value / cpu["decode"]["token_heads_per_s"]
+        cpu["append"]["gpu_over_cpu"] = append_rate / cpu["append"]["token_heads_per_s"]
+        if not args.no_cpu_configs:
+            cpu["configs"] = cpu_configs(cpu["threads"])
 
     line = {
         "metric": "decode attn tokens*heads/s over packed KV + achieved HBM GB/s (% of peak)",
@@ -517,8 +744,9 @@ def main():
             "kernel": "decode_lut_kernel<128,4,2>", "bytes_per_launch": bytes_launch,
             "kernel_ms": ms, "kernel_ms_median": ms_median,
         },
+        "outputs_checked": {"finite": out_ok, "max_abs": out_max, "bound": out_bound},
         "append": {
-            "token_heads_per_s": append_tokens / (append_ms * 1e-3),
+            "token_heads_per_s": append_rate,
             "gb_per_s": append_bytes / (append_ms * 1e-3) / 1e9,
             "frac_hbm": append_bytes / (append_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "ms_total": append_ms,

@@ -141,6 +141,15 @@ int adaptq_read_slots(adaptq_ctx_t ctx, int first_slot, int count,
                       uint8_t *k_codes, uint8_t *v_codes, float *k_scale,
                       float *v_scale);
 
+/* Extension, no counterpart in the reference.  For parity checks of the
+ * sparse-V selection (attention.cpp:448-473): decodes `query` like
+ * adaptq_compute and writes, for each cached token in ring order (oldest
+ * first), the weight (p_t * vscale_t) / sqrt(padded) its V row is summed
+ * with, 0 for tokens outside the selection.  weights: host [ring size].
+ * Returns the ring size (0 when empty), -1 when the context does not take
+ * the sparse-V branch or on error. */
+int adaptq_sparse_weights(adaptq_ctx_t ctx, const float *query, float *weights);
+
 /* Extension, no counterpart in the reference.  For callers that batch over
  * heads: the context of head head_idx of an MHA (NULL if out of range). */
 adaptq_ctx_t adaptq_mha_head(adaptq_mha_t mha, int head_idx);

@@ -81,6 +81,8 @@ class Oracle:
         L.orc_head_append.argtypes = [C.c_void_p, _f, _f, C.c_int]
         L.orc_head_compute.argtypes = [C.c_void_p, _f, _f]
         L.orc_head_compute.restype = C.c_int
+        L.orc_head_compute_sel.argtypes = [C.c_void_p, _f, _f, _f]
+        L.orc_head_compute_sel.restype = C.c_int
         L.orc_head_compute_batch.argtypes = [C.c_void_p, _f, C.c_int, _f]
         L.orc_head_compute_batch.restype = C.c_int
         L.orc_head_reset.argtypes = [C.c_void_p]
@@ -168,6 +170,16 @@ class OracleHead:
         n = self.L.orc_head_compute(self.h, fptr(q), fptr(out))
         return out, n
 
+    def sparse_weights(self, q):
+        """Sparse-V selection of one query: per-token weights (p * vscale) *
+        isp in ring order (oldest first), 0 for tokens left out."""
+        q = np.ascontiguousarray(q, np.float32)
+        out = np.zeros(self.dim, np.float32)
+        n = self.info()["size"]
+        w = np.full(max(n, 1), np.nan, np.float32)
+        self.L.orc_head_compute_sel(self.h, fptr(q), fptr(out), fptr(w))
+        return w[:n]
+
     def compute_batch(self, qs):
         qs = np.ascontiguousarray(qs, np.float32)
         nq = qs.shape[0]
@@ -238,6 +250,10 @@ class Ref:
         L.adaptq_kv_bytes.argtypes = [C.c_void_p]
         L.adaptq_kv_bytes.restype = C.c_size_t
         L.adaptq_version.restype = C.c_char_p
+        L.adaptq_reset.argtypes = [C.c_void_p]
+        L.refx_append_rows.argtypes = [C.c_void_p, _f, _f, C.c_int, C.c_int]
+        L.refx_compute_reps.argtypes = [C.c_void_p, _f, _f, C.c_int]
+        L.refx_compute_reps.restype = C.c_int
 
     def rademacher(self, n: int, seed: int) -> np.ndarray:
         D = np.empty(n, np.int8)

@@ -408,6 +408,14 @@ static void vaccum(float *acc, const uint8_t *row, const float *cb, float w,
 }
 
 int orc_head_compute(const orc_head *h, const float *q, float *out) {
+  return orc_head_compute_sel(h, q, out, NULL);
+}
+
+/* orc_head_compute, and on the sparse-V branch the selection: sel_w[t] (t in
+ * ring order, oldest first) = the weight (p_t * vscale_t) * isp the token's V
+ * row is accumulated with, 0 for tokens left out.  sel_w is untouched on the
+ * other branches. */
+int orc_head_compute_sel(const orc_head *h, const float *q, float *out, float *sel_w) {
   const int n = h->size, cap = h->cap, dim = h->dim, p = h->padded;
   if (!n) {
     memset(out, 0, sizeof(float) * (size_t)dim);
@@ -569,13 +577,15 @@ int orc_head_compute(const orc_head *h, const float *q, float *out) {
         ord[i].i = i;
       }
       qsort(ord, (size_t)n, sizeof(pidx), cmp_desc);
+      if (sel_w) memset(sel_w, 0, sizeof(float) * (size_t)n);
       float mass = 0.0f;
       int ii = 0;
       for (; ii + 3 < n && mass < h->v_mass; ii += 4) {
         for (int k = 0; k < 4; ++k) {
           int t = ord[ii + k].i, s = slots[t];
-          vaccum(acc, h->v_data + (size_t)s * h->v_pb, vcb,
-                 logits[t] * h->v_scale[s] * isp, p, h->v_bits, idx);
+          float w = logits[t] * h->v_scale[s] * isp;
+          if (sel_w) sel_w[t] = w;
+          vaccum(acc, h->v_data + (size_t)s * h->v_pb, vcb, w, p, h->v_bits, idx);
         }
         float q4 = ((logits[ord[ii].i] + logits[ord[ii + 1].i]) + logits[ord[ii + 2].i]) +
                    logits[ord[ii + 3].i];
@@ -584,8 +594,9 @@ int orc_head_compute(const orc_head *h, const float *q, float *out) {
       for (; ii < n && mass < h->v_mass; ++ii) {
         int t = ord[ii].i, s = slots[t];
         float w = logits[t];
-        vaccum(acc, h->v_data + (size_t)s * h->v_pb, vcb, w * h->v_scale[s] * isp, p,
-               h->v_bits, idx);
+        float ws = w * h->v_scale[s] * isp;
+        if (sel_w) sel_w[t] = ws;
+        vaccum(acc, h->v_data + (size_t)s * h->v_pb, vcb, ws, p, h->v_bits, idx);
         mass += w;
       }
       free(ord);

@@ -45,6 +45,10 @@ void   orc_head_destroy(orc_head *h);
 void   orc_head_append(orc_head *h, const float *key, const float *val,
                        int pos);
 int    orc_head_compute(const orc_head *h, const float *q, float *out);
+/* The same, and on the sparse-V branch each token's selection weight in ring
+ * order (0 = left out) into sel_w[n]. */
+int    orc_head_compute_sel(const orc_head *h, const float *q, float *out,
+                            float *sel_w);
 int    orc_head_compute_batch(const orc_head *h, const float *qs, int nq,
                               float *outs);
 void   orc_head_reset(orc_head *h);

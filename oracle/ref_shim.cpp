@@ -6,6 +6,7 @@
 // points for the pieces below the reference's C ABI (codec functions and the
 // ring contents of one AttentionHead), so tests can compare our restatement
 // with the reference bit for bit.  Nothing here restates any algorithm.
+#include "adaptq.h"
 #include "attention.h"
 #include "codebook.h"
 #include "fwht.h"
@@ -84,6 +85,21 @@ void refx_head_read_slots(void *h, int first, int count, uint8_t *kc,
     ks[i] = b.k_scale[s];
     vs[i] = b.v_scale[s];
   }
+}
+
+// Timing loops over the reference's own C ABI (include/adaptq.h), so a CPU
+// baseline measures the reference's append and compute, not one foreign call
+// per token: rows t = 0..n-1 of keys/vals ([n][dim]) at positions t, and one
+// query decoded `reps` times.
+void refx_append_rows(void *ctx, const float *keys, const float *vals, int n, int dim) {
+  for (int t = 0; t < n; ++t)
+    adaptq_append(static_cast<adaptq_ctx_t>(ctx), keys + (size_t)t * dim, vals + (size_t)t * dim, t);
+}
+
+int refx_compute_reps(void *ctx, const float *q, float *out, int reps) {
+  int r = 0;
+  for (int i = 0; i < reps; ++i) r = adaptq_compute(static_cast<adaptq_ctx_t>(ctx), q, out);
+  return r;
 }
 
 }  // extern "C"
