@@ -68,6 +68,8 @@ SIGNATURES = {
     "adaptq_plan_append_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,
                                             C.c_int, C.c_void_p]),
     "adaptq_plan_compute_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
+    "adaptq_plan_compute_device_static": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p,
+                                                    C.c_void_p]),
 }
 
 FEAT_AVX2, FEAT_HYBRID, FEAT_SPARSE_V, FEAT_HIP = 1, 2, 4, 8

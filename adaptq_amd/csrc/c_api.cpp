@@ -26,6 +26,14 @@
 #include "device.hpp"
 #include "launch.hpp"
 
+// Workspace of the allocation-free decode (adaptq_plan_compute_device_static):
+// one copy per GPU, held from the code object's load until the process ends.
+// Host code never passes `scratch` itself to a kernel (on the host it is only
+// a stand-in for the symbol): set-up reads each device's address of it with
+// hipGetSymbolAddress (DevSync::scratch) and that address is what kernels get.
+constexpr size_t kScratchBytes = (size_t)8 << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
 namespace {
 
 thread_local char tl_error[256] = "";
@@ -107,31 +115,51 @@ struct DevSync {
     hipEvent_t ev;
     bool fresh;  // recorded, not yet waited on by the library stream
   };
-  Caller caller[kMaxCallerStreams];
+  Caller caller[kMaxCallerStreams];  // events created with the stream
   int n_caller = 0;
   int evict = 0;
+  void *scratch = nullptr;  // this device's address of the static scratch
 };
 
 DevSync g_dev[kMaxDevices];
 
 DevSync *dev_sync(int dev) { return dev >= 0 && dev < kMaxDevices ? &g_dev[dev] : nullptr; }
 
-// Caller holds d->mu; dev is the current device.
+// Per-device set-up, once, with the device current (caller holds d->mu):
+// the library stream, its event, one event per caller-stream slot and the
+// device's address of the static scratch.  Everything a later call needs is
+// made here, so the calls themselves create nothing.
 hipError_t ensure_lib(DevSync *d) {
   if (d->lib) return hipSuccess;
   hipStream_t s = nullptr;
   // blocking (synchronises with the null stream), default priority
   hipError_t e = hipStreamCreateWithFlags(&s, hipStreamDefault);
   if (e != hipSuccess) return e;
-  hipEvent_t ev = nullptr;
-  e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+  hipEvent_t evs[1 + kMaxCallerStreams] = {};
+  int made = 0;
+  for (; made < 1 + kMaxCallerStreams && e == hipSuccess; ++made)
+    e = hipEventCreateWithFlags(&evs[made], hipEventDisableTiming);
+  void *sp = nullptr;
+  if (e == hipSuccess) e = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));
   if (e != hipSuccess) {
+    for (int i = 0; i < made; ++i)
+      if (evs[i]) (void)hipEventDestroy(evs[i]);
     (void)hipStreamDestroy(s);
     return e;
   }
+  d->lib_ev = evs[0];
+  for (int i = 0; i < kMaxCallerStreams; ++i) d->caller[i].ev = evs[1 + i];
+  d->scratch = sp;
   d->lib = s;
-  d->lib_ev = ev;
   return hipSuccess;
+}
+
+// Set-up of the current device (context creation calls it).
+hipError_t init_device(int dev) {
+  DevSync *d = dev_sync(dev);
+  if (!d) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> g(d->mu);
+  return ensure_lib(d);
 }
 
 // Caller holds d->mu: the library stream waits on every fresh caller event.
@@ -250,10 +278,9 @@ hipError_t caller_end(int dev, hipStream_t s) {
   for (int i = 0; i < d->n_caller && !c; ++i)
     if (d->caller[i].s == s) c = &d->caller[i];
   if (!c) {
+    if (!d->lib) return hipErrorNotInitialized;  // a context's creation sets the device up
     if (d->n_caller < kMaxCallerStreams) {
-      c = &d->caller[d->n_caller];
-      hipError_t e = hipEventCreateWithFlags(&c->ev, hipEventDisableTiming);
-      if (e != hipSuccess) return e;
+      c = &d->caller[d->n_caller];  // its event was made at set-up
       ++d->n_caller;
     } else {
       // reuse the slot of another stream once the library stream has
@@ -416,6 +443,10 @@ Ctx *create_ctx(int dim, int k_bits, int v_bits, int capacity, uint64_t seed, fl
   if (hipGetDevice(&c->device) != hipSuccess || c->device < 0 || c->device >= kMaxDevices) {
     delete c;
     set_errorf(fn, "no HIP device available");
+    return nullptr;
+  }
+  if (hip_fail(init_device(c->device), fn)) {
+    delete c;
     return nullptr;
   }
   c->dim = dim;
@@ -640,8 +671,10 @@ struct Plan {
 };
 
 // Scan of the plan's contexts (caller holds p->mu): flushes staged host
-// appends (library stream) and caches branch and largest ring size.
-bool plan_scan(Plan *p, const char *fn) {
+// appends (library stream) and caches branch and largest ring size.  With
+// flush = false (the allocation-free entry point: a flush may allocate
+// staging memory) staged host appends are an error instead.
+bool plan_scan(Plan *p, const char *fn, bool flush = true) {
   if (p->seen != 0 && g_epoch.load(std::memory_order_acquire) == p->seen) return true;
   const uint64_t e0 = g_epoch.load(std::memory_order_acquire);
   int max_n = 0;
@@ -649,6 +682,10 @@ bool plan_scan(Plan *p, const char *fn) {
   Mode mode = Mode::Dense;
   for (Ctx *c : p->ctxs) {
     std::lock_guard<std::mutex> g(c->mu);
+    if (!flush && c->staged > 0) {
+      set_errorf(fn, "a context holds staged host appends; flush it first (adaptq_flush)");
+      return false;
+    }
     if (!flush_locked(c, fn)) return false;
     if (c->st.size > 0) {
       const Mode m = mode_of(c);
@@ -1554,6 +1591,36 @@ int adaptq_plan_append_device(adaptq_plan_t h, const float *d_keys, const float 
   else
     bump_epoch();
   return 0;
+}
+
+int adaptq_plan_compute_device_static(adaptq_plan_t h, const float *d_queries, float *d_outs,
+                                      void *stream) {
+  const char *fn = "adaptq_plan_compute_device_static";
+  if (!require_handle(h, fn) || !require_pointer(d_queries, fn, "d_queries") ||
+      !require_pointer(d_outs, fn, "d_outs"))
+    return -1;
+  Plan *p = static_cast<Plan *>(h);
+  std::lock_guard<std::mutex> gp(p->mu);
+  if (!plan_scan(p, fn, false)) return -1;
+  DevSync *d = dev_sync(p->device);
+  void *ws = d ? d->scratch : nullptr;  // the device's address of `scratch`, set up at creation
+  if (!ws) {
+    set_errorf(fn, "the device's static scratch is not set up");
+    return -1;
+  }
+  const size_t need = p->mixed ? 0 : plan_ws_floats(p) * 4;
+  if (need > kScratchBytes) {
+    char msg[256];
+    std::snprintf(msg, sizeof(msg),
+                  "%s: the decode needs %zu bytes of workspace, more than the static scratch's "
+                  "%zu; use adaptq_plan_compute_device",
+                  fn, need, kScratchBytes);
+    set_error(msg);
+    return -1;
+  }
+  DeviceGuard g(p->device);
+  return plan_launch_decode(p, d_queries, d_outs, static_cast<float *>(ws),
+                            static_cast<hipStream_t>(stream), fn);
 }
 
 int adaptq_plan_compute_device(adaptq_plan_t h, const float *d_queries, float *d_outs,

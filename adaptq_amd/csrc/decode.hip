@@ -1236,8 +1236,12 @@ SplitPlan decode_plan(int n_items, const DecodeShape &sh) {
 
 }  // namespace
 
-size_t decode_workspace_floats(int n_items, const DecodeShape &sh) {
+size_t decode_workspace_floats(int n_items, const DecodeShape &shape) {
+  DecodeShape sh = shape;
+  if (sh.raw) sh.k_bits = sh.v_bits = 16;  // as launch_decode plans it
   const SplitPlan sp = decode_plan(n_items, sh);
+  // one split through the LUT kernel: the kernel finishes its items itself
+  if (sp.splits == 1 && lut_eligible(sh)) return 0;
   return (size_t)n_items * sp.splits * (sh.padded + 4);
 }
 
@@ -1258,10 +1262,9 @@ hipError_t launch_decode(HeadDesc *const *descs, int n_items, const DecodeShape 
   // queries, outputs and workspace
   for (int c0 = 0; c0 < n_items; c0 += kMaxItemsPerLaunch) {
     const int cnt = n_items - c0 < kMaxItemsPerLaunch ? n_items - c0 : kMaxItemsPerLaunch;
-    const hipError_t e =
-        launch_decode_items(descs + c0, cnt, sh, sp, d_q + (size_t)c0 * sh.dim,
-                            d_out + (size_t)c0 * sh.dim,
-                            d_ws + (size_t)c0 * sp.splits * (sh.padded + 4), s);
+    float *ws = d_ws ? d_ws + (size_t)c0 * sp.splits * (sh.padded + 4) : nullptr;
+    const hipError_t e = launch_decode_items(descs + c0, cnt, sh, sp, d_q + (size_t)c0 * sh.dim,
+                                             d_out + (size_t)c0 * sh.dim, ws, s);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;

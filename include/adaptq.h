@@ -270,6 +270,22 @@ int adaptq_plan_append_device(adaptq_plan_t plan, const float *d_keys,
 int adaptq_plan_compute_device(adaptq_plan_t plan, const float *d_queries,
                                float *d_outs, void *stream);
 
+/* Extension, no counterpart in the reference.  For callers that cannot
+ * allocate memory during a call (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc): adaptq_plan_compute_device with
+ * its workspace in a static device array of the library (8 MiB per GPU, held
+ * until the process ends) instead of memory the plan allocates.  The call
+ * makes no hipMalloc/hipFree or other allocation.  Same results as
+ * adaptq_plan_compute_device.  Returns -1 with a message when the decode
+ * needs more than 8 MiB of workspace (dense plans need none when a context's
+ * ring fits one block per item, about 512 items or more at padded 64/128;
+ * sparse-V needs about 4 bytes per cached token per context) or when a
+ * context holds staged host appends (flush them first).  Every call on a GPU
+ * shares that GPU's array: calls that overlap in time on one GPU (different
+ * streams or threads) race and must be serialised by the caller. */
+int adaptq_plan_compute_device_static(adaptq_plan_t plan, const float *d_queries,
+                                      float *d_outs, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

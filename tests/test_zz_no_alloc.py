@@ -1,0 +1,100 @@
+"""The allocation-free plan decode (adaptq_plan_compute_device_static: the
+workspace in the library's static device scratch) against the allocating one
+(adaptq_plan_compute_device) through the C ABI: two calls in a row, the
+second with a smaller input, on a dense plan whose rings need a split-K
+workspace and on a sparse-V plan; outputs bit-identical (the same kernels
+and split plan run on both).  Also the refusals: a workspace above the
+scratch's size, and staged host appends."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from adaptq_amd import _lib
+from gpu_head import GpuHead, err
+
+pytestmark = pytest.mark.gpu
+L = _lib.lib
+
+
+def _plan(heads):
+    p = L.adaptq_plan_create((C.c_void_p * len(heads))(*[h.h for h in heads]), len(heads))
+    assert p, err()
+    return p
+
+
+def _fill(torch, heads, n, seed):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    dim = heads[0].dim
+    k = torch.randn(len(heads), n, dim, generator=g, device="cuda")
+    v = torch.randn(len(heads), n, dim, generator=g, device="cuda")
+    p = _plan(heads)
+    assert L.adaptq_plan_append_device(p, C.c_void_p(k.data_ptr()), C.c_void_p(v.data_ptr()), n, 0,
+                                       None) == 0, err()
+    return p
+
+
+def _both(torch, plan, n_ctx, dim, seed):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    q = torch.randn(n_ctx, dim, generator=g, device="cuda")
+    a = torch.full((n_ctx, dim), float("nan"), device="cuda")
+    b = torch.full((n_ctx, dim), float("nan"), device="cuda")
+    assert L.adaptq_plan_compute_device(plan, C.c_void_p(q.data_ptr()), C.c_void_p(a.data_ptr()),
+                                        None) == 0, err()
+    assert L.adaptq_plan_compute_device_static(plan, C.c_void_p(q.data_ptr()),
+                                               C.c_void_p(b.data_ptr()), None) == 0, err()
+    torch.cuda.synchronize()
+    a, b = a.cpu().numpy(), b.cpu().numpy()
+    assert np.isfinite(b).all()
+    assert a.tobytes() == b.tobytes()
+
+
+@pytest.mark.parametrize("dim,kb,vb,vm,sizes", [
+    (128, 4, 2, 0.0, [(4, 20000), (2, 3000)]),   # dense, split-K partials in the scratch
+    (64, 4, 2, 0.95, [(3, 5000), (2, 1500)]),    # sparse-V, selection workspace in the scratch
+    (64, 3, 2, 0.95, [(2, 10000), (1, 9000)]),   # sparse-V with the device-wide sort
+])
+def test_static_matches_allocating(dim, kb, vb, vm, sizes):
+    import torch
+    for i, (n_ctx, n) in enumerate(sizes):
+        print(f"no-alloc decode d{dim} K{kb}V{vb} v_mass={vm}: {n_ctx} contexts x {n} tokens",
+              flush=True)
+        heads = [GpuHead(dim, kb, vb, n, 100 * i + h, vm, 0) for h in range(n_ctx)]
+        plan = _fill(torch, heads, n, 7 + i)
+        _both(torch, plan, n_ctx, dim, 11 + i)
+        L.adaptq_plan_destroy(plan)
+
+
+def test_static_refuses_oversized_workspace():
+    import torch
+    print("no-alloc decode: workspace above the scratch", flush=True)
+    # d1024 contexts take the generic kernel: 4 * (1024 + 4) bytes each, and
+    # 2,100 of them exceed the 8 MiB scratch (empty rings: nothing launches)
+    heads = [GpuHead(1024, 4, 2, 1, h) for h in range(2100)]
+    plan = _plan(heads)
+    q = torch.zeros(2100, 1024, device="cuda")
+    out = torch.zeros(2100, 1024, device="cuda")
+    assert L.adaptq_plan_compute_device_static(plan, C.c_void_p(q.data_ptr()),
+                                               C.c_void_p(out.data_ptr()), None) == -1
+    assert "static scratch" in err()
+    L.adaptq_plan_destroy(plan)
+
+
+def test_static_refuses_staged_host_appends():
+    import torch
+    print("no-alloc decode: staged host appends", flush=True)
+    g = GpuHead(64, 4, 2, 64, 3)
+    g.append(np.ones(64, np.float32), np.ones(64, np.float32), 0)
+    plan = _plan([g])
+    q = torch.zeros(1, 64, device="cuda")
+    out = torch.zeros(1, 64, device="cuda")
+    assert L.adaptq_plan_compute_device_static(plan, C.c_void_p(q.data_ptr()),
+                                               C.c_void_p(out.data_ptr()), None) == -1
+    assert "staged" in err()
+    assert L.adaptq_flush(g.h) == 0, err()
+    assert L.adaptq_plan_compute_device_static(plan, C.c_void_p(q.data_ptr()),
+                                               C.c_void_p(out.data_ptr()), None) == 0, err()
+    torch.cuda.synchronize()
+    L.adaptq_plan_destroy(plan)
