@@ -18,6 +18,8 @@
 //                                         4-bit codes by one table lookup)
 //   MSB-first pack                        quantizer.cpp:156-209
 //   ring insert, mirror                   ring_buffer.cpp:105-119, attention.cpp:338-366
+#include <algorithm>
+
 #include "launch.hpp"
 #include "quant.hpp"
 
@@ -156,6 +158,145 @@ __device__ __forceinline__ void load_wave_rows(const float *wave_rows, int lane,
   }
 }
 
+// Codebook indices of the P values in buf (finite), clamped to [nclip, clip]
+// when CLAMP, packed MSB-first into little-endian words
+// (quantizer.cpp:156-209): 4 bits = two codes per byte, high nibble first;
+// 2 bits = four per byte; 3 bits = eight per 24-bit big-endian group.
+template <int P, int B, bool CLAMP>
+__device__ __forceinline__ void pack_codes(const float (&buf)[P], uint32_t (&w)[Row<P, B>::words],
+                                           const Q4Entry *s_q4, float nclip, float clip) {
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    // the reference's two-sided clamp is the median for finite values
+    const float v = CLAMP ? __builtin_amdgcn_fmed3f(buf[i], nclip, clip) : buf[i];
+    const uint32_t q = B == 4 ? quantize_ss4(v, s_q4) : B == 3 ? quantize_ss3(v) : quantize_ss2(v);
+    // Bit position of code i inside the little-endian word stream.
+    int byte, shift;
+    if constexpr (B == 4) {
+      byte = i / 2;
+      shift = (i % 2) ? 0 : 4;
+    } else if constexpr (B == 2) {
+      byte = i / 4;
+      shift = 6 - 2 * (i % 4);
+    } else {
+      // 3-bit: group g = i/8 is the 24-bit big-endian word s0<<21|...|s7.
+      const int g = i / 8, k = i % 8;
+      const int bit = 21 - 3 * k;  // position inside the 24-bit word
+      // byte 0 of the group holds bits 23..16, byte 1 bits 15..8, byte 2 7..0
+      const int lo_byte = 2 - bit / 8, lo_shift = bit % 8;
+      if (lo_shift + 3 <= 8) {
+        byte = 3 * g + lo_byte;
+        shift = lo_shift;
+      } else {
+        // the code straddles two bytes: low part here, high part in byte-1
+        const int b0 = 3 * g + lo_byte;
+        const int nlow = 8 - lo_shift;
+        w[b0 / 4] |= (q & ((1u << nlow) - 1u)) << (8 * (b0 % 4) + lo_shift);
+        const int b1 = b0 - 1;
+        w[b1 / 4] |= (q >> nlow) << (8 * (b1 % 4));
+        continue;
+      }
+    }
+    w[byte / 4] |= q << (8 * (byte % 4) + shift);
+  }
+}
+
+// Encode one vector (P values in buf, zero-padded) of side `side` into ring
+// slot `slot`: the reference's quantize_into (quantizer.cpp:53-137) on the
+// lane's own registers, then the row and its scale leave as whole stores.
+template <int P, int B>
+__device__ __forceinline__ void encode_vec(float (&buf)[P], const HeadDesc *d, int side, int slot,
+                                           float inv_sqrt_p, float sqrt_p, const Q4Entry *s_q4) {
+  uint8_t *codes = side == 0 ? d->k_codes : d->v_codes;
+  float *scales = side == 0 ? d->k_scale : d->v_scale;
+
+  if constexpr (B == 16) {
+    uint32_t w[Row<P, 16>::words];
+#pragma unroll
+    for (int i = 0; i < P; ++i) w[i] = __float_as_uint(buf[i]);
+    store_row<Row<P, 16>::bytes>(codes, w, slot);
+    scales[slot] = 1.0f;
+    return;
+  } else {
+    // ||x||^2 left to right; padded zeros add +0 and change nothing.
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < P; ++i) s = __fadd_rn(s, __fmul_rn(buf[i], buf[i]));
+    const float norm = sqrtf(__fadd_rn(s, 1e-12f));
+    const float inv = 1.0f / norm;
+
+    // Normalise; the sign D[i] = -1 is an exact flip of the sign bit.
+    uint32_t sg[(P + 31) / 32];
+#pragma unroll
+    for (int k = 0; k < (P + 31) / 32; ++k) sg[k] = d->signs[k];
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      const uint32_t flip = (~sg[i / 32] >> (i % 32)) << 31;
+      buf[i] = __uint_as_float(__float_as_uint(__fmul_rn(buf[i], inv)) ^ flip);
+    }
+#pragma unroll
+    for (int len = 1; len < P; len <<= 1) {
+#pragma unroll
+      for (int base = 0; base < P; base += 2 * len) {
+#pragma unroll
+        for (int j = base; j < base + len; ++j) {
+          const float lo = buf[j], hi = buf[j + len];
+          buf[j] = __fadd_rn(lo, hi);
+          buf[j + len] = __fsub_rn(lo, hi);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < P; ++i) buf[i] = __fmul_rn(__fmul_rn(buf[i], inv_sqrt_p), sqrt_p);
+
+    // The clamp to +-3 sigma (quantizer.cpp:81-89) can change a code only if
+    // clip = 3 sigma is not above the largest threshold (0.9816 / 1.7484 /
+    // 2.1476 for 2 / 3 / 4 bits): then every |v| > clip codes as clip does.
+    // sigma is bounded without summing: for s >= 1e-10, ||x/norm||^2 >=
+    // s / (s + 1e-12) less the roundings of s, norm, inv and the products
+    // (< 150 u) >= 0.9899; the butterflies move the norm of H D x/norm by
+    // less than 7 u relative (log2 p stages of u each, a stage scaling norms
+    // by sqrt 2), the two scalings and the sequential sum of squares by less
+    // than (p + 3) u; so sigma^2 = s2 / p + 1e-12 >= 0.9898 and clip >= 2.98.
+    // A wave whose rows all have s >= 1e-10 skips sigma and the clamp; any
+    // other wave (tiny or NaN rows) takes the reference's steps as written.
+    // Either way the codes are the reference's.
+    const bool clamp_inert = __all(s >= 1e-10f);
+    uint32_t w[Row<P, B>::words];
+#pragma unroll
+    for (int k = 0; k < Row<P, B>::words; ++k) w[k] = 0u;
+    bool nan_row;
+    if (clamp_inert) {
+      // A NaN anywhere in the input reaches every element through the FWHT.
+      nan_row = buf[0] != buf[0];
+      pack_codes<P, B, false>(buf, w, s_q4, 0.0f, 0.0f);
+    } else {
+      float s2 = 0.0f;
+#pragma unroll
+      for (int i = 0; i < P; ++i) s2 = __fadd_rn(s2, __fmul_rn(buf[i], buf[i]));
+      const float sigma = sqrtf(__fadd_rn(s2 / (float)P, 1e-12f));
+      const float clip = __fmul_rn(3.0f, sigma);
+      nan_row = s2 != s2;
+      pack_codes<P, B, true>(buf, w, s_q4, -clip, clip);
+    }
+    // A NaN row: every code is the NaN code.
+    if (nan_row) {
+#pragma unroll
+      for (int k = 0; k < Row<P, B>::words; ++k) w[k] = nan_word<B>(k);
+    }
+    constexpr int xmask = kperm_mask(P, B);
+    bool stored = false;
+    if constexpr (xmask != 0) {
+      if (side == 0) {
+        store_row_perm<Row<P, B>::bytes>(codes, w, slot, (uint32_t)slot & (uint32_t)xmask);
+        stored = true;
+      }
+    }
+    if (!stored) store_row<Row<P, B>::bytes>(codes, w, slot);
+    scales[slot] = norm;
+  }
+}
+
 // Encode n_tok tokens of one side (K or V) for n_ctx heads.
 // UNIFORM: block (x, y) holds tokens x * 128 .. of head y, so a wave never
 // mixes heads: the descriptor and sign words are scalar loads and a sign flip
@@ -212,109 +353,7 @@ __device__ __forceinline__ void encode_row(const HeadDesc *d, const RingState st
   }
   if (!write_ring) return;
 
-  uint8_t *codes = side == 0 ? d->k_codes : d->v_codes;
-  float *scales = side == 0 ? d->k_scale : d->v_scale;
-
-  if constexpr (B == 16) {
-    uint32_t w[Row<P, 16>::words];
-#pragma unroll
-    for (int i = 0; i < P; ++i) w[i] = __float_as_uint(buf[i]);
-    store_row<Row<P, 16>::bytes>(codes, w, slot);
-    scales[slot] = 1.0f;
-    return;
-  } else {
-    // ||x||^2 left to right; padded zeros add +0 and change nothing.
-    float s = 0.0f;
-#pragma unroll
-    for (int i = 0; i < P; ++i) s = __fadd_rn(s, __fmul_rn(buf[i], buf[i]));
-    const float norm = sqrtf(__fadd_rn(s, 1e-12f));
-    const float inv = 1.0f / norm;
-
-    // Normalise; the sign D[i] = -1 is an exact flip of the sign bit.
-    uint32_t sg[(P + 31) / 32];
-#pragma unroll
-    for (int k = 0; k < (P + 31) / 32; ++k) sg[k] = d->signs[k];
-#pragma unroll
-    for (int i = 0; i < P; ++i) {
-      const uint32_t flip = (~sg[i / 32] >> (i % 32)) << 31;
-      buf[i] = __uint_as_float(__float_as_uint(__fmul_rn(buf[i], inv)) ^ flip);
-    }
-#pragma unroll
-    for (int len = 1; len < P; len <<= 1) {
-#pragma unroll
-      for (int base = 0; base < P; base += 2 * len) {
-#pragma unroll
-        for (int j = base; j < base + len; ++j) {
-          const float lo = buf[j], hi = buf[j + len];
-          buf[j] = __fadd_rn(lo, hi);
-          buf[j + len] = __fsub_rn(lo, hi);
-        }
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < P; ++i) buf[i] = __fmul_rn(__fmul_rn(buf[i], inv_sqrt_p), sqrt_p);
-
-    float s2 = 0.0f;
-#pragma unroll
-    for (int i = 0; i < P; ++i) s2 = __fadd_rn(s2, __fmul_rn(buf[i], buf[i]));
-    const float sigma = sqrtf(__fadd_rn(s2 / (float)P, 1e-12f));
-    const float clip = __fmul_rn(3.0f, sigma);
-    const float nclip = -clip;
-
-    uint32_t w[Row<P, B>::words];
-#pragma unroll
-    for (int k = 0; k < Row<P, B>::words; ++k) w[k] = 0u;
-#pragma unroll
-    for (int i = 0; i < P; ++i) {
-      // the reference's two-sided clamp is the median for finite values
-      const float v = __builtin_amdgcn_fmed3f(buf[i], nclip, clip);
-      const uint32_t q = B == 4 ? quantize_ss4(v, s_q4) : B == 3 ? quantize_ss3(v) : quantize_ss2(v);
-      // Bit position of code i inside the little-endian word stream.
-      int byte, shift;
-      if constexpr (B == 4) {
-        byte = i / 2;
-        shift = (i % 2) ? 0 : 4;
-      } else if constexpr (B == 2) {
-        byte = i / 4;
-        shift = 6 - 2 * (i % 4);
-      } else {
-        // 3-bit: group g = i/8 is the 24-bit big-endian word s0<<21|...|s7.
-        const int g = i / 8, k = i % 8;
-        const int bit = 21 - 3 * k;  // position inside the 24-bit word
-        // byte 0 of the group holds bits 23..16, byte 1 bits 15..8, byte 2 7..0
-        const int lo_byte = 2 - bit / 8, lo_shift = bit % 8;
-        if (lo_shift + 3 <= 8) {
-          byte = 3 * g + lo_byte;
-          shift = lo_shift;
-        } else {
-          // the code straddles two bytes: low part here, high part in byte-1
-          const int b0 = 3 * g + lo_byte;
-          const int nlow = 8 - lo_shift;
-          w[b0 / 4] |= (q & ((1u << nlow) - 1u)) << (8 * (b0 % 4) + lo_shift);
-          const int b1 = b0 - 1;
-          w[b1 / 4] |= (q >> nlow) << (8 * (b1 % 4));
-          continue;
-        }
-      }
-      w[byte / 4] |= q << (8 * (byte % 4) + shift);
-    }
-    // A NaN anywhere in the input reaches every element (the FWHT sums all of
-    // them), and then s2 is NaN: every code is the NaN code.
-    if (s2 != s2) {
-#pragma unroll
-      for (int k = 0; k < Row<P, B>::words; ++k) w[k] = nan_word<B>(k);
-    }
-    constexpr int xmask = kperm_mask(P, B);
-    bool stored = false;
-    if constexpr (xmask != 0) {
-      if (side == 0) {
-        store_row_perm<Row<P, B>::bytes>(codes, w, slot, (uint32_t)slot & (uint32_t)xmask);
-        stored = true;
-      }
-    }
-    if (!stored) store_row<Row<P, B>::bytes>(codes, w, slot);
-    scales[slot] = norm;
-  }
+  encode_vec<P, B>(buf, d, side, slot, inv_sqrt_p, sqrt_p, s_q4);
 }
 
 template <int P, int B, bool UNIFORM>

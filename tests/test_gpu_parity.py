@@ -67,6 +67,48 @@ def test_append_bit_exact(oracle, dim, kb, vb, family):
     _ring_equal(g, o)
 
 
+@pytest.mark.parametrize("dim,kb,vb", [(128, 4, 2), (64, 2, 3), (128, 3, 4), (32, 4, 4)])
+def test_append_clamp_paths(oracle, dim, kb, vb):
+    """The append kernel skips sigma and the +-3 sigma clamp for a wave whose
+    rows all have sum x^2 >= 1e-10 (provably inert there) and runs the
+    reference's steps for any other wave.  Waves of 64 consecutive tokens:
+    all normal rows (skip); one tiny row among normal ones; rows just above
+    and below the bound; denormal-scale rows; single-spike rows (all FWHT
+    outputs equal in magnitude); rows that rotate to a single value far
+    above 3 sigma (where the clamp acts).  Codes and scales bit-exact."""
+    print(f"append clamp paths dim={dim} k{kb}v{vb}", flush=True)
+    rng = np.random.default_rng(dim + kb * 7 + vb)
+    n = 6 * 64
+    k = rng.standard_normal((n, dim)).astype(np.float32)
+    v = rng.standard_normal((n, dim)).astype(np.float32)
+    k[64 + 17] *= np.float32(1e-7)                       # one tiny row in a normal wave
+    v[64 + 40] *= np.float32(1e-30)
+    b = np.sqrt(1e-10 / dim)                              # rows around s = 1e-10
+    k[128:192] *= np.float32(b) * np.linspace(0.98, 1.02, 64, dtype=np.float32)[:, None]
+    v[128:192] *= np.float32(b) * np.linspace(1.02, 0.98, 64, dtype=np.float32)[:, None]
+    k[192:256] *= np.float32(1e-20)                       # squares underflow
+    v[192:256] *= np.float32(3e-23)
+    k[256:320] = 0.0                                      # single spikes
+    v[256:320] = 0.0
+    for t in range(256, 320):
+        k[t, t % dim] = np.float32(rng.uniform(0.1, 5.0))
+        v[t, (3 * t) % dim] = np.float32(-rng.uniform(0.1, 5.0))
+    seed = int(rng.integers(0, 2**63))
+    g = GpuHead(dim, kb, vb, n, seed)
+    o = oracle.head(dim, kb, vb, n, seed)
+    # rows D . h_j (a Hadamard row under the head's signs) rotate to one
+    # value sqrt(p) and zeros: far above 3 sigma, where the clamp acts
+    D = o.signs().astype(np.float32)[:dim]
+    idx = np.arange(dim)
+    for t in range(320, 384):
+        hj = np.array([(-1) ** bin(i & (t % dim)).count("1") for i in idx], np.float32)
+        hv = np.array([(-1) ** bin(i & ((5 * t) % dim)).count("1") for i in idx], np.float32)
+        k[t] = D * hj * np.float32(rng.uniform(0.5, 2.0))
+        v[t] = D * hv * np.float32(-rng.uniform(0.5, 2.0))
+    _fill([g, o], k, v)
+    _ring_equal(g, o)
+
+
 def test_append_special_values(oracle):
     dim, cap = 64, 32
     rows = [np.zeros(dim, np.float32), np.full(dim, np.nan, np.float32),
