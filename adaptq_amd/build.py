@@ -34,7 +34,7 @@ HIP_FLAGS = [
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
 ]
 
-SOURCES = ["append.hip", "decode.hip", "sparse.hip", "layout.hip", "kbackend.hip", "c_api.cpp", "vtable.cpp"]
+SOURCES = ["append.hip", "decode.hip", "mquery.hip", "sparse.hip", "layout.hip", "kbackend.hip", "c_api.cpp", "vtable.cpp"]
 
 
 def _run(cmd):

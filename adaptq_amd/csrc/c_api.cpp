@@ -620,7 +620,7 @@ int compute_locked(Ctx *c, const float *queries, int nq, float *outs, const char
     c->items_uploaded = nq;
   }
   const size_t wsf = mode == Mode::Sparse ? aq::sparse_workspace_floats(nq, sh)
-                                          : aq::decode_workspace_floats(nq, sh);
+                                          : aq::decode_multi_workspace_floats(nq, 1, sh);
   if (hip_fail(c->d_ws.ensure(wsf * 4), fn)) return -1;
   std::memcpy(c->h_io.p, queries, (size_t)nq * c->dim * 4);
   const float *dq = static_cast<const float *>(c->h_io.dp);
@@ -632,7 +632,7 @@ int compute_locked(Ctx *c, const float *queries, int nq, float *outs, const char
     e = mode == Mode::Sparse
             ? aq::launch_decode_sparse(items, nq, sh, c->v_mass, dq, dout,
                                        static_cast<float *>(c->d_ws.p), s)
-            : aq::launch_decode(items, nq, sh, dq, dout, static_cast<float *>(c->d_ws.p), s);
+            : aq::launch_decode_multi(items, nq, 1, sh, dq, dout, static_cast<float *>(c->d_ws.p), s);
   if (e == hipSuccess) e = lib_wait(c->device, lib_end(c->device));
   if (hip_fail(e, fn)) return -1;
   std::memcpy(outs, static_cast<uint8_t *>(c->h_io.p) + io, (size_t)nq * c->dim * 4);
@@ -820,7 +820,7 @@ int launch_all_locked(Mha *m, const float *dq, float *dout, hipStream_t s, const
   aq::DecodeShape sh{c0->dim, c0->padded, c0->k_bits, c0->v_bits, mode == Mode::Hybrid,
                      n > 0 ? n : 1};
   const size_t wsf = mode == Mode::Sparse ? aq::sparse_workspace_floats(H, sh)
-                                          : aq::decode_workspace_floats(H, sh);
+                                          : aq::decode_multi_workspace_floats(H, m->n_heads, sh);
   if (hip_fail(m->d_ws.ensure(wsf * 4), fn)) return -1;
   auto **items = static_cast<aq::HeadDesc **>(m->d_list.p);
   if (reps > 1) {
@@ -844,8 +844,9 @@ int launch_all_locked(Mha *m, const float *dq, float *dout, hipStream_t s, const
   else if (mode == Mode::Sparse)
     e = aq::launch_decode_sparse(items, H, sh, c0->v_mass, dq, dout,
                                  static_cast<float *>(m->d_ws.p), s);
-  else
-    e = aq::launch_decode(items, H, sh, dq, dout, static_cast<float *>(m->d_ws.p), s);
+  else  // reps queries per head: the multi-query kernel once there are enough
+    e = aq::launch_decode_multi(items, H, m->n_heads, sh, dq, dout,
+                                static_cast<float *>(m->d_ws.p), s);
   if (hip_fail(e, fn)) return -1;
   return n;
 }

@@ -1236,6 +1236,16 @@ SplitPlan decode_plan(int n_items, const DecodeShape &sh) {
 
 }  // namespace
 
+hipError_t launch_finalize(HeadDesc *const *descs, int n_items, int padded, int n_splits,
+                           const float *partials, float *outs, bool inverse_fwht, hipStream_t s) {
+  if (n_items <= 0) return hipSuccess;
+  if (inverse_fwht)
+    finalize_kernel<true><<<n_items, kThreads, 0, s>>>(descs, padded, n_splits, partials, outs, 0);
+  else
+    finalize_kernel<false><<<n_items, kThreads, 0, s>>>(descs, padded, n_splits, partials, outs, 0);
+  return hipGetLastError();
+}
+
 size_t decode_workspace_floats(int n_items, const DecodeShape &shape) {
   DecodeShape sh = shape;
   if (sh.raw) sh.k_bits = sh.v_bits = 16;  // as launch_decode plans it

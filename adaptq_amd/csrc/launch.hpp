@@ -33,6 +33,25 @@ hipError_t launch_decode(HeadDesc *const *d_item_desc, int n_items, const Decode
                          const float *d_queries, float *d_outs, float *d_workspace,
                          hipStream_t stream);
 
+// Merge of split partials (m, l, acc[padded]) per item, laid out
+// [item][split][padded + 4], into outputs [item][dim]: log-sum-exp weights,
+// normalisation, inverse FWHT and signs when V is quantised.
+hipError_t launch_finalize(HeadDesc *const *descs, int n_items, int padded, int n_splits,
+                           const float *partials, float *outs, bool inverse_fwht, hipStream_t s);
+
+// Decode of many queries per head: items [n_items] = n_items / n_heads
+// queries of each of the n_heads heads, item j * n_heads + h being query j of
+// head d_item_desc[h] (the first n_heads items name the heads); queries and
+// outputs [n_items][dim] in item order.  Same results as launch_decode on
+// the same items: with enough queries per head on shapes the MFMA kernel
+// covers (dense branch, quantised K and V, padded 64/128) every K/V tile is
+// read once for all the queries of its head (mquery.hip); otherwise
+// launch_decode runs.
+size_t decode_multi_workspace_floats(int n_items, int n_heads, const DecodeShape &shape);
+hipError_t launch_decode_multi(HeadDesc *const *d_item_desc, int n_items, int n_heads,
+                               const DecodeShape &shape, const float *d_queries, float *d_outs,
+                               float *d_workspace, hipStream_t stream);
+
 // Sparse-V decode (v_mass > 0 on quantised K and V), restating
 // attention.cpp:448-473.  d_workspace must hold sparse_workspace_floats().
 size_t sparse_workspace_floats(int n_items, const DecodeShape &shape);
