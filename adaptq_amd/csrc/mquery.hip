@@ -165,8 +165,18 @@ __global__ __launch_bounds__(256) void mq_rotate_kernel(HeadDesc *const *item_de
   }
   const float *q = queries + (size_t)(j * n_heads + h) * dim;
   const cfloat *qs = (const cfloat *)q;
+  // left to right: the row's 16-entry blocks come in as scalar loads ahead of
+  // their squares
   float sq = 0.0f;
-  for (int e = 0; e < dim; ++e) sq = __fadd_rn(sq, __fmul_rn(qs[e], qs[e]));
+  const int nb = dim / 16;
+  for (int b = 0; b < nb; ++b) {
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = qs[16 * b + k];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) sq = __fadd_rn(sq, __fmul_rn(v[k], v[k]));
+  }
+  for (int e = 16 * nb; e < dim; ++e) sq = __fadd_rn(sq, __fmul_rn(qs[e], qs[e]));
   const float qn = sqrtf(__fadd_rn(sq, 1e-12f));
   const float inv = 1.0f / qn;
   float x[E];

@@ -27,9 +27,11 @@
 // FWHT.  Short rings (up to 3,072 tokens) run the last three steps in one
 // block per item, at padded 64 the logits too (sparse_fused_kernel).
 #include <rocprim/device/device_radix_sort.hpp>
+#include <type_traits>
 
 #include "expf_ref.hpp"
 #include "launch.hpp"
+#include "seqsum.hpp"
 
 namespace aq {
 
@@ -91,8 +93,23 @@ __device__ void rotate_query_exact(float *s_q, const float *q, int dim, int P,
   for (int i = threadIdx.x; i < P; i += blockDim.x) s_q[i] = i < dim ? q[i] : 0.0f;
   __syncthreads();
   if (threadIdx.x == 0) {
+    // left to right; 16 entries' loads in flight ahead of their squares
     float s = 0.0f;
-    for (int i = 0; i < dim; ++i) s = __fadd_rn(s, __fmul_rn(s_q[i], s_q[i]));
+    const float4 *q4 = reinterpret_cast<const float4 *>(s_q);
+    const int nb = dim / 16;
+    for (int b = 0; b < nb; ++b) {
+      float4 v[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[k] = q4[4 * b + k];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        s = __fadd_rn(s, __fmul_rn(v[k].x, v[k].x));
+        s = __fadd_rn(s, __fmul_rn(v[k].y, v[k].y));
+        s = __fadd_rn(s, __fmul_rn(v[k].z, v[k].z));
+        s = __fadd_rn(s, __fmul_rn(v[k].w, v[k].w));
+      }
+    }
+    for (int i = 16 * nb; i < dim; ++i) s = __fadd_rn(s, __fmul_rn(s_q[i], s_q[i]));
     s_qn = sqrtf(__fadd_rn(s, 1e-12f));
   }
   __syncthreads();
@@ -122,26 +139,34 @@ __device__ void rotate_query_exact(float *s_q, const float *q, int dim, int P,
   __syncthreads();
 }
 
-// dot(s_q, CB[codes of row]) with the reference's 8 FMA lanes (lane L takes
-// codes L, L+8, ...) summed pairwise (attention.cpp:83-136).  cbk is the K
-// codebook in LDS (a run-time index into a constant array is a memory load
-// per code).
-// PT = 0: any padded size, codes read byte by byte.  PT = 64/128: the row is
-// read as words; 3-bit rows are in reference order; for 2/4-bit codes
-// reference word w sits at stored word w ^ (x >> 2) with its bytes permuted by
-// b ^ (x & 3) (kperm_mask), and one v_perm per word restores the reference
-// byte order.
 template <int PT, int KB>
-__device__ __forceinline__ float kdot_row(const uint8_t *row, int x, const float *s_q, int P,
-                                          const float *cbk) {
-  float s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  if constexpr (PT != 0 && KB == 3) {
-    // 3-bit rows are unpermuted: 24-bit big-endian groups of 8 codes
-    constexpr int W = PT * 3 / 32;
-    const uint32_t *r32 = reinterpret_cast<const uint32_t *>(row);
-    uint32_t w[W];
+struct KRow {
+  static constexpr int words = PT * KB / 32;  // PT = 64 or 128
+};
+
+// The row's words in reference byte order (PT = 64/128): 3-bit rows are
+// stored so; 2/4-bit rows are XOR-permuted by x = slot & mask.
+template <int PT, int KB>
+__device__ __forceinline__ void kload_row(const uint8_t *row, int x, uint32_t *w) {
+  const uint32_t *r32 = reinterpret_cast<const uint32_t *>(row);
+  if constexpr (KB == 3) {
 #pragma unroll
-    for (int i = 0; i < W; ++i) w[i] = r32[i];
+    for (int i = 0; i < KRow<PT, KB>::words; ++i) w[i] = r32[i];
+  } else {
+    const uint32_t xw = (uint32_t)x >> 2;
+    const uint32_t sel = 0x03020100u ^ (((uint32_t)x & 3u) * 0x01010101u);
+#pragma unroll
+    for (int i = 0; i < KRow<PT, KB>::words; ++i) w[i] = __builtin_amdgcn_perm(0u, r32[i ^ xw], sel);
+  }
+}
+
+// dot(s_q, CB[codes]) of a row given as words in reference order, with the
+// reference's 8 FMA lanes summed pairwise (attention.cpp:83-136)
+template <int PT, int KB>
+__device__ __forceinline__ float kdot_words(const uint32_t *w, const float *s_q, const float *cbk) {
+  float s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if constexpr (KB == 3) {
+    // 24-bit big-endian groups of 8 codes
 #pragma unroll
     for (int g = 0; g < PT / 8; ++g) {
       const int b0 = 3 * g;
@@ -152,14 +177,7 @@ __device__ __forceinline__ float kdot_row(const uint8_t *row, int x, const float
       for (int k = 0; k < 8; ++k)
         s[k] = fmaf(cbk[(w24 >> (21 - 3 * k)) & 7u], s_q[8 * g + k], s[k]);
     }
-  } else if constexpr (PT != 0 && (KB == 2 || KB == 4)) {
-    constexpr int W = PT * KB / 32;
-    const uint32_t *r32 = reinterpret_cast<const uint32_t *>(row);
-    const uint32_t xw = (uint32_t)x >> 2;
-    const uint32_t sel = 0x03020100u ^ (((uint32_t)x & 3u) * 0x01010101u);
-    uint32_t w[W];
-#pragma unroll
-    for (int i = 0; i < W; ++i) w[i] = __builtin_amdgcn_perm(0u, r32[i ^ xw], sel);
+  } else {
 #pragma unroll
     for (int j = 0; j < PT; ++j) {
       int c;
@@ -172,14 +190,32 @@ __device__ __forceinline__ float kdot_row(const uint8_t *row, int x, const float
       }
       s[j & 7] = fmaf(cbk[c], s_q[j], s[j & 7]);
     }
+  }
+  const float t0 = s[0] + s[4], t1 = s[1] + s[5], t2 = s[2] + s[6], t3 = s[3] + s[7];
+  return (t0 + t1) + (t2 + t3);
+}
+
+// dot(s_q, CB[codes of row]) with the reference's 8 FMA lanes (lane L takes
+// codes L, L+8, ...) summed pairwise (attention.cpp:83-136).  cbk is the K
+// codebook in LDS (a run-time index into a constant array is a memory load
+// per code).  PT = 0: any padded size, codes read byte by byte.  PT = 64/128:
+// the row is read as words (kload_row).
+template <int PT, int KB>
+__device__ __forceinline__ float kdot_row(const uint8_t *row, int x, const float *s_q, int P,
+                                          const float *cbk) {
+  if constexpr (PT != 0 && KB >= 2 && KB <= 4) {
+    uint32_t w[KRow<PT, KB>::words];
+    kload_row<PT, KB>(row, x, w);
+    return kdot_words<PT, KB>(w, s_q, cbk);
   } else {
+    float s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     for (int j = 0; j < P; j += 8)
 #pragma unroll
       for (int L = 0; L < 8; ++L)
         if (j + L < P) s[L] = fmaf(cbk[kcode_at<KB>(row, j + L, x)], s_q[j + L], s[L]);
+    const float t0 = s[0] + s[4], t1 = s[1] + s[5], t2 = s[2] + s[6], t3 = s[3] + s[7];
+    return (t0 + t1) + (t2 + t3);
   }
-  const float t0 = s[0] + s[4], t1 = s[1] + s[5], t2 = s[2] + s[6], t3 = s[3] + s[7];
-  return (t0 + t1) + (t2 + t3);
 }
 
 template <int PT, int KB>
@@ -313,6 +349,7 @@ struct SelectShared {
   float bcast[2];
   int cut;
   uint64_t last;
+  SeqShared seq;
 };
 
 // Block maximum with the reference's NaN-skipping compare (x > m ? x : m;
@@ -363,6 +400,97 @@ __device__ __forceinline__ void scan_counts(SelectShared &sh) {
   __syncthreads();
 }
 
+// Stable LSD radix sort, 8 bits a pass, of the n <= 2 kSelThreads keys
+// sh.key[0..n) with payloads sh.idx[0..n) (in: token order; out: sorted, in
+// the same arrays), skipping the digits every key shares (diff: OR ^ AND of
+// the keys).  Position r kSelThreads + t is thread t's in round r; a wave
+// ranks its keys of one digit with 8 ballots (lanes with the same digit
+// below it), leaders record the wave's count of each digit per round, and
+// one exclusive scan in (digit, round, wave) order gives every key its
+// destination.  sh.key / sh.idx from 4,096 on are the second buffer.
+__device__ __forceinline__ void sort8_small(SelectShared &sh, int n, uint32_t diff) {
+  constexpr int R = 2;
+  constexpr int NE = 256 * R * (kSelThreads / 64);  // count entries, 8 per thread
+  static_assert(NE == 8 * kSelThreads, "8 count entries per thread");
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint64_t below = (1ull << lane) - 1ull;
+  uint32_t *kA = sh.key, *kB = sh.key + 4096;
+  uint16_t *iA = sh.idx, *iB = sh.idx + 4096;
+  uint16_t *cnt = sh.cnt;
+  for (int sft = 0; sft < 32; sft += 8) {
+    if (((diff >> sft) & 255u) == 0) continue;
+    reinterpret_cast<uint4 *>(cnt)[tid] = make_uint4(0u, 0u, 0u, 0u);
+    __syncthreads();
+    uint32_t kk[R], dg[R], rk[R];
+    uint16_t ii[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int pos = r * kSelThreads + tid;
+      const bool valid = pos < n;
+      kk[r] = valid ? kA[pos] : 0u;
+      ii[r] = valid ? iA[pos] : (uint16_t)0;
+      dg[r] = (kk[r] >> sft) & 255u;
+      uint64_t same = __ballot(valid);
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const uint64_t m = __ballot((dg[r] >> b) & 1u);
+        same &= ((dg[r] >> b) & 1u) ? m : ~m;
+      }
+      rk[r] = (uint32_t)__popcll(same & below);
+      if (valid && rk[r] == 0u) cnt[(dg[r] * R + r) * 16 + wave] = (uint16_t)__popcll(same);
+    }
+    __syncthreads();
+    // exclusive scan of the counts in (digit, round, wave) order
+    {
+      uint4 *c4 = reinterpret_cast<uint4 *>(cnt) + tid;
+      const uint4 a = *c4;
+      uint32_t w[4] = {a.x, a.y, a.z, a.w};
+      uint32_t run = 0u;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = w[i] & 0xFFFFu, hi = w[i] >> 16;
+        w[i] = run | ((run + lo) << 16);
+        run += lo + hi;
+      }
+      uint32_t incl = run;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += y;
+      }
+      if (lane == 63) sh.wsum[wave] = incl;
+      __syncthreads();
+      uint32_t base = incl - run;
+      for (int k = 0; k < wave; ++k) base += sh.wsum[k];
+      const uint32_t b2 = base * 0x10001u;  // every prefix is below 2^16: no carry between halves
+      *c4 = make_uint4(w[0] + b2, w[1] + b2, w[2] + b2, w[3] + b2);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (r * kSelThreads + tid < n) {
+        const uint32_t dst = (uint32_t)cnt[(dg[r] * R + r) * 16 + wave] + rk[r];
+        kB[dst] = kk[r];
+        iB[dst] = ii[r];
+      }
+    }
+    __syncthreads();
+    uint32_t *tk = kA;
+    kA = kB;
+    kB = tk;
+    uint16_t *ti = iA;
+    iA = iB;
+    iB = ti;
+  }
+  if (kA != sh.key) {
+    for (int i = tid; i < n; i += kSelThreads) {
+      sh.key[i] = kA[i];
+      sh.idx[i] = iA[i];
+    }
+    __syncthreads();
+  }
+}
+
 // Selection for n <= kLdsSort tokens.  Thread t owns tokens E t .. E t + E - 1
 // in registers.  Steps:
 //   1. max of the logits (the reference's start value -1e30 and compare)
@@ -376,14 +504,20 @@ __device__ __forceinline__ void scan_counts(SelectShared &sh) {
 //      (attention.cpp:454-472)
 //   5. per-token weights (p * vscale) * isp for the selected tokens, else 0,
 //      written over the logits in token order
+//   The logits come from lg, or, with lin != null, from the caller's
+//   registers (the same tokens); the weights go to lg and, if given, to wout.
 template <int E>
 __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, float *lg, int n, int s0,
-                             SelectShared &sh) {
+                             SelectShared &sh, const float *lin = nullptr,
+                             float *wout = nullptr) {
   const int tid = threadIdx.x, p0 = tid * E;
   const int cap = d->cap, P = d->padded;
-  float ev[E];
+  float ev[E], l_own[E];
 #pragma unroll
-  for (int e = 0; e < E; ++e) ev[e] = p0 + e < n ? lg[p0 + e] : 0.0f;
+  for (int e = 0; e < E; ++e) ev[e] = p0 + e < n ? (lin ? lin[e] : lg[p0 + e]) : 0.0f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) l_own[e] = ev[e];
+  if (!wout) wout = lg;
   float mx = -1e30f;
 #pragma unroll
   for (int e = 0; e < E; ++e)
@@ -433,6 +567,15 @@ __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, fl
   }
   __syncthreads();
 
+  if constexpr (E <= 2) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      sh.key[p0 + e] = k[e];
+      sh.idx[p0 + e] = (uint16_t)ix[e];
+    }
+    __syncthreads();
+    sort8_small(sh, n, diff);
+  } else {
   for (int sft = 0; sft < 32; sft += 4) {
     if (((diff >> sft) & 15u) == 0) continue;
     // counts of each digit among this thread's tokens (8-bit fields) and the
@@ -476,6 +619,7 @@ __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, fl
     sh.idx[p0 + e] = (uint16_t)ix[e];
   }
   __syncthreads();
+  }
 
   const int n_quads = n / 4;
   for (int q = tid; q < n_quads; q += blockDim.x)
@@ -483,11 +627,16 @@ __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, fl
                                       hi_p(sh.key[4 * q + 2])),
                             hi_p(sh.key[4 * q + 3]));
   __syncthreads();
+  // the mass loop, on one lane
   if (tid == 0) {
     float mass = 0.0f;
     int ii = 4 * mass_scan(sh.stage, n_quads, v_mass, &mass);
     for (; ii < n && mass < v_mass; ++ii) mass = __fadd_rn(mass, hi_p(sh.key[ii]));
     sh.cut = ii;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    const int ii = sh.cut;
     sh.last = ii > 0 ? ((uint64_t)sh.key[ii - 1] << 32) | sh.idx[ii - 1] : 0;
   }
   __syncthreads();
@@ -498,19 +647,20 @@ __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, fl
   const int cut = sh.cut;
   const uint64_t last = sh.last;
   const float isp = 1.0f / sqrtf((float)P);
-  float lv[E], vs[E];
+  float vs[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int t = p0 + e;
-    lv[e] = t < n ? lg[t] : 0.0f;
     vs[e] = t < n ? d->v_scale[ring_slot(s0, t, cap)] : 0.0f;
   }
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int t = p0 + e;
     if (t < n) {
-      const float p = __fmul_rn(expf_ref(lv[e] - mx), inv);
-      lg[t] = cut > 0 && make_key(p, t) <= last ? __fmul_rn(__fmul_rn(p, vs[e]), isp) : 0.0f;
+      const float p = __fmul_rn(expf_ref(l_own[e] - mx), inv);
+      const float w = cut > 0 && make_key(p, t) <= last ? __fmul_rn(__fmul_rn(p, vs[e]), isp) : 0.0f;
+      wout[t] = w;
+      if (wout != lg) lg[t] = w;  // the workspace keeps every launch's weights
     }
   }
 }
@@ -571,20 +721,20 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
   mx = s_red[0];
   __syncthreads();
 
-  // 2. exponentials and their left-to-right sum
-  float sv = 0.0f;
-  for (int base = 0; base < n; base += kStage) {
-    const int m = n - base < kStage ? n - base : kStage;
-    for (int i = tid; i < m; i += blockDim.x) {
-      const float e = expf_ref(lg[base + i] - mx);
-      lg[base + i] = e;
-      s_stage[i] = e;
-    }
-    __syncthreads();
-    if (tid == 0) sv = serial_sum(s_stage, m, sv);
-    __syncthreads();
+  // 2. exponentials and their left-to-right sum (a NaN term makes it NaN)
+  int nan_e = 0;
+#pragma unroll 8
+  for (int i = tid; i < n; i += kSelThreads) {
+    const float e = expf_ref(lg[i] - mx);
+    lg[i] = e;
+    nan_e |= e != e;
   }
-  if (tid == 0) s_bcast[0] = 1.0f / sv;
+  if (__syncthreads_or(nan_e)) {
+    if (tid == 0) s_bcast[0] = __builtin_nanf("");
+  } else {
+    const float sv = block_seq_sum<4>([lg](int i) { return lg[i]; }, n, 0.0f, __builtin_inff(), sh.seq).s;
+    if (tid == 0) s_bcast[0] = 1.0f / sv;
+  }
   __syncthreads();
   const float inv = s_bcast[0];
   if (tid == 0) lg[n] = inv;
@@ -608,6 +758,7 @@ __global__ __launch_bounds__(kSelThreads) void sparse_cut_kernel(HeadDesc *const
   __shared__ float s_bcast[2];
   __shared__ int s_cut;
   __shared__ uint64_t s_last;
+  __shared__ SeqShared s_seq;
   const int item = blockIdx.x;
   const int tid = threadIdx.x;
   const HeadDesc *d = item_desc[item];
@@ -618,36 +769,47 @@ __global__ __launch_bounds__(kSelThreads) void sparse_cut_kernel(HeadDesc *const
   const float inv = lg[n];
   const uint64_t *kk = keys + (size_t)item * S;
   const uint32_t *tt = toks + (size_t)item * S;
-  auto skey = [&](int i) -> uint64_t { return ((uint64_t)(uint32_t)kk[i] << 32) | tt[i]; };
+  auto skey = [kk, tt](int i) -> uint64_t { return ((uint64_t)(uint32_t)kk[i] << 32) | tt[i]; };
 
-  // 4. the cut: whole quads while mass < v_mass, then single tokens
+  // 4. the cut: whole quads while mass < v_mass, then single tokens; NaN
+  // probabilities (sorted last) keep the one-lane chain
   const int n_quads = n / 4;  // quads with ii + 3 < n
-  float mass = 0.0f;
-  int ii = 0;
-  bool open = true;  // thread 0: the quad loop has not stopped
-  for (int base = 0; base < n_quads; base += kStage) {
-    const int m = n_quads - base < kStage ? n_quads - base : kStage;
-    for (int k = tid; k < m; k += blockDim.x) {
-      const int q = 4 * (base + k);
-      s_stage[k] = __fadd_rn(__fadd_rn(__fadd_rn(key_p(skey(q)), key_p(skey(q + 1))), key_p(skey(q + 2))),
-                             key_p(skey(q + 3)));
+  auto quad = [skey](int k) {
+    const int q = 4 * k;
+    return __fadd_rn(__fadd_rn(__fadd_rn(key_p(skey(q)), key_p(skey(q + 1))), key_p(skey(q + 2))),
+                     key_p(skey(q + 3)));
+  };
+  if ((uint32_t)kk[n - 1] == 0xFFFFFFFFu) {
+    float mass = 0.0f;
+    int ii = 0;
+    bool open = true;  // thread 0: the quad loop has not stopped
+    for (int base = 0; base < n_quads; base += kStage) {
+      const int m = n_quads - base < kStage ? n_quads - base : kStage;
+      for (int k = tid; k < m; k += blockDim.x) s_stage[k] = quad(base + k);
+      __syncthreads();
+      if (tid == 0 && open) {
+        const int k = mass_scan(s_stage, m, v_mass, &mass);
+        ii = 4 * (base + k);
+        open = k == m;
+        s_bcast[1] = open ? 1.0f : 0.0f;
+      }
+      __syncthreads();
+      if (s_bcast[1] == 0.0f) break;
+      __syncthreads();
     }
-    __syncthreads();
-    if (tid == 0 && open) {
-      const int k = mass_scan(s_stage, m, v_mass, &mass);
-      ii = 4 * (base + k);
-      open = k == m;
-      s_bcast[1] = open ? 1.0f : 0.0f;
+    if (tid == 0) {
+      for (; ii < n && mass < v_mass; ++ii) mass = __fadd_rn(mass, key_p(skey(ii)));
+      s_cut = ii;
     }
-    __syncthreads();
-    if (s_bcast[1] == 0.0f) break;
-    __syncthreads();
+  } else {
+    const SeqResult rq = block_seq_sum<4>(quad, n_quads, 0.0f, v_mass, s_seq);
+    const int i1 = 4 * rq.count;
+    const SeqResult rs = block_seq_sum<4>([skey, i1](int i) { return key_p(skey(i1 + i)); }, n - i1,
+                                          rq.s, v_mass, s_seq);
+    if (tid == 0) s_cut = i1 + rs.count;
   }
-  if (tid == 0) {
-    for (; ii < n && mass < v_mass; ++ii) mass = __fadd_rn(mass, key_p(skey(ii)));
-    s_cut = ii;
-    s_last = ii > 0 ? skey(ii - 1) : 0;
-  }
+  __syncthreads();
+  if (tid == 0) s_last = s_cut > 0 ? skey(s_cut - 1) : 0;
   __syncthreads();
   const int cut = s_cut;
   const uint64_t last = s_last;
@@ -734,31 +896,30 @@ __global__ __launch_bounds__(kSelThreads) void sparse_fused_kernel(
   float *lg = ws + (size_t)item * ws_stride;
   const int s0 = (int)(((long long)d->st.head - n + cap) % cap);
   const int E = n <= kSelThreads ? 1 : n <= 2 * kSelThreads ? 2 : 4;
+  float lreg[4];  // the thread's logits when computed here
   if constexpr (!LOGITS_IN) {
-    // logits of the tokens select_small gives this thread (E per thread);
-    // each thread reads back only its own
+    // logits of the tokens select_small gives this thread (E per thread),
+    // handed over in registers
     rotate_query_exact(s_q, queries + (size_t)item * dim, dim, PT, d->signs, inv_sqrt_p, sqrt_p);
     const float attn_s = 1.0f / (sqrtf((float)dim) * (float)PT);
     for (int e = 0; e < E; ++e) {
       const int t = tid * E + e;
       if (t < n) {
         const int slot = ring_slot(s0, t, cap);
+        const float ks = d->k_scale[slot];  // issued with the row, not after the dot
         const uint8_t *row = d->k_codes + (size_t)slot * d->k_pb;
         const float dot = kdot_row<PT, KB>(row, slot & kperm_mask(PT, KB), s_q, PT, s_cbk);
-        lg[t] = __fmul_rn(__fmul_rn(dot, attn_s), d->k_scale[slot]);
+        lreg[e] = __fmul_rn(__fmul_rn(dot, attn_s), ks);
       }
     }
   }
-  if (E == 1) select_small<1>(d, v_mass, lg, n, s0, sh);
-  else if (E == 2) select_small<2>(d, v_mass, lg, n, s0, sh);
-  else select_small<4>(d, v_mass, lg, n, s0, sh);
-  __syncthreads();
-  // the weights (each thread's own, in lg) into LDS over the sort keys
+  // the weights go to LDS over the sort keys (select_small reads no key
+  // after its cut)
   float *w_lds = reinterpret_cast<float *>(sh.key);
-  for (int e = 0; e < E; ++e) {
-    const int t = tid * E + e;
-    if (t < n) w_lds[t] = lg[t];
-  }
+  const float *lin = LOGITS_IN ? nullptr : lreg;
+  if (E == 1) select_small<1>(d, v_mass, lg, n, s0, sh, lin, w_lds);
+  else if (E == 2) select_small<2>(d, v_mass, lg, n, s0, sh, lin, w_lds);
+  else select_small<4>(d, v_mass, lg, n, s0, sh, lin, w_lds);
   __syncthreads();
 
   // weighted V rows: lane (sub, u) takes unit u of token wave * TPI + sub,
