@@ -417,6 +417,163 @@ __global__ __launch_bounds__(128) void append_kv_kernel(HeadDesc *const *descs, 
   encode_row<P, VB, false>(d, st, c, 0, 1, vals, 1, dim, inv_sqrt_p, sqrt_p, s_q4);
 }
 
+// One token for few heads: a wave per vector (wave 0 the key, wave 1 the
+// value of head blockIdx.x), lane l holding entries l and l + 64.  The same
+// float steps as encode_vec in the same order: the sums of squares left to
+// right (every lane runs the chain over the squares in LDS), the butterflies
+// of span 1, 2, ... between lanes (shfl_xor) and, at padded 128, inside the
+// lane; codes are gathered in LDS and lane k packs word k of the row.  A lane
+// per vector (append_kv_kernel) leaves one wave with the whole codec's
+// dependency chain when there are few heads (about 10 us for 4 heads).
+template <int P, int KB, int VB>
+__global__ __launch_bounds__(128) void append_one_kernel(HeadDesc *const *descs,
+                                                         const float *__restrict__ keys,
+                                                         const float *__restrict__ vals, int dim,
+                                                         float inv_sqrt_p, float sqrt_p) {
+  constexpr int E = P / 64;
+  __shared__ Q4Entry s_q4[(KB == 4 || VB == 4) ? kQ4Entries : 1];
+  __shared__ __align__(16) float s_sq[2][P];
+  __shared__ uint8_t s_code[2][P];
+  const int c = blockIdx.x;
+  const int lane = threadIdx.x & 63, side = threadIdx.x >> 6;
+  if constexpr (KB == 4 || VB == 4) {
+    for (int i = threadIdx.x; i < kQ4Entries; i += blockDim.x) s_q4[i] = q4s_entry(i);
+  }
+  HeadDesc *d = descs[c];
+  const RingState st = d->st;
+  __syncthreads();  // both waves have the old state and the table
+  const int cap = d->cap;
+  if (threadIdx.x == 0) d->st = ring_after(st, 1, cap, d->hyb);
+  const float *x = (side == 0 ? keys : vals) + (size_t)c * dim;
+  if (0 < mirror_count(st, 1, cap, d->hyb)) {
+    float *m = (side == 0 ? d->raw_k : d->raw_v) + (size_t)st.raw_count * dim;
+    for (int i = lane; i < dim; i += 64) m[i] = x[i];
+  }
+  if (cap <= 0) return;
+  const int slot = (int)((long long)st.head % cap);
+  float v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) v[e] = lane + 64 * e < dim ? x[lane + 64 * e] : 0.0f;
+  const int B = side == 0 ? KB : VB;
+  uint8_t *codes = side == 0 ? d->k_codes : d->v_codes;
+  float *scales = side == 0 ? d->k_scale : d->v_scale;
+  auto seq_sumsq = [&](const float (&u)[E]) {
+    // left to right over the P squares (every lane runs the same chain)
+#pragma unroll
+    for (int e = 0; e < E; ++e) s_sq[side][lane + 64 * e] = __fmul_rn(u[e], u[e]);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float4 *q4 = reinterpret_cast<const float4 *>(s_sq[side]);
+    float acc = 0.0f;
+#pragma unroll
+    for (int b = 0; b < P / 16; ++b) {
+      float4 r[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) r[k] = q4[4 * b + k];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        acc = __fadd_rn(acc, r[k].x);
+        acc = __fadd_rn(acc, r[k].y);
+        acc = __fadd_rn(acc, r[k].z);
+        acc = __fadd_rn(acc, r[k].w);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();  // s_sq is read by every lane before it is rewritten
+    return acc;
+  };
+  if (B == 16) {
+    float *row = reinterpret_cast<float *>(codes + (size_t)slot * 4 * P);
+#pragma unroll
+    for (int e = 0; e < E; ++e) row[lane + 64 * e] = v[e];
+    if (lane == 0) scales[slot] = 1.0f;
+    return;
+  }
+  const float s = seq_sumsq(v);
+  const float norm = sqrtf(__fadd_rn(s, 1e-12f));
+  const float inv = 1.0f / norm;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = lane + 64 * e;
+    const uint32_t flip = (~d->signs[i >> 5] >> (i & 31)) << 31;
+    v[e] = __uint_as_float(__float_as_uint(__fmul_rn(v[e], inv)) ^ flip);
+  }
+#pragma unroll
+  for (int len = 1; len < 64 && len < P; len <<= 1) {
+    const bool upper = (lane & len) != 0;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const float o = __shfl_xor(v[e], len, 64);
+      v[e] = upper ? __fsub_rn(o, v[e]) : __fadd_rn(v[e], o);
+    }
+  }
+  if constexpr (E == 2) {
+    const float lo = v[0], hi = v[1];
+    v[0] = __fadd_rn(lo, hi);
+    v[1] = __fsub_rn(lo, hi);
+  }
+#pragma unroll
+  for (int e = 0; e < E; ++e) v[e] = __fmul_rn(__fmul_rn(v[e], inv_sqrt_p), sqrt_p);
+  // the clamp (see encode_vec): inert when s >= 1e-10
+  bool nan_row;
+  if (s >= 1e-10f) {
+    nan_row = __shfl(v[0], 0, 64) != __shfl(v[0], 0, 64);
+  } else {
+    const float s2 = seq_sumsq(v);
+    const float sigma = sqrtf(__fadd_rn(s2 / (float)P, 1e-12f));
+    const float clip = __fmul_rn(3.0f, sigma);
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] = __builtin_amdgcn_fmed3f(v[e], -clip, clip);
+    nan_row = s2 != s2;
+  }
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const uint32_t q = B == 4 ? quantize_ss4(v[e], s_q4) : B == 3 ? quantize_ss3(v[e]) : quantize_ss2(v[e]);
+    s_code[side][lane + 64 * e] = (uint8_t)q;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int nw = P * B / 32;  // words of the row
+  if (lane < nw) {
+    const uint8_t *cd = s_code[side];
+    uint32_t w = 0u;
+    if (nan_row) {
+      w = B == 2 ? nan_word<2>(lane) : B == 4 ? nan_word<4>(lane) : nan_word<3>(lane);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int b = 4 * lane + j;  // byte b of the row, MSB-first codes
+        uint32_t byte;
+        if (B == 4) {
+          byte = ((uint32_t)cd[2 * b] << 4) | cd[2 * b + 1];
+        } else if (B == 2) {
+          byte = ((uint32_t)cd[4 * b] << 6) | ((uint32_t)cd[4 * b + 1] << 4) |
+                 ((uint32_t)cd[4 * b + 2] << 2) | cd[4 * b + 3];
+        } else {
+          const int g = b / 3;  // 24-bit big-endian group of 8 codes
+          uint32_t grp = 0u;
+#pragma unroll
+          for (int k = 0; k < 8; ++k) grp |= (uint32_t)cd[8 * g + k] << (21 - 3 * k);
+          byte = (grp >> (16 - 8 * (b % 3))) & 255u;
+        }
+        w |= byte << (8 * j);
+      }
+    }
+    uint32_t *row = reinterpret_cast<uint32_t *>(codes + (size_t)slot * (P * B / 8));
+    const uint32_t xm = side == 0 ? (uint32_t)kperm_mask(P, B) : 0u;
+    if (xm != 0u) {
+      // the K row's XOR byte order (kperm_mask): word i, bytes permuted by x & 3, at i ^ (x >> 2)
+      const uint32_t xx = (uint32_t)slot & xm;
+      row[(uint32_t)lane ^ (xx >> 2)] = __builtin_amdgcn_perm(0u, w, 0x03020100u ^ ((xx & 3u) * 0x01010101u));
+    } else {
+      row[lane] = w;
+    }
+  }
+  if (lane == 0) scales[slot] = norm;
+}
+
 // Same codec for padded dimensions above 128: identical float steps in the
 // same order, with the vector in per-lane scratch instead of VGPRs (wide heads
 // are rare; the unrolled register kernel would cost minutes of compile time).
@@ -579,10 +736,29 @@ hipError_t launch_side(HeadDesc *const *descs, int n_ctx, int side, int bits, co
 
 }  // namespace
 
+// Heads up to which a one-token append takes a wave per vector (above, a lane
+// per vector keeps the launch to a few waves' worth of work per CU).
+constexpr int kOneWaveMaxCtx = 2048;
+
 hipError_t launch_append(HeadDesc *const *descs, int n_ctx, int dim, int padded, int k_bits,
                          int v_bits, const float *keys, const float *vals, int n_tok,
                          hipStream_t s) {
   if (n_ctx <= 0 || n_tok <= 0) return hipSuccess;
+  if (n_tok == 1 && (padded == 64 || padded == 128) && n_ctx <= kOneWaveMaxCtx) {
+    // few heads: a wave per vector, a block per head (both sides, the ring state)
+    const float sp = sqrtf((float)padded), isp = 1.0f / sp;
+#define AQ_ONE(P_, KB_, VB_)                                                                  \
+  if (padded == P_ && k_bits == KB_ && v_bits == VB_) {                                      \
+    append_one_kernel<P_, KB_, VB_><<<n_ctx, 128, 0, s>>>(descs, keys, vals, dim, isp, sp); \
+    return hipGetLastError();                                                                \
+  }
+#define AQ_ONE_V(P_, KB_) AQ_ONE(P_, KB_, 2) AQ_ONE(P_, KB_, 3) AQ_ONE(P_, KB_, 4) AQ_ONE(P_, KB_, 16)
+    AQ_ONE_V(64, 2) AQ_ONE_V(64, 3) AQ_ONE_V(64, 4) AQ_ONE_V(64, 16)
+    AQ_ONE_V(128, 2) AQ_ONE_V(128, 3) AQ_ONE_V(128, 4) AQ_ONE_V(128, 16)
+#undef AQ_ONE_V
+#undef AQ_ONE
+    return hipErrorInvalidValue;
+  }
   if (n_tok == 1 && (padded == 64 || padded == 128)) {
     // one launch for both sides and the ring states
     const float sp = sqrtf((float)padded), isp = 1.0f / sp;

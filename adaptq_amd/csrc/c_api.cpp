@@ -112,10 +112,9 @@ struct DevSync {
   uint64_t lib_ev_at = 0;  // submission count when lib_ev was recorded
   struct Caller {
     hipStream_t s;
-    hipEvent_t ev;
-    bool fresh;  // recorded, not yet waited on by the library stream
+    bool fresh;  // device-form work queued since the last wait_callers
   };
-  Caller caller[kMaxCallerStreams];  // events created with the stream
+  Caller caller[kMaxCallerStreams];  // caller streams seen
   int n_caller = 0;
   int evict = 0;
   void *scratch = nullptr;  // this device's address of the static scratch
@@ -126,29 +125,25 @@ DevSync g_dev[kMaxDevices];
 DevSync *dev_sync(int dev) { return dev >= 0 && dev < kMaxDevices ? &g_dev[dev] : nullptr; }
 
 // Per-device set-up, once, with the device current (caller holds d->mu):
-// the library stream, its event, one event per caller-stream slot and the
-// device's address of the static scratch.  Everything a later call needs is
-// made here, so the calls themselves create nothing.
+// the library stream, its event and the device's address of the static
+// scratch.  Everything a later call needs is made here, so the calls
+// themselves create nothing.
 hipError_t ensure_lib(DevSync *d) {
   if (d->lib) return hipSuccess;
   hipStream_t s = nullptr;
   // blocking (synchronises with the null stream), default priority
   hipError_t e = hipStreamCreateWithFlags(&s, hipStreamDefault);
   if (e != hipSuccess) return e;
-  hipEvent_t evs[1 + kMaxCallerStreams] = {};
-  int made = 0;
-  for (; made < 1 + kMaxCallerStreams && e == hipSuccess; ++made)
-    e = hipEventCreateWithFlags(&evs[made], hipEventDisableTiming);
+  hipEvent_t ev = nullptr;
+  e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
   void *sp = nullptr;
   if (e == hipSuccess) e = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));
   if (e != hipSuccess) {
-    for (int i = 0; i < made; ++i)
-      if (evs[i]) (void)hipEventDestroy(evs[i]);
+    if (ev) (void)hipEventDestroy(ev);
     (void)hipStreamDestroy(s);
     return e;
   }
-  d->lib_ev = evs[0];
-  for (int i = 0; i < kMaxCallerStreams; ++i) d->caller[i].ev = evs[1 + i];
+  d->lib_ev = ev;
   d->scratch = sp;
   d->lib = s;
   return hipSuccess;
@@ -162,18 +157,30 @@ hipError_t init_device(int dev) {
   return ensure_lib(d);
 }
 
-// Caller holds d->mu: the library stream waits on every fresh caller event.
+// Caller holds d->mu: the device finishes the work queued so far on every
+// caller stream that has carried device-form launches since the last such
+// wait, before any library-stream work is queued.  The host waits for the
+// device here rather than recording an event on each caller stream after
+// each launch: a record per call cost about 3 us of host time and stretched
+// the GPU timeline by as much, and a record made only now could touch a
+// stream its owner has destroyed since.  Steady device-form use never gets
+// here; a host-form call, reset, inspection or snapshot after device-form
+// launches pays one device wait.
 hipError_t wait_callers(DevSync *d) {
   bool any = false;
-  for (int i = 0; i < d->n_caller; ++i) {
-    DevSync::Caller &c = d->caller[i];
-    if (!c.fresh) continue;
-    const hipError_t e = hipStreamWaitEvent(d->lib, c.ev, 0);
-    if (e != hipSuccess) return e;
-    c.fresh = false;
-    any = true;
+  for (int i = 0; i < d->n_caller; ++i) any = any || d->caller[i].fresh;
+  if (!any) return hipSuccess;
+  const int dev = (int)(d - g_dev);
+  int cur = -1;
+  hipError_t e = hipGetDevice(&cur);
+  if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (cur >= 0 && cur != dev) {
+    const hipError_t e2 = hipSetDevice(cur);
+    if (e == hipSuccess) e = e2;
   }
-  if (any) ++d->enq;  // the wait is library-stream work the host may need to see done
+  if (e != hipSuccess) return e;
+  for (int i = 0; i < d->n_caller; ++i) d->caller[i].fresh = false;
   return hipSuccess;
 }
 
@@ -265,9 +272,9 @@ hipError_t caller_begin(int dev, hipStream_t s) {
   return lib_wait(dev, target);
 }
 
-// After a device-form launch on caller stream s: record it for the library
-// stream to wait on.  Launches captured into a graph run at replay, outside
-// this bookkeeping.
+// After a device-form launch on caller stream s: note the stream, so that
+// library-stream work waits for it (wait_callers).  Launches captured into a
+// graph run at replay, outside this bookkeeping.
 hipError_t caller_end(int dev, hipStream_t s) {
   if (is_null_stream(s)) return hipSuccess;  // later library-stream work waits for it
   DevSync *d = dev_sync(dev);
@@ -288,18 +295,14 @@ hipError_t caller_end(int dev, hipStream_t s) {
       c = &d->caller[d->evict];
       d->evict = (d->evict + 1) % kMaxCallerStreams;
       if (c->fresh) {
-        hipError_t e = ensure_lib(d);
-        if (e == hipSuccess) e = hipStreamWaitEvent(d->lib, c->ev, 0);
+        const hipError_t e = wait_callers(d);  // before the slot forgets its stream
         if (e != hipSuccess) return e;
-        ++d->enq;
       }
     }
     c->s = s;
-    c->fresh = false;
   }
-  const hipError_t e = hipEventRecord(c->ev, s);
-  if (e == hipSuccess) c->fresh = true;
-  return e;
+  c->fresh = true;
+  return hipSuccess;
 }
 
 // Any change to a context's host-visible ring state (staged rows, appends,

@@ -111,6 +111,41 @@ struct VLut {
 // stages in place); fp32 K: qr = q.  Padded entries are zero.
 template <int P>
 __device__ void load_query(float *s_q, const float *q, int dim, bool rotate, const uint32_t *signs) {
+  if constexpr (P == 64 || P == 128) {
+    // one wave: lane l holds entries l and l + 64, butterflies of span < 64
+    // between lanes, span 64 inside the lane (the same additions, no barriers)
+    constexpr int E = P / 64;
+    if (threadIdx.x < 64) {
+      const int lane = threadIdx.x;
+      float v[E];
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const int i = lane + 64 * e;
+        v[e] = i < dim ? q[i] : 0.0f;
+        if (rotate && !((signs[i >> 5] >> (i & 31)) & 1u)) v[e] = -v[e];
+      }
+      if (rotate) {
+#pragma unroll
+        for (int len = 1; len < 64; len <<= 1) {
+          const bool upper = (lane & len) != 0;
+#pragma unroll
+          for (int e = 0; e < E; ++e) {
+            const float o = __shfl_xor(v[e], len, 64);
+            v[e] = upper ? o - v[e] : v[e] + o;
+          }
+        }
+        if constexpr (E == 2) {
+          const float lo = v[0], hi = v[1];
+          v[0] = lo + hi;
+          v[1] = lo - hi;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < E; ++e) s_q[lane + 64 * e] = v[e];
+    }
+    __syncthreads();
+    return;
+  }
   for (int i = threadIdx.x; i < P; i += blockDim.x) {
     float v = i < dim ? q[i] : 0.0f;
     if (rotate && !((signs[i >> 5] >> (i & 31)) & 1u)) v = -v;
@@ -285,6 +320,38 @@ template <bool INVERSE_FWHT>
 __device__ void finish_item(float *s_acc, int P, int dim, float L, const uint32_t *signs,
                             float *out, bool guard = false, int n = 1) {
   const float invL = guard && !(L > 0.0f && isfinite(L)) ? 1.0f / (float)n : 1.0f / L;
+  if (P == 64 || P == 128) {
+    // one wave, the same operations in the same order without barriers (every
+    // caller ends here): lane l holds entries l and l + 64
+    if (threadIdx.x >= 64) return;
+    const int lane = threadIdx.x;
+    const bool two = P == 128;
+    float v0 = s_acc[lane] * invL, v1 = two ? s_acc[lane + 64] * invL : 0.0f;
+    if (INVERSE_FWHT) {
+#pragma unroll
+      for (int len = 1; len < 64; len <<= 1) {
+        const bool upper = (lane & len) != 0;
+        const float o0 = __shfl_xor(v0, len, 64), o1 = __shfl_xor(v1, len, 64);
+        v0 = upper ? o0 - v0 : v0 + o0;
+        v1 = upper ? o1 - v1 : v1 + o1;
+      }
+      if (two) {
+        const float lo = v0, hi = v1;
+        v0 = lo + hi;
+        v1 = lo - hi;
+      }
+      const float scale = 1.0f / sqrtf((float)P);
+      v0 = v0 * scale;
+      v1 = v1 * scale;
+      if (lane < dim) out[lane] = ((signs[lane >> 5] >> (lane & 31)) & 1u) ? v0 : -v0;
+      if (two && lane + 64 < dim)
+        out[lane + 64] = ((signs[(lane + 64) >> 5] >> (lane & 31)) & 1u) ? v1 : -v1;
+    } else {
+      if (lane < dim) out[lane] = v0;
+      if (two && lane + 64 < dim) out[lane + 64] = v1;
+    }
+    return;
+  }
   for (int i = threadIdx.x; i < P; i += blockDim.x) s_acc[i] *= invL;
   __syncthreads();
   if (INVERSE_FWHT) {

@@ -421,9 +421,13 @@ def secondary(L, last_error, torch, np, stream, reps=20, which=("C1", "C2", "C3"
             for l, m in enumerate(ms):
                 ok(L.adaptq_mha_append_all_device(m, dp(kvd[0, l]), dp(kvd[1, l]), n, 0, sp))
 
+            # pointers made before timing: the span measures the library's
+            # calls, not Python's tensor indexing (a few us per view)
+            qp, op = [dp(qd[l]) for l in range(nl)], [dp(od[l]) for l in range(nl)]
+
             def step():
                 for l, m in enumerate(ms):
-                    ok(L.adaptq_mha_compute_all_device(m, dp(qd[l]), dp(od[l]), sp))
+                    ok(L.adaptq_mha_compute_all_device(m, qp[l], op[l], sp))
             us = span(step)
             nbytes = packed_bytes if hyb == 0 else nl * nh * n * 2 * 64 * 4
             c2[name] = rate(us, nbytes)
@@ -434,9 +438,11 @@ def secondary(L, last_error, torch, np, stream, reps=20, which=("C1", "C2", "C3"
             if not all(plans):
                 raise RuntimeError(last_error())
 
+            q0, o0, q1, o1 = dp(qd[0]), dp(od[0]), dp(qd[1:]), dp(od[1:])
+
             def step_plans():
-                ok(L.adaptq_plan_compute_device(plans[0], dp(qd[0]), dp(od[0]), sp))
-                ok(L.adaptq_plan_compute_device(plans[1], dp(qd[1:]), dp(od[1:]), sp))
+                ok(L.adaptq_plan_compute_device(plans[0], q0, o0, sp))
+                ok(L.adaptq_plan_compute_device(plans[1], q1, o1, sp))
             c2[name + "_two_plans"] = rate(span(step_plans), nbytes)
             for p in plans:
                 L.adaptq_plan_destroy(p)
@@ -468,13 +474,18 @@ def secondary(L, last_error, torch, np, stream, reps=20, which=("C1", "C2", "C3"
             b.record(stream)
             torch.cuda.synchronize()
             append_us = a.elapsed_time(b) * 1e3
+            # pointers made before timing (tensor views cost a few us each)
+            pp = [[(dp(per[0, s, l]), dp(per[1, s, l]), dp(per[2, s, l])) for l in range(nl)]
+                  for s in range(steps)]
+            op = [dp(od[l]) for l in range(nl)]
             a.record(stream)
             t0 = time.perf_counter()
             for s in range(steps):
+                ps = pp[s]
                 for l, m in enumerate(ms):
-                    ok(L.adaptq_mha_append_all_device(m, dp(per[0, s, l]), dp(per[1, s, l]), 1,
-                                                      n0 + s, sp))
-                    ok(L.adaptq_mha_compute_all_device(m, dp(per[2, s, l]), dp(od[l]), sp))
+                    kp, vp, qp = ps[l]
+                    ok(L.adaptq_mha_append_all_device(m, kp, vp, 1, n0 + s, sp))
+                    ok(L.adaptq_mha_compute_all_device(m, qp, op[l], sp))
             b.record(stream)
             torch.cuda.synchronize()
             wall = (time.perf_counter() - t0) * 1e6
@@ -492,14 +503,15 @@ def secondary(L, last_error, torch, np, stream, reps=20, which=("C1", "C2", "C3"
                      L.adaptq_plan_create((C.c_void_p * (len(ctx) - nh))(*ctx[nh:]), len(ctx) - nh)]
             if not all(plans):
                 raise RuntimeError(last_error())
+            pq = [[(pl, dp(per[0, s, lo:hi]), dp(per[1, s, lo:hi]), dp(per[2, s, lo:hi]), dp(od[lo:hi]))
+                   for pl, lo, hi in ((plans[0], 0, 1), (plans[1], 1, nl))] for s in range(steps)]
             torch.cuda.synchronize()
             a.record(stream)
             t0 = time.perf_counter()
             for s in range(steps):
-                for pl, lo, hi in ((plans[0], 0, 1), (plans[1], 1, nl)):
-                    ok(L.adaptq_plan_append_device(pl, dp(per[0, s, lo:hi]), dp(per[1, s, lo:hi]), 1,
-                                                   n0 + s, sp))
-                    ok(L.adaptq_plan_compute_device(pl, dp(per[2, s, lo:hi]), dp(od[lo:hi]), sp))
+                for pl, kp, vp, qp, opl in pq[s]:
+                    ok(L.adaptq_plan_append_device(pl, kp, vp, 1, n0 + s, sp))
+                    ok(L.adaptq_plan_compute_device(pl, qp, opl, sp))
             b.record(stream)
             torch.cuda.synchronize()
             wall = (time.perf_counter() - t0) * 1e6
