@@ -82,18 +82,17 @@ bool valid_bits(int b) { return b == 16 || (b >= 2 && b <= 4); }
 //
 // Work on a context's ring is queued on two kinds of streams: the library's
 // own stream per device (host-form calls: flushes of staged rows, host
-// compute, reset) and callers' streams (the *_device entry points).  They are
-// ordered on the device, without the host waiting.  The library stream is a
-// blocking stream, so the HIP null stream (NULL, torch's default stream) and
-// it wait for each other's earlier work by themselves; for any other caller
-// stream:
-//   * after a device-form launch, an event is recorded on the caller's stream
-//     (one event per caller stream and device);
-//   * before library-stream work, the library stream waits on every caller
-//     event recorded since its previous such wait;
+// compute, reset) and callers' streams (the *_device entry points).  The
+// library stream is a blocking stream, so the HIP null stream (NULL, torch's
+// default stream) and it wait for each other's earlier work by themselves;
+// for any other caller stream:
+//   * after a device-form launch, the caller's stream is marked as carrying
+//     device-form work (a table of up to 16 streams per device);
+//   * before library-stream work, if any marked stream exists, the host waits
+//     for the device once (wait_callers) and clears the marks;
 //   * before a device-form launch, the caller's stream waits on an event
 //     recorded after the library stream's latest work, unless the host has
-//     already seen that work complete.
+//     already seen that work complete (no host wait).
 // Library-stream submissions are numbered per device; `done` is the highest
 // number the host has seen complete, so host waits (outputs of host-form
 // calls, reuse of pinned staging memory, inspection) happen only when the
@@ -287,11 +286,11 @@ hipError_t caller_end(int dev, hipStream_t s) {
   if (!c) {
     if (!d->lib) return hipErrorNotInitialized;  // a context's creation sets the device up
     if (d->n_caller < kMaxCallerStreams) {
-      c = &d->caller[d->n_caller];  // its event was made at set-up
+      c = &d->caller[d->n_caller];
       ++d->n_caller;
     } else {
-      // reuse the slot of another stream once the library stream has
-      // waited on what it recorded
+      // reuse the slot of another stream once the device has finished the
+      // work that stream carried
       c = &d->caller[d->evict];
       d->evict = (d->evict + 1) % kMaxCallerStreams;
       if (c->fresh) {

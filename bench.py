@@ -322,11 +322,13 @@ def secondary(L, last_error, torch, np, stream, reps=20, which=("C1", "C2", "C3"
     `reps` HIP-event spans on `stream`, in µs, with the algorithmic bytes each
     span reads.  Every stack is created fresh, filled through the device
     append, then timed; data are seeded and generated as each config states.
-      C1: 4 heads d64 K4/V2, 2048 tokens: one whole-MHA decode, dense
-          (v_mass 0, hybrid 0) and Engine defaults (v_mass 0.95, hybrid 512:
-          the sparse-V branch at n = 2048).
+      C1: 4 heads d64 K4/V2, 2048 tokens: the whole-MHA append of the 2048
+          tokens (one span) and one whole-MHA decode, dense (v_mass 0,
+          hybrid 0) and Engine defaults (v_mass 0.95, hybrid 512: the
+          sparse-V branch at n = 2048).
       C2: 24 layers x 14 heads d64, n = 512 (layer 0 K16/V2, others K4/V2,
-          channels 3 and 17 x20): one decode step over all layers, packed
+          channels 3 and 17 x20): the appends of every layer (one span), one
+          decode step over all layers, packed
           (hybrid 0) and hybrid FP32 (Engine defaults: every layer takes the
           raw-mirror branch), each with one call per layer and through two
           plans (layer 0, layers 1-23).
@@ -366,6 +368,17 @@ def secondary(L, last_error, torch, np, stream, reps=20, which=("C1", "C2", "C3"
     def rate(us, nbytes):
         return {"us": us, "bytes": nbytes, "gb_per_s": nbytes / us / 1e3}
 
+    def once(fn):
+        """One HIP-event span of fn on `stream` (appends change the state, so
+        they are timed once), in us."""
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3
+
     def stack(specs):
         ms = [L.adaptq_mha_create(*s) for s in specs]
         if not all(ms):
@@ -397,9 +410,10 @@ def secondary(L, last_error, torch, np, stream, reps=20, which=("C1", "C2", "C3"
         c1 = {}
         for name, vm, hyb in (("dense", 0.0, 0), ("engine_defaults_sparse_v", 0.95, 512)):
             ms = stack([(4, 64, 4, 2, 2048, 42, vm, hyb)])
-            ok(L.adaptq_mha_append_all_device(ms[0], dp(kd), dp(vd), 2048, 0, sp))
+            app_us = once(lambda: ok(L.adaptq_mha_append_all_device(ms[0], dp(kd), dp(vd), 2048, 0, sp)))
             us = span(lambda: ok(L.adaptq_mha_compute_all_device(ms[0], dp(qd), dp(od), sp)))
             c1[name] = rate(us, 4 * 2048 * decode_bytes_per_token(64, 4, 2))
+            c1[name + "_append_2048"] = rate(app_us, 4 * 2048 * append_bytes_per_token(64, 64, 4, 2))
             free(ms)
         res["C1"] = c1
 
@@ -418,8 +432,14 @@ def secondary(L, last_error, torch, np, stream, reps=20, which=("C1", "C2", "C3"
         c2 = {}
         for name, vm, hyb in (("packed", 0.0, 0), ("hybrid_fp32", 0.95, 512)):
             ms = stack([(nh, 64, 16 if l == 0 else 4, 2, n, 42 ^ l, vm, hyb) for l in range(nl)])
-            for l, m in enumerate(ms):
-                ok(L.adaptq_mha_append_all_device(m, dp(kvd[0, l]), dp(kvd[1, l]), n, 0, sp))
+            kp, vp = [dp(kvd[0, l]) for l in range(nl)], [dp(kvd[1, l]) for l in range(nl)]
+
+            def append_all():
+                for l, m in enumerate(ms):
+                    ok(L.adaptq_mha_append_all_device(m, kp[l], vp[l], n, 0, sp))
+            c2[name + "_append_512"] = rate(
+                once(append_all), nh * n * (append_bytes_per_token(64, 64, 16, 2)
+                                            + (nl - 1) * append_bytes_per_token(64, 64, 4, 2)))
 
             # pointers made before timing: the span measures the library's
             # calls, not Python's tensor indexing (a few us per view)

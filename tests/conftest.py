@@ -18,6 +18,33 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a HIP GPU (MI355X); run with -m gpu")
 
 
+def pytest_terminal_summary(terminalreporter):
+    """Worst output errors per test module (every gpu_head.rel_err call), and
+    the per-test ledger as JSON at $AQ_PARITY_LOG when that is set."""
+    mod = sys.modules.get("gpu_head")
+    ledger = getattr(mod, "ERROR_LEDGER", None) if mod else None
+    if not ledger:
+        return
+    path = os.environ.get("AQ_PARITY_LOG")
+    if path:
+        import json
+        with open(path, "w") as f:
+            json.dump(ledger, f, indent=1, sort_keys=True)
+    per_file = {}
+    for node, e in ledger.items():
+        f = per_file.setdefault(node.split("::")[0], {"calls": 0, "norm_max": 0.0,
+                                                       "elem_rel_max": 0.0})
+        f["calls"] += e["calls"]
+        f["norm_max"] = max(f["norm_max"], e["norm_max"])
+        f["elem_rel_max"] = max(f["elem_rel_max"], e["elem_rel_max"])
+    tr = terminalreporter
+    tr.write_sep("-", "worst output errors (norm-wise max|y-r|/max|r|; elementwise over |r| >= 1e-3 max|r|)")
+    for name in sorted(per_file):
+        f = per_file[name]
+        tr.write_line(f"{name}: {f['calls']} comparisons, norm-wise {f['norm_max']:.2e}, "
+                      f"elementwise {f['elem_rel_max']:.2e}")
+
+
 @pytest.fixture(scope="session")
 def oracle():
     from bind import Oracle

@@ -3,6 +3,7 @@ with the same surface as oracle/bind.py's OracleHead, plus comparison utils."""
 from __future__ import annotations
 
 import ctypes as C
+import os
 
 import numpy as np
 
@@ -76,11 +77,41 @@ class GpuHead:
         return kc, vc, ks, vs
 
 
+# Worst errors seen per test (nodeid without parameters): every rel_err call
+# records its norm-wise error and elementwise statistics; conftest prints the
+# ledger at the end of the session and writes it to $AQ_PARITY_LOG if set.
+ERROR_LEDGER: dict = {}
+
+
+def _record(y, r, ne):
+    node = os.environ.get("PYTEST_CURRENT_TEST", "").split(" ")[0]
+    if not node or y.size == 0:
+        return
+    key = node.split("[")[0]
+    d = np.abs(y - r)
+    scale = float(np.max(np.abs(r)))
+    # elementwise relative error over the elements that carry the output
+    # (|r| >= 1e-3 max|r|); near-zero elements make it meaningless
+    big = np.abs(r) >= 1e-3 * scale if scale > 0 else np.zeros(r.shape, bool)
+    er = d[big] / np.abs(r[big]) if big.any() else np.zeros(1)
+    e = ERROR_LEDGER.setdefault(key, {"calls": 0, "elements": 0, "norm_max": 0.0,
+                                      "abs_max": 0.0, "elem_rel_max": 0.0,
+                                      "elem_rel_median_max": 0.0})
+    e["calls"] += 1
+    e["elements"] += int(y.size)
+    e["norm_max"] = max(e["norm_max"], ne)
+    e["abs_max"] = max(e["abs_max"], float(np.max(d)))
+    e["elem_rel_max"] = max(e["elem_rel_max"], float(np.max(er)))
+    e["elem_rel_median_max"] = max(e["elem_rel_median_max"], float(np.median(er)))
+
+
 def rel_err(y, r):
     """Norm-wise relative error max|y - r| / max(max|r|, 1e-30)."""
     y = np.asarray(y, np.float64)
     r = np.asarray(r, np.float64)
-    return float(np.max(np.abs(y - r)) / max(float(np.max(np.abs(r))), 1e-30))
+    ne = float(np.max(np.abs(y - r)) / max(float(np.max(np.abs(r))), 1e-30))
+    _record(y, r, ne)
+    return ne
 
 
 def same_bits(a, b):
