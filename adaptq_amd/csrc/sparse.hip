@@ -732,7 +732,7 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
   if (__syncthreads_or(nan_e)) {
     if (tid == 0) s_bcast[0] = __builtin_nanf("");
   } else {
-    const float sv = block_seq_sum<4>([lg](int i) { return lg[i]; }, n, 0.0f, __builtin_inff(), sh.seq).s;
+    const float sv = block_seq_sum<8>([lg](int i) { return lg[i]; }, n, 0.0f, __builtin_inff(), sh.seq).s;
     if (tid == 0) s_bcast[0] = 1.0f / sv;
   }
   __syncthreads();
@@ -802,9 +802,9 @@ __global__ __launch_bounds__(kSelThreads) void sparse_cut_kernel(HeadDesc *const
       s_cut = ii;
     }
   } else {
-    const SeqResult rq = block_seq_sum<4>(quad, n_quads, 0.0f, v_mass, s_seq);
+    const SeqResult rq = block_seq_sum<8>(quad, n_quads, 0.0f, v_mass, s_seq);
     const int i1 = 4 * rq.count;
-    const SeqResult rs = block_seq_sum<4>([skey, i1](int i) { return key_p(skey(i1 + i)); }, n - i1,
+    const SeqResult rs = block_seq_sum<8>([skey, i1](int i) { return key_p(skey(i1 + i)); }, n - i1,
                                           rq.s, v_mass, s_seq);
     if (tid == 0) s_cut = i1 + rs.count;
   }

@@ -1,0 +1,256 @@
+// The segment algorithm of block_seq_sum (adaptq_amd/csrc/seqsum.hpp) run on
+// the host, one chunk at a time exactly as the block runs it (fp64 prefix,
+// per-thread, one-edge and per-term classes and integer increments from
+// seqsum_terms.hpp, segment heads, the walk with its runs of hardware terms,
+// checks, serial redo and serial tail beyond the segment table, the stop search inside a clean
+// segment), against the plain left-to-right fp32 chain with its stop test.
+// Sequences: softmax-like exponentials, sorted probabilities and their quad
+// sums with mass stops (also stops equal to a value the chain reaches),
+// tie-heavy terms (exact small integers and dyadic fractions over large
+// sums), subnormals, wide exponent ranges, zeros and -0, and non-zero start
+// values; 1 to 8 terms per thread (chunks of 1,024 to 8,192 terms).  Prints the mismatch count and the share of chunks redone;
+// exits 0 when nothing mismatches.
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <random>
+#include <vector>
+
+#include "../../adaptq_amd/csrc/seqsum_terms.hpp"
+
+using namespace aq::seqsum_detail;
+
+static uint32_t fbits(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  return u;
+}
+static float bfloat(uint32_t u) {
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+
+struct Res {
+  int count;
+  float s;
+};
+
+// The one-lane chain: add while s < stop.
+static Res chain(const std::vector<float> &x, float s, float stop) {
+  int i = 0;
+  const int n = (int)x.size();
+  for (; i < n && s < stop; ++i) s = s + x[i];
+  return {i, s};
+}
+
+static long long g_chunks = 0, g_redo = 0, g_tail = 0;
+
+// The block algorithm, serially: chunks of kBlock threads x T terms (C =
+// kBlock T), each thread's run classified as one (range_class) or term by
+// term, runs of hardware terms as one segment.
+static Res model(const std::vector<float> &x, float s, float stop, int T) {
+  const int n = (int)x.size(), C = kBlock * T;
+  if (n <= kSerialMax) return chain(x, s, stop);
+  for (int c0 = 0;; c0 += C) {
+    if (!(s < stop) || c0 >= n) return {c0 < n ? c0 : n, s};
+    const int cn = n - c0 < C ? n - c0 : C;
+    ++g_chunks;
+    std::vector<int> cls(cn);
+    std::vector<uint32_t> r(cn);
+    double P = (double)s;  // the prefix before each thread's run (the block's
+                           // scan associates differently; the bounds cover it)
+    for (int j0 = 0; j0 < cn; j0 += T) {
+      const int nv = cn - j0 < T ? cn - j0 : T;
+      double loc = 0.0;
+      for (int k = 0; k < nv; ++k) loc += (double)x[c0 + j0 + k];
+      const int u = range_class(P, loc, j0 + nv);
+      const int E = u == kUnc ? edge_of(P, loc, j0 + nv) : kUnc;
+      const double del = range_del(P, loc, j0 + nv);
+      double Pj = P;
+      for (int k = 0; k < nv; ++k) {
+        const float xj = x[c0 + j0 + k];
+        int c;
+        uint32_t rj = 0u;
+        if (u != kUnc) {
+          c = scaled_incr(xj, u, rj) ? u : kUnc;
+        } else if (E != kUnc) {
+          c = split_class(Pj, (double)xj, del, E);
+          if (c != kUnc && !scaled_incr(xj, c, rj)) c = kUnc;
+        } else {
+          c = term_class(Pj, xj, j0 + k);
+          if (c != kUnc && !term_incr(xj, c, rj)) c = kUnc;
+        }
+        cls[j0 + k] = c;
+        r[j0 + k] = c == kUnc ? 0u : rj;
+        Pj += (double)xj;
+      }
+      P += loc;
+    }
+    // segments: a head wherever the class changes
+    std::vector<int> seg_start, seg_cls;
+    std::vector<uint64_t> seg_r;
+    uint64_t R = 0;
+    int pc = kNoClass;
+    for (int j = 0; j < cn; ++j) {
+      if (cls[j] != pc) {
+        seg_start.push_back(c0 + j);
+        seg_cls.push_back(cls[j]);
+        seg_r.push_back(R);
+      }
+      pc = cls[j];
+      R += r[j];
+    }
+    const int ns_all = (int)seg_start.size(), ns = ns_all < kMaxSeg ? ns_all : kMaxSeg;
+    seg_start.push_back(c0 + cn);
+    seg_r.push_back(R);
+    auto hw_run = [&](int from, int to, float &w) {
+      for (int i = from; i < to; ++i) {
+        if (!(w < stop)) return i;
+        w = w + x[i];
+      }
+      return -1;
+    };
+    // walk: the first kMaxSeg segments, then the rest of the chunk term by term
+    float w = s;
+    int stop_at = -1, stop_seg = -1, redo = 0;
+    for (int k = 0; k < ns && !redo; ++k) {
+      const int cl = seg_cls[k];
+      if (cl == kUnc) {
+        stop_at = hw_run(seg_start[k], seg_start[k + 1], w);
+        if (stop_at >= 0) break;
+        continue;
+      }
+      if (!(w < stop)) {
+        stop_at = seg_start[k];
+        break;
+      }
+      const uint64_t inc64 = seg_r[k + 1] - seg_r[k];
+      const uint32_t inc = inc64 >= kTop ? kTop : (uint32_t)inc64;
+      const uint32_t wb = fbits(w), exb = (uint32_t)(cl + 150), nb = wb + inc;
+      if ((wb >> 23) != exb || inc >= kTop || (nb >> 23) != exb) {
+        redo = 1;
+        break;
+      }
+      if (!(bfloat(nb) < stop)) {
+        stop_seg = k;
+        break;
+      }
+      w = bfloat(nb);
+    }
+    if (redo) {
+      ++g_redo;
+      w = s;
+      stop_seg = -1;
+      stop_at = hw_run(c0, c0 + cn, w);
+    } else if (ns_all > kMaxSeg && stop_at < 0 && stop_seg < 0) {
+      ++g_tail;
+      stop_at = hw_run(seg_start[kMaxSeg], c0 + cn, w);
+    }
+    if (stop_seg >= 0) {
+      const int lo = seg_start[stop_seg], hi = seg_start[stop_seg + 1];
+      const int eu = seg_cls[stop_seg];
+      const uint64_t r_lo = seg_r[stop_seg];
+      const uint32_t K0 = (fbits(w) & 0x7FFFFFu) | 0x800000u, kst = kstop_of(stop, eu);
+      int at = hi;
+      uint64_t Rb = r_lo;
+      for (int i = lo; i < hi; ++i) {
+        if (i > lo && (uint64_t)K0 + (Rb - r_lo) >= (uint64_t)kst) {
+          at = i;
+          break;
+        }
+        Rb += r[i - c0];
+      }
+      if (at == hi) Rb = seg_r[stop_seg + 1];
+      w = std::ldexp((float)(K0 + (uint32_t)(Rb - r_lo)), eu);
+      stop_at = at;
+    }
+    s = w;
+    if (stop_at >= 0) return {stop_at, s};
+  }
+}
+
+static long long g_cases = 0, g_bad = 0;
+
+static void check(const std::vector<float> &x, float s0, float stop, const char *what) {
+  const Res a = chain(x, s0, stop);
+  for (int T : {8, 4, 2, 1}) {
+    const Res b = model(x, s0, stop, T);
+    ++g_cases;
+    if (a.count != b.count || fbits(a.s) != fbits(b.s)) {
+      if (g_bad < 10)
+        std::printf("MISMATCH %s n=%zu T=%d stop=%a: chain (%d, %a) model (%d, %a)\n", what,
+                    x.size(), T, (double)stop, a.count, (double)a.s, b.count, (double)b.s);
+      ++g_bad;
+    }
+  }
+}
+
+int main() {
+  std::mt19937_64 rng(12345);
+  std::normal_distribution<double> nd(0.0, 1.0);
+  std::uniform_real_distribution<double> ud(0.0, 1.0);
+  const float inf = INFINITY;
+  for (int rep = 0; rep < 6; ++rep) {
+    for (int n : {257, 1000, 5000, 33000}) {
+      for (double sig : {0.05, 1.0, 4.0}) {
+        // softmax exponentials, their sum, the probabilities sorted
+        // descending, their quad sums and mass stops
+        std::vector<float> l(n), e(n);
+        float mx = -1e30f;
+        for (int i = 0; i < n; ++i) {
+          l[i] = (float)(sig * nd(rng));
+          if (l[i] > mx) mx = l[i];
+        }
+        for (int i = 0; i < n; ++i) e[i] = std::exp(l[i] - mx);
+        check(e, 0.0f, inf, "softmax sum");
+        const float sv = chain(e, 0.0f, inf).s, inv = 1.0f / sv;
+        std::vector<float> p(n);
+        for (int i = 0; i < n; ++i) p[i] = e[i] * inv;
+        std::sort(p.begin(), p.end(), [](float a, float b) { return a > b; });
+        std::vector<float> q(n / 4);
+        for (int k = 0; k < n / 4; ++k) q[k] = ((p[4 * k] + p[4 * k + 1]) + p[4 * k + 2]) + p[4 * k + 3];
+        for (float vm : {0.5f, 0.95f, 0.999f, 0.9999f, 1.0f, 2.0f}) check(q, 0.0f, vm, "mass quads");
+        // stops at values the chain reaches exactly
+        std::vector<float> reach;
+        float m = 0.0f;
+        for (float t : q) {
+          m = m + t;
+          reach.push_back(m);
+        }
+        for (int k = 0; k < 4 && !reach.empty(); ++k)
+          check(q, 0.0f, reach[(size_t)(ud(rng) * reach.size()) % reach.size()], "mass at a reached value");
+        check(p, 0.0f, 0.95f, "mass singles");
+      }
+    }
+    // tie-heavy: exact small integers and dyadic fractions over large sums
+    for (int n : {300, 4000, 40000}) {
+      std::vector<float> t(n);
+      for (int i = 0; i < n; ++i) t[i] = (float)(1 + (rng() % 3));
+      check(t, 16777216.0f, inf, "integers over 2^24");
+      check(t, 8388608.0f, inf, "integers over 2^23");
+      for (int i = 0; i < n; ++i) t[i] = std::ldexp(1.0f, -(int)(rng() % 4));
+      check(t, 4194304.0f, inf, "dyadic over 2^22");
+      check(t, 0.0f, inf, "dyadic from 0");
+      for (int i = 0; i < n; ++i) t[i] = 0.5f + (float)(rng() % 4) * 0.25f;
+      check(t, 0.0f, (float)n * 0.6f, "dyadic with a stop");
+      // subnormals and zeros
+      for (int i = 0; i < n; ++i) t[i] = bfloat((uint32_t)(rng() % 0x800000u));
+      check(t, 0.0f, inf, "subnormals");
+      for (int i = 0; i < n; ++i) t[i] = (rng() % 3 == 0) ? -0.0f : (rng() % 2 ? 0.0f : 1e-38f);
+      check(t, 0.0f, inf, "zeros and -0");
+      // wide exponent range
+      for (int i = 0; i < n; ++i) t[i] = std::ldexp((float)(0.5 + 0.5 * ud(rng)), (int)(rng() % 120) - 60);
+      check(t, 0.0f, inf, "wide range");
+      check(t, 1.0f, 3.0e17f, "wide range with a stop");
+      // uniform terms with a non-zero start
+      for (int i = 0; i < n; ++i) t[i] = (float)ud(rng);
+      check(t, 123.456f, inf, "uniform from 123.456");
+      check(t, 0.0f, (float)n * 0.25f, "uniform with a stop");
+    }
+  }
+  std::printf("%lld cases, %lld mismatches, %lld of %lld chunks redone, %lld with a serial tail\n",
+              g_cases, g_bad, g_redo, g_chunks, g_tail);
+  return g_bad == 0 ? 0 : 1;
+}
