@@ -74,25 +74,45 @@ struct SeqResult {
 
 namespace seqsum_detail {
 
-// Terms xs[i - c0] for i in [from, to) added one at a time while s < stop,
-// s held as its bit pattern wb (uniform over the wave, so the compiler keeps
-// it scalar; sb: stop's bits, stop > 0, so s < stop is an unsigned compare of
-// |s|'s bits); 8 terms are read from LDS at a time.  Returns the index the
-// stop test failed at, or -1.
-__device__ __forceinline__ int hw_run(const float *xs, int c0, int from, int to, uint32_t sb,
+// Terms xs[i - c0] for i in [from, to) added one at a time while s < stop
+// (s: its bit pattern wb, uniform over the wave).  Whole steps of 8 terms,
+// read from LDS one step ahead, are added as one chain; the sum never
+// decreases (terms are not negative), so when a step ends below the stop no
+// test inside it failed.  The step that reaches the stop, and the last
+// partial step, are added term by term with the test before each.  Returns
+// the index whose test failed, or -1.
+__device__ __forceinline__ int hw_run(const float *xs, int c0, int from, int to, float stop,
                                       uint32_t &wb) {
-  for (int i = from; i < to; i += 8) {
+  float w = __uint_as_float(wb);
+  int i = from;
+  if (i + 8 <= to) {
     float v[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = i + k < to ? xs[i + k - c0] : 0.0f;
+    for (int k = 0; k < 8; ++k) v[k] = xs[i + k - c0];
+    for (;;) {
+      const bool more = i + 16 <= to;
+      float nv[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      if (i + k < to) {
-        if ((wb & 0x7FFFFFFFu) >= sb) return i + k;
-        wb = __builtin_amdgcn_readfirstlane(__float_as_uint(__fadd_rn(__uint_as_float(wb), v[k])));
-      }
+      for (int k = 0; k < 8; ++k) nv[k] = more ? xs[i + 8 + k - c0] : 0.0f;
+      float wn = w;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) wn = __fadd_rn(wn, v[k]);
+      if (!__builtin_amdgcn_readfirstlane((int)(wn < stop))) break;  // i: the step to test
+      w = wn;
+      i += 8;
+      if (!more) break;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = nv[k];
     }
   }
+  for (; i < to; ++i) {
+    if (!__builtin_amdgcn_readfirstlane((int)(w < stop))) {
+      wb = __builtin_amdgcn_readfirstlane(__float_as_uint(w));
+      return i;
+    }
+    w = __fadd_rn(w, xs[i - c0]);
+  }
+  wb = __builtin_amdgcn_readfirstlane(__float_as_uint(w));
   return -1;
 }
 
@@ -281,7 +301,7 @@ __device__ __forceinline__ SeqResult block_seq_sum(Load load, int n, float s, fl
           const int cl = __builtin_amdgcn_readlane(l_cls, t);
           const int st = __builtin_amdgcn_readlane(l_start, t);
           if (cl == kUnc) {
-            stop_at = hw_run(sh.xs, c0, st, __builtin_amdgcn_readlane(l_end, t), sb, wb);
+            stop_at = hw_run(sh.xs, c0, st, __builtin_amdgcn_readlane(l_end, t), stop, wb);
             if (stop_at >= 0) break;
             continue;
           }
@@ -306,10 +326,10 @@ __device__ __forceinline__ SeqResult block_seq_sum(Load load, int n, float s, fl
       if (redo) {
         // a prediction failed: the chunk term by term
         wb = __builtin_amdgcn_readfirstlane(__float_as_uint(s));
-        stop_at = hw_run(sh.xs, c0, c0, c0 + cn, sb, wb);
+        stop_at = hw_run(sh.xs, c0, c0, c0 + cn, stop, wb);
         stop_seg = -1;
       } else if (ns_all > kMaxSeg && stop_at < 0 && stop_seg < 0) {
-        stop_at = hw_run(sh.xs, c0, sh.seg_start[kMaxSeg], c0 + cn, sb, wb);
+        stop_at = hw_run(sh.xs, c0, sh.seg_start[kMaxSeg], c0 + cn, stop, wb);
       }
       if (lane == 0) {
         sh.stop_at = stop_at;

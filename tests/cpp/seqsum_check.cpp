@@ -2,13 +2,14 @@
 // the host, one chunk at a time exactly as the block runs it (fp64 prefix,
 // per-thread, one-edge and per-term classes and integer increments from
 // seqsum_terms.hpp, segment heads, the walk with its runs of hardware terms,
-// checks, serial redo and serial tail beyond the segment table, the stop search inside a clean
-// segment), against the plain left-to-right fp32 chain with its stop test.
-// Sequences: softmax-like exponentials, sorted probabilities and their quad
-// sums with mass stops (also stops equal to a value the chain reaches),
-// tie-heavy terms (exact small integers and dyadic fractions over large
-// sums), subnormals, wide exponent ranges, zeros and -0, and non-zero start
-// values; 1 to 8 terms per thread (chunks of 1,024 to 8,192 terms).  Prints the mismatch count and the share of chunks redone;
+// checks, serial redo and serial tail beyond the segment table, the stop
+// search inside a clean segment), against the plain left-to-right fp32
+// chain with its stop test.  Sequences: softmax-like exponentials, sorted
+// probabilities and their quad sums with mass stops (also stops equal to a
+// value the chain reaches), tie-heavy terms (exact small integers and dyadic
+// fractions over large sums), subnormals, wide exponent ranges, zeros and
+// -0, and non-zero start values; 1 to 8 terms per thread (chunks of 1,024 to
+// 8,192 terms).  Prints the mismatch count and the share of chunks redone;
 // exits 0 when nothing mismatches.
 #include <algorithm>
 #include <cmath>
@@ -106,7 +107,15 @@ static Res model(const std::vector<float> &x, float s, float stop, int T) {
     seg_start.push_back(c0 + cn);
     seg_r.push_back(R);
     auto hw_run = [&](int from, int to, float &w) {
-      for (int i = from; i < to; ++i) {
+      int i = from;
+      while (i + 8 <= to) {
+        float wn = w;
+        for (int k = 0; k < 8; ++k) wn = wn + x[i + k];
+        if (!(wn < stop)) break;
+        w = wn;
+        i += 8;
+      }
+      for (; i < to; ++i) {
         if (!(w < stop)) return i;
         w = w + x[i];
       }
