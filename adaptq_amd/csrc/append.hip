@@ -417,24 +417,28 @@ __global__ __launch_bounds__(128) void append_kv_kernel(HeadDesc *const *descs, 
   encode_row<P, VB, false>(d, st, c, 0, 1, vals, 1, dim, inv_sqrt_p, sqrt_p, s_q4);
 }
 
-// One token for few heads: a wave per vector (wave 0 the key, wave 1 the
-// value of head blockIdx.x), lane l holding entries l and l + 64.  The same
-// float steps as encode_vec in the same order: the sums of squares left to
-// right (every lane runs the chain over the squares in LDS), the butterflies
-// of span 1, 2, ... between lanes (shfl_xor) and, at padded 128, inside the
-// lane; codes are gathered in LDS and lane k packs word k of the row.  A lane
-// per vector (append_kv_kernel) leaves one wave with the whole codec's
-// dependency chain when there are few heads (about 10 us for 4 heads).
+// Few vectors: a wave per vector (wave 0 the key, wave 1 the value of token
+// blockIdx.y of head blockIdx.x), lane l holding entries l and l + 64.  The
+// same float steps as encode_vec in the same order: the sums of squares left
+// to right (every lane runs the chain over the squares in LDS), the
+// butterflies of span 1, 2, ... between lanes (shfl_xor) and, at padded 128,
+// inside the lane; codes are gathered in LDS and lane k packs word k of the
+// row.  A lane per vector (append_kv_kernel, append_kernel) leaves each wave
+// with the whole codec's dependency chain for 64 vectors, which few vectors
+// cannot hide (about 10 us for one token of 4 heads, 36 us for 2,048 tokens
+// of 4 heads).  With one token the kernel advances the ring states itself;
+// with more, commit_kernel follows.
 template <int P, int KB, int VB>
 __global__ __launch_bounds__(128) void append_one_kernel(HeadDesc *const *descs,
                                                          const float *__restrict__ keys,
                                                          const float *__restrict__ vals, int dim,
-                                                         float inv_sqrt_p, float sqrt_p) {
+                                                         int n_tok, float inv_sqrt_p,
+                                                         float sqrt_p) {
   constexpr int E = P / 64;
   __shared__ Q4Entry s_q4[(KB == 4 || VB == 4) ? kQ4Entries : 1];
   __shared__ __align__(16) float s_sq[2][P];
   __shared__ uint8_t s_code[2][P];
-  const int c = blockIdx.x;
+  const int c = blockIdx.x, t = blockIdx.y;
   const int lane = threadIdx.x & 63, side = threadIdx.x >> 6;
   if constexpr (KB == 4 || VB == 4) {
     for (int i = threadIdx.x; i < kQ4Entries; i += blockDim.x) s_q4[i] = q4s_entry(i);
@@ -443,14 +447,14 @@ __global__ __launch_bounds__(128) void append_one_kernel(HeadDesc *const *descs,
   const RingState st = d->st;
   __syncthreads();  // both waves have the old state and the table
   const int cap = d->cap;
-  if (threadIdx.x == 0) d->st = ring_after(st, 1, cap, d->hyb);
-  const float *x = (side == 0 ? keys : vals) + (size_t)c * dim;
-  if (0 < mirror_count(st, 1, cap, d->hyb)) {
-    float *m = (side == 0 ? d->raw_k : d->raw_v) + (size_t)st.raw_count * dim;
+  if (n_tok == 1 && threadIdx.x == 0) d->st = ring_after(st, 1, cap, d->hyb);
+  const float *x = (side == 0 ? keys : vals) + ((size_t)c * n_tok + t) * dim;
+  if (t < mirror_count(st, n_tok, cap, d->hyb)) {
+    float *m = (side == 0 ? d->raw_k : d->raw_v) + (size_t)(st.raw_count + t) * dim;
     for (int i = lane; i < dim; i += 64) m[i] = x[i];
   }
-  if (cap <= 0) return;
-  const int slot = (int)((long long)st.head % cap);
+  if (cap <= 0 || t < n_tok - cap) return;  // overwritten within this append
+  const int slot = (int)(((long long)st.head + t) % cap);
   float v[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) v[e] = lane + 64 * e < dim ? x[lane + 64 * e] : 0.0f;
@@ -736,21 +740,27 @@ hipError_t launch_side(HeadDesc *const *descs, int n_ctx, int side, int bits, co
 
 }  // namespace
 
-// Heads up to which a one-token append takes a wave per vector (above, a lane
+// Token-heads up to which an append takes a wave per vector (above, a lane
 // per vector keeps the launch to a few waves' worth of work per CU).
-constexpr int kOneWaveMaxCtx = 2048;
+constexpr int kOneWaveMaxVectors = 16384;
 
 hipError_t launch_append(HeadDesc *const *descs, int n_ctx, int dim, int padded, int k_bits,
                          int v_bits, const float *keys, const float *vals, int n_tok,
                          hipStream_t s) {
   if (n_ctx <= 0 || n_tok <= 0) return hipSuccess;
-  if (n_tok == 1 && (padded == 64 || padded == 128) && n_ctx <= kOneWaveMaxCtx) {
-    // few heads: a wave per vector, a block per head (both sides, the ring state)
+  if ((padded == 64 || padded == 128) && n_tok <= 65535 &&
+      (long long)n_ctx * n_tok <= kOneWaveMaxVectors) {
+    // few vectors: a wave per vector, a block per token and head (both sides;
+    // the ring states in the kernel for one token, by commit_kernel for more)
     const float sp = sqrtf((float)padded), isp = 1.0f / sp;
-#define AQ_ONE(P_, KB_, VB_)                                                                  \
-  if (padded == P_ && k_bits == KB_ && v_bits == VB_) {                                      \
-    append_one_kernel<P_, KB_, VB_><<<n_ctx, 128, 0, s>>>(descs, keys, vals, dim, isp, sp); \
-    return hipGetLastError();                                                                \
+    const dim3 grid((unsigned)n_ctx, (unsigned)n_tok);
+#define AQ_ONE(P_, KB_, VB_)                                                                   \
+  if (padded == P_ && k_bits == KB_ && v_bits == VB_) {                                       \
+    append_one_kernel<P_, KB_, VB_><<<grid, 128, 0, s>>>(descs, keys, vals, dim, n_tok, isp, sp); \
+    if (n_tok == 1) return hipGetLastError();                                                 \
+    if (const hipError_t e1 = hipGetLastError(); e1 != hipSuccess) return e1;                \
+    commit_kernel<<<(n_ctx + 255) / 256, 256, 0, s>>>(descs, n_ctx, n_tok);                   \
+    return hipGetLastError();                                                                 \
   }
 #define AQ_ONE_V(P_, KB_) AQ_ONE(P_, KB_, 2) AQ_ONE(P_, KB_, 3) AQ_ONE(P_, KB_, 4) AQ_ONE(P_, KB_, 16)
     AQ_ONE_V(64, 2) AQ_ONE_V(64, 3) AQ_ONE_V(64, 4) AQ_ONE_V(64, 16)

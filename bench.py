@@ -323,18 +323,18 @@ def secondary(L, last_error, torch, np, stream, reps=20, which=("C1", "C2", "C3"
     span reads.  Every stack is created fresh, filled through the device
     append, then timed; data are seeded and generated as each config states.
       C1: 4 heads d64 K4/V2, 2048 tokens: the whole-MHA append of the 2048
-          tokens (one span) and one whole-MHA decode, dense (v_mass 0,
+          tokens (median of 5, each on emptied rings) and one whole-MHA decode, dense (v_mass 0,
           hybrid 0) and Engine defaults (v_mass 0.95, hybrid 512: the
           sparse-V branch at n = 2048).
       C2: 24 layers x 14 heads d64, n = 512 (layer 0 K16/V2, others K4/V2,
-          channels 3 and 17 x20): the appends of every layer (one span), one
+          channels 3 and 17 x20): the appends of every layer (median of 5), one
           decode step over all layers, packed
           (hybrid 0) and hybrid FP32 (Engine defaults: every layer takes the
           raw-mirror branch), each with one call per layer and through two
           plans (layer 0, layers 1-23).
       C3: 22 layers x 4 heads d64 (layer 0 K16/V2, others K3/V2), Student-t(4)
-          / sqrt 2: 1024-token bulk append, then 256 steps of (append 1 +
-          decode) for every layer; µs per step, host wall clock included;
+          / sqrt 2: 1024-token bulk append (median of 5), then 256 steps of
+          (append 1 + decode) for every layer; µs per step, host wall clock included;
           per-layer calls (as the reference's Engine makes them) and two
           plans (layer 0, layers 1-21) per step.
       C4: 8 heads d128 K4/V4, cap 32768, 40000 tokens appended (7232
@@ -368,16 +368,23 @@ def secondary(L, last_error, torch, np, stream, reps=20, which=("C1", "C2", "C3"
     def rate(us, nbytes):
         return {"us": us, "bytes": nbytes, "gb_per_s": nbytes / us / 1e3}
 
-    def once(fn):
-        """One HIP-event span of fn on `stream` (appends change the state, so
-        they are timed once), in us."""
-        torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        fn()
-        b.record(stream)
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) * 1e3
+    def appended(fn, mhas, n=5):
+        """Median of n HIP-event spans of the append fn on `stream`, each on
+        rings emptied by adaptq_mha_reset (untimed) and filled again, in us;
+        the rings end filled."""
+        ts = []
+        for i in range(n):
+            if i:
+                for m in mhas:
+                    L.adaptq_mha_reset(m)
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            fn()
+            b.record(stream)
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b) * 1e3)
+        return float(np.median(ts))
 
     def stack(specs):
         ms = [L.adaptq_mha_create(*s) for s in specs]
@@ -410,7 +417,8 @@ def secondary(L, last_error, torch, np, stream, reps=20, which=("C1", "C2", "C3"
         c1 = {}
         for name, vm, hyb in (("dense", 0.0, 0), ("engine_defaults_sparse_v", 0.95, 512)):
             ms = stack([(4, 64, 4, 2, 2048, 42, vm, hyb)])
-            app_us = once(lambda: ok(L.adaptq_mha_append_all_device(ms[0], dp(kd), dp(vd), 2048, 0, sp)))
+            app_us = appended(lambda: ok(L.adaptq_mha_append_all_device(ms[0], dp(kd), dp(vd), 2048, 0, sp)),
+                              ms)
             us = span(lambda: ok(L.adaptq_mha_compute_all_device(ms[0], dp(qd), dp(od), sp)))
             c1[name] = rate(us, 4 * 2048 * decode_bytes_per_token(64, 4, 2))
             c1[name + "_append_2048"] = rate(app_us, 4 * 2048 * append_bytes_per_token(64, 64, 4, 2))
@@ -438,7 +446,7 @@ def secondary(L, last_error, torch, np, stream, reps=20, which=("C1", "C2", "C3"
                 for l, m in enumerate(ms):
                     ok(L.adaptq_mha_append_all_device(m, kp[l], vp[l], n, 0, sp))
             c2[name + "_append_512"] = rate(
-                once(append_all), nh * n * (append_bytes_per_token(64, 64, 16, 2)
+                appended(append_all, ms), nh * n * (append_bytes_per_token(64, 64, 16, 2)
                                             + (nl - 1) * append_bytes_per_token(64, 64, 4, 2)))
 
             # pointers made before timing: the span measures the library's
@@ -488,12 +496,8 @@ def secondary(L, last_error, torch, np, stream, reps=20, which=("C1", "C2", "C3"
             def bulk_append():
                 for l, m in enumerate(ms):
                     ok(L.adaptq_mha_append_all_device(m, dp(bulk[0, l]), dp(bulk[1, l]), n0, 0, sp))
+            append_us = appended(bulk_append, ms)
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            bulk_append()
-            b.record(stream)
-            torch.cuda.synchronize()
-            append_us = a.elapsed_time(b) * 1e3
             # pointers made before timing (tensor views cost a few us each)
             pp = [[(dp(per[0, s, l]), dp(per[1, s, l]), dp(per[2, s, l])) for l in range(nl)]
                   for s in range(steps)]
@@ -554,12 +558,8 @@ def secondary(L, last_error, torch, np, stream, reps=20, which=("C1", "C2", "C3"
         qd = torch.randn(nq, nh, 128, generator=g, device=dev)
         od = torch.empty_like(qd)
         ms = stack([(nh, 128, 4, 4, cap, 7, 0.0, 0)])
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        ok(L.adaptq_mha_append_all_device(ms[0], dp(kd), dp(vd), ntok, 0, sp))
-        b.record(stream)
-        torch.cuda.synchronize()
-        app_us = a.elapsed_time(b) * 1e3
+        app_us = appended(lambda: ok(L.adaptq_mha_append_all_device(ms[0], dp(kd), dp(vd), ntok, 0, sp)),
+                          ms)
         per_query = nh * cap * decode_bytes_per_token(128, 4, 4)
         row = 128 * 4
         us = span(lambda: ok(L.adaptq_ggml_attn_f32_device(ms[0], dp(qd), 128, nh, nq, row, nh * row,
