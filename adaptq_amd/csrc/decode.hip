@@ -305,6 +305,11 @@ __device__ void write_partial(float *part, float m, float l, const float *acc_ld
   for (int i = threadIdx.x; i < P; i += blockDim.x) part[4 + i] = acc_lds[i];
 }
 
+// Headroom (base 2) of the quantised-K decode's lazy reference maximum: the
+// weights exp2(logit - m) stay below 2^16, far from fp32 overflow for any
+// ring (2^31 tokens x 2^16 x the V scales).
+constexpr float kLazyMax = 16.0f;
+
 // The reference seeds the running maximum of every softmax at -1e30
 // (attention.cpp:496, :566, and compute_avx2): logits at or below it get
 // weight expf(l - (-1e30)) = 0.  In base-2 units (quantised K) the seed is
@@ -824,14 +829,21 @@ __global__ __launch_bounds__(kLutThreads, (KB == 2 || KB == 4) ? 4 : 2) void dec
   for (; base < t_end; base += kStride) {
     const bool valid = base + lane < t_end;
 
-    // ---- online softmax (wave-uniform running max) ----
-    const float tmax = wave_max_dpp(logit);
-    if (tmax > m_run) {
-      const float alpha = m_run == -INFINITY ? 0.0f : wexp(m_run - tmax);
+    // ---- online softmax (wave-uniform reference maximum) ----
+    // Quantised K: the reference maximum moves only when a logit exceeds it
+    // by more than kLazyMax (base 2), so weights stay below 2^kLazyMax and
+    // most tiles need one compare instead of the wave maximum; the softmax
+    // is the same up to rounding, as the maximum only scales every weight.
+    const bool bump = KQ ? __ballot(logit > m_run + kLazyMax) != 0ull : true;
+    if (bump) {
+      const float tmax = wave_max_dpp(logit);
+      if (tmax > m_run) {
+        const float alpha = m_run == -INFINITY ? 0.0f : wexp(m_run - tmax);
 #pragma unroll
-      for (int i = 0; i < D; ++i) acc[i] *= alpha;
-      l_run *= alpha;
-      m_run = tmax;
+        for (int i = 0; i < D; ++i) acc[i] *= alpha;
+        l_run *= alpha;
+        m_run = tmax;
+      }
     }
     const float e = valid ? wexp(logit - m_run) : 0.0f;
     l_run += e;
