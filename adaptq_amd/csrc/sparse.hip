@@ -882,7 +882,7 @@ __global__ __launch_bounds__(kSelThreads) void sparse_fused_kernel(
   constexpr int U = PT * VB / 8 / UB;  // units per V row (4..16)
   constexpr int TPI = 64 / U;          // tokens per wave step
   constexpr int NW = kSelThreads / 64;
-  constexpr int UNR = 4;               // row loads in flight per lane
+  constexpr int UNR = PT ? 16 : 4;               // row loads in flight per lane
   const int item = blockIdx.x, tid = threadIdx.x;
   const HeadDesc *d = item_desc[item];
   const int n = d->st.size, cap = d->cap, dim = d->dim;
@@ -999,14 +999,17 @@ struct VUnit {
 // with w_t the selection weight (0 for tokens left out).  A row of P codes is
 // U = P / VUnit::codes units; a wave takes TPI = max(1, 64 / U) tokens per
 // step, lane (sub, u) the units u, u + 64, ... of token sub, so every lane
-// reads whole bytes of a row in one coalesced cache line.
-template <int VB>
+// reads whole bytes of a row in one coalesced cache line.  PT: the padded
+// size when it is 64 or 128 (one unit per lane: 16 tokens' loads in flight
+// per lane), else 0 (any size, 4 tokens in flight).
+template <int VB, int PT>
 __global__ __launch_bounds__(kThreads) void sparse_vsum_kernel(HeadDesc *const *item_desc,
                                                                const float *ws, size_t ws_stride,
                                                                int chunk, int n_splits,
                                                                float *partials) {
   constexpr int CPU = VUnit<VB>::codes, UB = VUnit<VB>::bytes;
-  constexpr int kMaxAcc = 16;  // codes per lane at P = 1024: 4 x 4, 8 x 2 or 2 x 8
+  // codes per lane: at most 16 (P = 1024: 4 x 4, 8 x 2 or 2 x 8), one unit at PT
+  constexpr int kMaxAcc = PT ? CPU : 16;
   __shared__ float s_cb[16];
   __shared__ float s_red[kThreads / 64][kMaxPadded];
   const int item = blockIdx.y, split = blockIdx.x;
@@ -1032,7 +1035,7 @@ __global__ __launch_bounds__(kThreads) void sparse_vsum_kernel(HeadDesc *const *
   // UNR tokens per step, their weights and code units requested before any
   // is used (rows of weight 0 still load: the step's loads stay in flight
   // together)
-  constexpr int UNR = 4;
+  constexpr int UNR = PT ? 16 : 4;
   const int step = (kThreads / 64) * TPI;
   if (active) {
     for (int t = t0 + wave * TPI + sub; t < t_end; t += UNR * step) {
@@ -1288,9 +1291,21 @@ hipError_t launch_decode_sparse(HeadDesc *const *descs, int n_items, const Decod
     }
     const dim3 g3(splits, cnt);
     switch (sh.v_bits) {
-      case 2: sparse_vsum_kernel<2><<<g3, kThreads, 0, s>>>(dsc, w, stride, kVChunk, splits, parts); break;
-      case 3: sparse_vsum_kernel<3><<<g3, kThreads, 0, s>>>(dsc, w, stride, kVChunk, splits, parts); break;
-      case 4: sparse_vsum_kernel<4><<<g3, kThreads, 0, s>>>(dsc, w, stride, kVChunk, splits, parts); break;
+      case 2:
+        if (sh.padded == 64) sparse_vsum_kernel<2, 64><<<g3, kThreads, 0, s>>>(dsc, w, stride, kVChunk, splits, parts);
+        else if (sh.padded == 128) sparse_vsum_kernel<2, 128><<<g3, kThreads, 0, s>>>(dsc, w, stride, kVChunk, splits, parts);
+        else sparse_vsum_kernel<2, 0><<<g3, kThreads, 0, s>>>(dsc, w, stride, kVChunk, splits, parts);
+        break;
+      case 3:
+        if (sh.padded == 64) sparse_vsum_kernel<3, 64><<<g3, kThreads, 0, s>>>(dsc, w, stride, kVChunk, splits, parts);
+        else if (sh.padded == 128) sparse_vsum_kernel<3, 128><<<g3, kThreads, 0, s>>>(dsc, w, stride, kVChunk, splits, parts);
+        else sparse_vsum_kernel<3, 0><<<g3, kThreads, 0, s>>>(dsc, w, stride, kVChunk, splits, parts);
+        break;
+      case 4:
+        if (sh.padded == 64) sparse_vsum_kernel<4, 64><<<g3, kThreads, 0, s>>>(dsc, w, stride, kVChunk, splits, parts);
+        else if (sh.padded == 128) sparse_vsum_kernel<4, 128><<<g3, kThreads, 0, s>>>(dsc, w, stride, kVChunk, splits, parts);
+        else sparse_vsum_kernel<4, 0><<<g3, kThreads, 0, s>>>(dsc, w, stride, kVChunk, splits, parts);
+        break;
       default: return hipErrorInvalidValue;
     }
     e = hipGetLastError();
