@@ -882,7 +882,7 @@ __global__ __launch_bounds__(kSelThreads) void sparse_fused_kernel(
   constexpr int U = PT * VB / 8 / UB;  // units per V row (4..16)
   constexpr int TPI = 64 / U;          // tokens per wave step
   constexpr int NW = kSelThreads / 64;
-  constexpr int UNR = PT ? 16 : 4;               // row loads in flight per lane
+  constexpr int UNR = 4;               // row loads in flight per lane
   const int item = blockIdx.x, tid = threadIdx.x;
   const HeadDesc *d = item_desc[item];
   const int n = d->st.size, cap = d->cap, dim = d->dim;
