@@ -665,6 +665,201 @@ __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, fl
   }
 }
 
+// Sort of rings above kSelectInBlock and up to kItemSortMax tokens: a stable
+// LSD radix sort of each item's 32-bit keys key_hi(p) with the tokens as
+// payload.  The select kernel stores the keys less the item's smallest key,
+// so the digits cover only the bits of the key range: kRsBits a pass, at
+// most 3 passes (keys of probabilities in [0, 1] span less than 2^30; NaN
+// keys are all equal).  Ties keep token order, which is the order make_key
+// gives them.  Pass k is two launches over (blocks of kRsKeys positions) x items.
+// The count kernel: a block counts the pass's digits among its positions and
+// stores them at count[block][digit].  The scatter kernel: a block takes its
+// offsets from the item's counts (digits below, then the same digit in
+// blocks before it), ranks its keys stably in LDS (a ballot per digit bit
+// and running per-wave digit counts) and writes each key
+// to offset[digit] + its rank among the block's keys of that digit.  Nothing
+// crosses blocks inside a launch (device-wide atomics on the counts, and a
+// last-block scan behind device-scope fences, each measured 3-5x slower than
+// the two launches).  Longer rings use one device-wide rocPRIM sort instead.
+constexpr int kRsThreads = 512;
+constexpr int kRsRounds = 4;
+constexpr int kRsWaves = kRsThreads / 64;
+constexpr int kRsKeys = kRsThreads * kRsRounds;  // positions per block and pass
+constexpr int kRsBits = 10;
+constexpr int kRsPasses = 3;
+constexpr int kRsDigits = 1 << kRsBits;
+constexpr int kRsDPT = kRsDigits / kRsThreads;  // digits per thread
+constexpr int kItemSortMax = 65536;
+constexpr int kRsMaxBlocks = kItemSortMax / kRsKeys;
+constexpr int kRsBins = kRsDigits * kRsMaxBlocks;  // (block, digit) counts
+static_assert(kRsDigits % kRsThreads == 0, "whole digits per thread");
+
+// Word offsets inside an item's sort region (uint32): a header (0: passes,
+// 5: the smallest key, 6: tokens; pass k takes bits kRsBits k and up), the counts ((block, digit),
+// block-major), then keys A, keys B, tokens A, tokens B of Sa = align64(S)
+// words.
+struct ItemSort {
+  static constexpr size_t cnt = 16, keys = cnt + kRsBins;
+  static constexpr size_t sa(int S) { return ((size_t)S + 63) & ~(size_t)63; }
+  static constexpr size_t words(int S) { return keys + 4 * sa(S); }
+};
+
+// The item sort's state for one (item, pass): false when the item does not
+// take this pass (sorted in the select kernel, or its key range is shorter).
+struct RsPass {
+  uint32_t *reg;
+  int n, G, sft;
+  const uint32_t *sk, *stk;  // input keys and tokens
+  uint32_t *dk, *dtk;        // output keys and tokens
+};
+
+__device__ __forceinline__ bool rs_pass(int pass, uint32_t *sort_ws, size_t item_words, int S,
+                                        RsPass &r) {
+  // one read of the header (the select kernel's): passes 0 for items it
+  // sorted itself
+  r.reg = sort_ws + (size_t)blockIdx.y * item_words;
+  const uint4 h = *reinterpret_cast<const uint4 *>(r.reg);
+  const uint4 h1 = *reinterpret_cast<const uint4 *>(r.reg + 4);
+  if (pass >= (int)h.x) return false;
+  r.n = (int)h1.z;
+  r.G = (r.n + kRsKeys - 1) / kRsKeys;
+  if ((int)blockIdx.x >= r.G) return false;
+  r.sft = pass * kRsBits;
+  const size_t Sa = ItemSort::sa(S);
+  const int in = pass & 1, out = in ^ 1;
+  r.sk = r.reg + ItemSort::keys + in * Sa;
+  r.stk = r.reg + ItemSort::keys + (2 + in) * Sa;
+  r.dk = r.reg + ItemSort::keys + out * Sa;
+  r.dtk = r.reg + ItemSort::keys + (2 + out) * Sa;
+  return true;
+}
+
+// Count kernel of one pass of the item sort (see above): grid (blocks, items).
+__global__ __launch_bounds__(kRsThreads) void sparse_rsort_count_kernel(int pass, uint32_t *sort_ws,
+                                                                        size_t item_words, int S) {
+  __shared__ uint32_t s_hist[kRsDigits];
+  RsPass r;
+  if (!rs_pass(pass, sort_ws, item_words, S, r)) return;
+  const int b = blockIdx.x, tid = threadIdx.x;
+  uint32_t k[kRsRounds];
+#pragma unroll
+  for (int j = 0; j < kRsRounds; ++j) {
+    const int pos = b * kRsKeys + j * kRsThreads + tid;
+    k[j] = pos < r.n ? r.sk[pos] : 0u;
+  }
+#pragma unroll
+  for (int j = 0; j < kRsDPT; ++j) s_hist[j * kRsThreads + tid] = 0u;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kRsRounds; ++j)
+    if (b * kRsKeys + j * kRsThreads + tid < r.n)
+      atomicAdd(&s_hist[(k[j] >> r.sft) & (kRsDigits - 1u)], 1u);
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kRsDPT; ++j)
+    r.reg[ItemSort::cnt + (size_t)b * kRsDigits + j * kRsThreads + tid] = s_hist[j * kRsThreads + tid];
+}
+
+// Scatter kernel of one pass of the item sort (see above): grid (blocks, items).
+// Wave w of the block owns positions w 64 R .. w 64 R + 64 R - 1 of its
+// range, 64 a round: a key's rank among the block's keys of its digit is the
+// count of that digit in earlier waves (a prefix over the waves' totals),
+// plus in this wave's earlier rounds (the wave's running count), plus in
+// lanes below it (a ballot per digit bit).
+__global__ __launch_bounds__(kRsThreads) void sparse_rsort_pass_kernel(int pass, uint32_t *sort_ws,
+                                                                       size_t item_words, int S) {
+  constexpr int R = kRsRounds, NW = kRsWaves;
+  __shared__ __align__(16) uint16_t s_wc[NW][kRsDigits];  // per-wave digit counts
+  __shared__ uint32_t s_off[kRsDigits];
+  __shared__ uint32_t s_wsum[NW];
+  RsPass rp;
+  if (!rs_pass(pass, sort_ws, item_words, S, rp)) return;
+  const int b = blockIdx.x, n = rp.n, sft = rp.sft;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int p0 = b * kRsKeys + wave * 64 * R + lane;  // this lane's position in round 0
+  uint32_t kk[R], tk[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const bool valid = p0 + 64 * r < n;
+    kk[r] = valid ? rp.sk[p0 + 64 * r] : 0u;
+    tk[r] = valid ? rp.stk[p0 + 64 * r] : 0u;
+  }
+  // this block's offsets: thread t takes digits 2t, 2t + 1, adds each one's
+  // counts over every block (total) and over the blocks before this one; an
+  // exclusive scan of the totals over the digits gives each digit's start
+  static_assert(kRsDPT == 2, "two digits (one uint2) per thread");
+  {
+    const uint2 *c = reinterpret_cast<const uint2 *>(rp.reg + ItemSort::cnt) + tid;
+    uint32_t tot[2] = {0u, 0u}, pre[2] = {0u, 0u};
+    for (int j0 = 0; j0 < rp.G; j0 += 8) {
+      uint2 v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        v[j] = j0 + j < rp.G ? c[(size_t)(j0 + j) * (kRsDigits / 2)] : make_uint2(0u, 0u);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const bool before = j0 + j < b;
+        pre[0] += before ? v[j].x : 0u;
+        pre[1] += before ? v[j].y : 0u;
+        tot[0] += v[j].x;
+        tot[1] += v[j].y;
+      }
+    }
+    const uint32_t mine = tot[0] + tot[1];
+    uint32_t incl = mine;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += y;
+    }
+    if (lane == 63) s_wsum[wave] = incl;
+    uint4 *z4 = reinterpret_cast<uint4 *>(&s_wc[0][0]);
+    for (int i = tid; i < NW * kRsDigits / 8; i += kRsThreads) z4[i] = make_uint4(0u, 0u, 0u, 0u);
+    __syncthreads();
+    uint32_t base = incl - mine;
+    for (int k = 0; k < wave; ++k) base += s_wsum[k];
+    s_off[2 * tid] = base + pre[0];
+    s_off[2 * tid + 1] = base + tot[0] + pre[1];
+  }
+  const uint64_t below = (1ull << lane) - 1ull;
+  uint32_t dg[R], rk[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const bool valid = p0 + 64 * r < n;
+    dg[r] = (kk[r] >> sft) & (kRsDigits - 1u);
+    uint64_t same = __ballot(valid);
+#pragma unroll
+    for (int bit = 0; bit < kRsBits; ++bit) {
+      const uint64_t m = __ballot((dg[r] >> bit) & 1u);
+      same &= ((dg[r] >> bit) & 1u) ? m : ~m;
+    }
+    const uint32_t lower = (uint32_t)__popcll(same & below);
+    const uint32_t earlier = s_wc[wave][dg[r]];  // this wave's earlier rounds
+    rk[r] = earlier + lower;
+    if (valid && lower == 0u) s_wc[wave][dg[r]] = (uint16_t)(earlier + (uint32_t)__popcll(same));
+  }
+  __syncthreads();
+  // per digit, the counts of the waves before (exclusive prefix, in place)
+  for (int d = tid; d < kRsDigits; d += kRsThreads) {
+    uint32_t run = 0u;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const uint32_t c = s_wc[w][d];
+      s_wc[w][d] = (uint16_t)run;
+      run += c;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (p0 + 64 * r < n) {
+      const uint32_t dst = s_off[dg[r]] + s_wc[wave][dg[r]] + rk[r];
+      rp.dk[dst] = kk[r];
+      rp.dtk[dst] = tk[r];
+    }
+  }
+}
+
 // One block of kSelThreads per item: the sparse-V selection as per-token
 // weights.  n <= kSelectInBlock: select_small, all of it.  Larger n (keys != null):
 // the first of three steps.  This kernel takes the max, the exponentials and
@@ -682,7 +877,9 @@ __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, fl
 __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *const *item_desc,
                                                                     float v_mass, float *ws,
                                                                     size_t ws_stride, int S,
-                                                                    uint64_t *keys, uint32_t *toks) {
+                                                                    uint64_t *keys, uint32_t *toks,
+                                                                    uint32_t *sort_ws,
+                                                                    size_t item_words) {
   __shared__ SelectShared sh;
   const int item = blockIdx.x;
   const int tid = threadIdx.x;
@@ -695,6 +892,8 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
       toks[(size_t)item * S + i] = 0u;
     }
   }
+  // items this kernel sorts itself take no item-sort pass
+  if (sort_ws && n <= kSelectInBlock && tid == 0) sort_ws[(size_t)item * item_words] = 0u;
   if (n == 0) return;
   float *lg = ws + (size_t)item * ws_stride;
   const int s0 = (int)(((long long)d->st.head - n + cap) % cap);
@@ -739,21 +938,69 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
   const float inv = s_bcast[0];
   if (tid == 0) lg[n] = inv;
 
-  // 3. sort keys and tokens into the item's slot
+  if (!sort_ws) {
+    // 3. sort keys and tokens into the item's slot
 #pragma unroll 8
-  for (int i = tid; i < S; i += kSelThreads) {
-    keys[(size_t)item * S + i] = slot_hi | (i < n ? key_hi(__fmul_rn(lg[i], inv)) : 0xFFFFFFFFu);
-    toks[(size_t)item * S + i] = (uint32_t)i;
+    for (int i = tid; i < S; i += kSelThreads) {
+      keys[(size_t)item * S + i] = slot_hi | (i < n ? key_hi(__fmul_rn(lg[i], inv)) : 0xFFFFFFFFu);
+      toks[(size_t)item * S + i] = (uint32_t)i;
+    }
+    return;
+  }
+  // 3. the item sort's input: keys less the smallest key, tokens in token
+  // order, and the passes the key range needs.  p = e * inv is monotone in
+  // e, so the largest e gives the smallest key and the smallest e the
+  // largest (a NaN inv makes every key 0xFFFFFFFF).
+  uint32_t *reg = sort_ws + (size_t)item * item_words;
+  uint32_t *k_a = reg + ItemSort::keys, *t_a = k_a + 2 * ItemSort::sa(S);
+  float e_lo = __builtin_inff(), e_hi = 0.0f;
+#pragma unroll 8
+  for (int i = tid; i < n; i += kSelThreads) {
+    const float e = lg[i];
+    e_lo = fminf(e_lo, e);
+    e_hi = fmaxf(e_hi, e);
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    e_lo = fminf(e_lo, __shfl_xor(e_lo, off));
+    e_hi = fmaxf(e_hi, __shfl_xor(e_hi, off));
+  }
+  if ((tid & 63) == 0) {
+    s_red[tid >> 6] = e_lo;
+    s_red[32 + (tid >> 6)] = e_hi;
+  }
+  __syncthreads();
+  for (int w = 0; w < kSelThreads / 64; ++w) {
+    e_lo = fminf(e_lo, s_red[w]);
+    e_hi = fmaxf(e_hi, s_red[32 + w]);
+  }
+  const uint32_t kmin = key_hi(__fmul_rn(e_hi, inv)), kmax = key_hi(__fmul_rn(e_lo, inv));
+#pragma unroll 8
+  for (int i = tid; i < n; i += kSelThreads) {
+    k_a[i] = key_hi(__fmul_rn(lg[i], inv)) - kmin;
+    t_a[i] = (uint32_t)i;
+  }
+  if (tid == 0) {
+    const uint32_t range = kmax - kmin;
+    const int bits = range ? 32 - __clz((int)range) : 0;
+    const int np = (bits + kRsBits - 1) / kRsBits;  // 0: every key equal, token order is sorted
+    reg[0] = (uint32_t)np;
+    reg[5] = kmin;
+    reg[6] = (uint32_t)n;
   }
 }
 
 // The cut and the weights of an item above kSelectInBlock tokens, over its sorted
-// slot (keys: slot << 32 | key_hi, toks: tokens).
+// keys: the item sort's final buffers (sort_ws != null: key_hi and tokens), or
+// the item's slot of the device-wide sort (keys: slot << 32 | key_hi, toks:
+// tokens).
+template <bool ITEM>
 __global__ __launch_bounds__(kSelThreads) void sparse_cut_kernel(HeadDesc *const *item_desc,
                                                                  float v_mass, float *ws,
                                                                  size_t ws_stride, int S,
                                                                  const uint64_t *keys,
-                                                                 const uint32_t *toks) {
+                                                                 const uint32_t *toks,
+                                                                 const uint32_t *sort_ws,
+                                                                 size_t item_words) {
   __shared__ float s_stage[kStage];
   __shared__ float s_bcast[2];
   __shared__ int s_cut;
@@ -767,9 +1014,25 @@ __global__ __launch_bounds__(kSelThreads) void sparse_cut_kernel(HeadDesc *const
   float *lg = ws + (size_t)item * ws_stride;
   const int s0 = (int)(((long long)d->st.head - n + cap) % cap);
   const float inv = lg[n];
-  const uint64_t *kk = keys + (size_t)item * S;
-  const uint32_t *tt = toks + (size_t)item * S;
-  auto skey = [kk, tt](int i) -> uint64_t { return ((uint64_t)(uint32_t)kk[i] << 32) | tt[i]; };
+  // sorted key i: 32-bit words at stride 2 (the low halves of the 64-bit
+  // slot keys) or 1 (the item sort's)
+  const uint32_t *kk;
+  const uint32_t *tt;
+  constexpr int ks = ITEM ? 1 : 2;
+  uint32_t kmin = 0u;
+  if constexpr (ITEM) {
+    const uint32_t *reg = sort_ws + (size_t)item * item_words;
+    const size_t fin = reg[0] & 1u, Sa = ItemSort::sa(S);  // the last pass's output
+    kk = reg + ItemSort::keys + fin * Sa;
+    tt = reg + ItemSort::keys + (2 + fin) * Sa;
+    kmin = reg[5];
+  } else {
+    kk = reinterpret_cast<const uint32_t *>(keys + (size_t)item * S);
+    tt = toks + (size_t)item * S;
+  }
+  auto skey = [kk, tt, kmin](int i) -> uint64_t {
+    return ((uint64_t)(kk[ks * i] + kmin) << 32) | tt[i];
+  };
 
   // 4. the cut: whole quads while mass < v_mass, then single tokens; NaN
   // probabilities (sorted last) keep the one-lane chain
@@ -779,7 +1042,7 @@ __global__ __launch_bounds__(kSelThreads) void sparse_cut_kernel(HeadDesc *const
     return __fadd_rn(__fadd_rn(__fadd_rn(key_p(skey(q)), key_p(skey(q + 1))), key_p(skey(q + 2))),
                      key_p(skey(q + 3)));
   };
-  if ((uint32_t)kk[n - 1] == 0xFFFFFFFFu) {
+  if (kk[ks * (n - 1)] + kmin == 0xFFFFFFFFu) {
     float mass = 0.0f;
     int ii = 0;
     bool open = true;  // thread 0: the quad loop has not stopped
@@ -1196,7 +1459,9 @@ int vsum_splits(int n) { return (n + kVChunk - 1) / kVChunk; }
 size_t sparse_workspace_floats(int n_items, const DecodeShape &sh) {
   const int n = sh.max_n > 0 ? sh.max_n : 1;
   size_t f = align64((size_t)n_items * item_stride(n) + (size_t)n_items * vsum_splits(n) * sh.padded);
-  if (n > kSelectInBlock) f += sort_space(n_items < kMaxItems ? n_items : kMaxItems, n).floats;
+  const int cnt = n_items < kMaxItems ? n_items : kMaxItems;
+  if (n > kItemSortMax) f += sort_space(cnt, n).floats;
+  else if (n > kSelectInBlock) f += align64((size_t)cnt * ItemSort::words(n));
   return f;
 }
 
@@ -1266,7 +1531,28 @@ hipError_t launch_decode_sparse(HeadDesc *const *descs, int n_items, const Decod
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (n <= kSelectInBlock) {
-      sparse_select_kernel<<<cnt, kSelThreads, 0, s>>>(dsc, v_mass, w, stride, 0, nullptr, nullptr);
+      sparse_select_kernel<<<cnt, kSelThreads, 0, s>>>(dsc, v_mass, w, stride, 0, nullptr, nullptr,
+                                                       nullptr, 0);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    } else if (n <= kItemSortMax) {
+      // the item sort: keys, up to kRsPasses passes (each returns at once
+      // for items whose key range is shorter), the cut
+      uint32_t *rs = reinterpret_cast<uint32_t *>(sort_base);
+      const size_t iw = ItemSort::words(n);
+      sparse_select_kernel<<<cnt, kSelThreads, 0, s>>>(dsc, v_mass, w, stride, n, nullptr, nullptr,
+                                                       rs, iw);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      const dim3 gp((n + kRsKeys - 1) / kRsKeys, cnt);
+      for (int pass = 0; pass < kRsPasses; ++pass) {
+        sparse_rsort_count_kernel<<<gp, kRsThreads, 0, s>>>(pass, rs, iw, n);
+        sparse_rsort_pass_kernel<<<gp, kRsThreads, 0, s>>>(pass, rs, iw, n);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+      }
+      sparse_cut_kernel<true><<<cnt, kSelThreads, 0, s>>>(dsc, v_mass, w, stride, n, nullptr,
+                                                          nullptr, rs, iw);
       e = hipGetLastError();
       if (e != hipSuccess) return e;
     } else {
@@ -1278,14 +1564,16 @@ hipError_t launch_decode_sparse(HeadDesc *const *descs, int n_items, const Decod
       uint32_t *t_in = reinterpret_cast<uint32_t *>(sort_base + 2 * ss.keys_floats);
       uint32_t *t_out = reinterpret_cast<uint32_t *>(sort_base + 2 * ss.keys_floats + ss.toks_floats);
       void *temp = sort_base + 2 * ss.keys_floats + 2 * ss.toks_floats;
-      sparse_select_kernel<<<cnt, kSelThreads, 0, s>>>(dsc, v_mass, w, stride, n, k_in, t_in);
+      sparse_select_kernel<<<cnt, kSelThreads, 0, s>>>(dsc, v_mass, w, stride, n, k_in, t_in,
+                                                       nullptr, 0);
       e = hipGetLastError();
       if (e != hipSuccess) return e;
       size_t temp_bytes = ss.temp_bytes;
       e = rocprim::radix_sort_pairs(temp, temp_bytes, k_in, k_out, t_in, t_out, (size_t)cnt * n, 0u,
                                     32u + (unsigned)item_bits(cnt), s);
       if (e != hipSuccess) return e;
-      sparse_cut_kernel<<<cnt, kSelThreads, 0, s>>>(dsc, v_mass, w, stride, n, k_out, t_out);
+      sparse_cut_kernel<false><<<cnt, kSelThreads, 0, s>>>(dsc, v_mass, w, stride, n, k_out,
+                                                           t_out, nullptr, 0);
       e = hipGetLastError();
       if (e != hipSuccess) return e;
     }

@@ -7,9 +7,11 @@ vscale_t) / sqrt(p) for selected tokens, 0 otherwise, in ring order) are
 compared with the oracle's, token by token: the selected set must be the same,
 and the weights the same bits.  The cases cover every selection code path:
 the fused one-block kernel (rings up to 3,072 tokens at padded 64/128), the
-in-LDS radix sort of the select kernel (up to 8,192 tokens), and the
-device-wide sort plus cut kernel above that (a wrapped 32,768-token ring),
-at v_mass 0.95 / 0.999 / 0.9999 and with peaked queries.
+in-LDS radix sort of the select kernel (up to 8,192 tokens), the per-item
+multi-block radix sort plus cut kernel above that (up to 65,536 tokens: a
+wrapped 32,768-token ring, exact ties across sort blocks, every probability
+equal) and the device-wide sort beyond, at v_mass 0.95 / 0.999 / 0.9999 and
+with peaked queries.
 """
 import numpy as np
 import pytest
@@ -80,8 +82,9 @@ def test_config1_selection(oracle):
     (64, 3, 2, 3072, 0.9999, 1.0),    # fused at its size limit, 3-bit K
     (64, 4, 2, 5000, 0.95, 6.0),      # in-LDS sort, peaked query
     (128, 2, 3, 8192, 0.999, 1.0),    # in-LDS sort at its size limit
-    (64, 4, 4, 9000, 0.95, 1.0),      # device-wide sort
-    (128, 4, 2, 12000, 0.9999, 3.0),  # device-wide sort, peaked
+    (64, 4, 4, 9000, 0.95, 1.0),      # item sort, 5 blocks a pass
+    (128, 4, 2, 12000, 0.9999, 3.0),  # item sort, peaked
+    (64, 2, 2, 65536, 0.95, 1.0),     # item sort at its size limit
 ])
 def test_selection_paths(oracle, dim, kb, vb, n_tok, v_mass, peak):
     rng = np.random.default_rng(1000 + n_tok)
@@ -101,6 +104,34 @@ def test_wrapped_long_ring_selection(oracle):
     for j in range(2):
         q = rng.standard_normal(128).astype(np.float32)
         check_selection(g, o, q, f"config4 ring q{j}")
+
+
+def test_item_sort_ties(oracle):
+    """Exact ties spread over every sort block: 10,000 tokens whose K rows
+    repeat 97 vectors (equal codes and scales, so equal probabilities), and
+    a zero query, where every probability is equal (no sort pass runs)."""
+    rng = np.random.default_rng(11)
+    n = 10000
+    g = GpuHead(64, 4, 2, n, 23, 0.95, 0)
+    o = oracle.head(64, 4, 2, n, 23, 0.95, 0)
+    base = rng.standard_normal((97, 64)).astype(np.float32)
+    vals = rng.standard_normal((n, 64)).astype(np.float32)
+    for t in range(n):
+        g.append(base[t % 97], vals[t], t)
+        o.append(base[t % 97], vals[t], t)
+    for j in range(2):
+        q = rng.standard_normal(64).astype(np.float32)
+        check_selection(g, o, q, f"repeated keys q{j}")
+    check_selection(g, o, np.zeros(64, np.float32), "zero query")
+
+
+def test_device_wide_sort_selection(oracle):
+    """A ring above the item sort's limit (70,000 tokens) takes the
+    device-wide sort."""
+    rng = np.random.default_rng(70)
+    g, o = fill(64, 2, 2, 70000, 29, 70000, 0.95, oracle, rng)
+    q = rng.standard_normal(64).astype(np.float32)
+    check_selection(g, o, q, "n=70000")
 
 
 def test_student_t_selection(oracle):
