@@ -18,14 +18,18 @@
 // softmax sum.  Exactly equal probabilities are ordered by age here; the
 // reference's std::sort leaves their order unspecified.
 //
-// Kernels: one grid over (token blocks, items) computes the logits; one block
-// per item does softmax, the sort (a stable radix sort in LDS up to 8,192
-// tokens; above, one device-wide rocPRIM radix sort of every item's keys
-// between that kernel and a cut kernel) and the cut, and turns the selection
-// into per-token weights; a grid over (token chunks, items) sums the
-// weighted V rows; one block per item adds the chunks and applies the inverse
-// FWHT.  Short rings (up to 3,072 tokens) run the last three steps in one
-// block per item, at padded 64 the logits too (sparse_fused_kernel).
+// Kernels: one grid over (token blocks, items) computes the logits and the
+// blocks' maxima.  Up to 8,192 tokens, one block per item then does softmax,
+// the sort (a stable radix sort in LDS) and the cut, and turns the selection
+// into per-token weights.  Above, a grid computes the exponentials, one block
+// per item their left-to-right sum and the sort keys, a per-item radix sort
+// over many blocks (up to 65,536 tokens; above, one device-wide rocPRIM
+// sort) orders them, and one block per item takes the cut.  A grid over
+// (token chunks, items) sums the weighted V rows (deriving the weights from
+// the cut above 8,192 tokens); one block per item adds the chunks and
+// applies the inverse FWHT.  Short rings (up to 3,072 tokens) run the last
+// three steps in one block per item, at padded 64 the logits too
+// (sparse_fused_kernel).
 #include <rocprim/device/device_radix_sort.hpp>
 #include <type_traits>
 
@@ -218,6 +222,22 @@ __device__ __forceinline__ float kdot_row(const uint8_t *row, int x, const float
   }
 }
 
+// Logical token t of an n-token ring lives in slot s0 + t (mod cap), with
+// s0 = (head - n) mod cap (attention.cpp:562-563).
+__device__ __forceinline__ int ring_slot(int s0, int t, int cap) {
+  const int s = s0 + t;
+  return s >= cap ? s - cap : s;
+}
+
+// Logits blocks: kThreads threads of kLgPer tokens (token k kThreads + t of
+// the block is thread t's k-th).  Per item the workspace holds the n logits
+// (later the exponentials, then the weights), 1/sum at [n], and from [n + 4]
+// four floats per logits block: the block's maximum logit, then (from the
+// exp kernel) its smallest and largest exponential and a NaN flag.
+constexpr int kLgPer = 1;
+constexpr int kLgTokens = kThreads * kLgPer;
+__host__ __device__ constexpr int lg_blocks(int n) { return (n + kLgTokens - 1) / kLgTokens; }
+
 template <int PT, int KB>
 __global__ __launch_bounds__(kThreads) void sparse_logits_kernel(HeadDesc *const *item_desc,
                                                                  const float *__restrict__ queries,
@@ -226,20 +246,114 @@ __global__ __launch_bounds__(kThreads) void sparse_logits_kernel(HeadDesc *const
                                                                  size_t ws_stride) {
   __shared__ float s_q[kMaxPadded];
   __shared__ float s_cbk[16];
+  __shared__ float s_m[kThreads / 64];
   const int item = blockIdx.y;
   const HeadDesc *d = item_desc[item];
   const int n = d->st.size, cap = d->cap, dim = d->dim, P = d->padded;
-  if ((int)(blockIdx.x * blockDim.x) >= n) return;
-  if (threadIdx.x < (1 << KB)) s_cbk[threadIdx.x] = cbv<KB>(threadIdx.x);
-  rotate_query_exact(s_q, queries + (size_t)item * dim, dim, P, d->signs, inv_sqrt_p, sqrt_p);
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const int slot = (int)(((long long)d->st.head - n + cap + i) % cap);
-  const uint8_t *row = d->k_codes + (size_t)slot * d->k_pb;
-  const int x = slot & kperm_mask(P, KB);
-  const float dot = kdot_row<PT, KB>(row, x, s_q, P, s_cbk);
+  const int i0 = blockIdx.x * kLgTokens;
+  if (i0 >= n) return;
+  const int tid = threadIdx.x;
+  if (tid < (1 << KB)) s_cbk[tid] = cbv<KB>(tid);
+  const int s0 = (int)(((long long)d->st.head - n + cap) % cap);
   const float attn_s = 1.0f / (sqrtf((float)dim) * (float)P);
-  ws[(size_t)item * ws_stride + i] = __fmul_rn(__fmul_rn(dot, attn_s), d->k_scale[slot]);
+  float *lg = ws + (size_t)item * ws_stride;
+  rotate_query_exact(s_q, queries + (size_t)item * dim, dim, P, d->signs, inv_sqrt_p, sqrt_p);
+  // one token at a time (unrolled, the dots would share the query's
+  // registers and spill); the block's maximum with the reference's start
+  // value and NaN-skipping compare (attention.cpp:566), which maxima of
+  // blocks combine the same way
+  float m = -1e30f;
+#pragma unroll 1
+  for (int k = 0; k < kLgPer; ++k) {
+    const int i = i0 + k * kThreads + tid;
+    if (i < n) {
+      const int slot = ring_slot(s0, i, cap);
+      const float dot = kdot_row<PT, KB>(d->k_codes + (size_t)slot * d->k_pb,
+                                         slot & kperm_mask(P, KB), s_q, P, s_cbk);
+      const float l = __fmul_rn(__fmul_rn(dot, attn_s), d->k_scale[slot]);
+      lg[i] = l;
+      if (l > m) m = l;
+    }
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    const float y = __shfl_xor(m, off);
+    if (y > m) m = y;
+  }
+  if ((tid & 63) == 0) s_m[tid >> 6] = m;
+  __syncthreads();
+  if (tid == 0) {
+    for (int w2 = 1; w2 < kThreads / 64; ++w2)
+      if (s_m[w2] > m) m = s_m[w2];
+    lg[n + 4 + 4 * blockIdx.x] = m;
+  }
+}
+
+// Exponentials of rings the select kernel does not sort itself (n >
+// kSelectInBlock): grid (logits blocks, items).  The item's maximum is the
+// maximum of its blocks' maxima; e = expf(l - max) (the reference's libm
+// expf, bit for bit) over the logits; each block records its smallest and
+// largest e and whether any is NaN.
+__global__ __launch_bounds__(kThreads) void sparse_exp_kernel(HeadDesc *const *item_desc, float *ws,
+                                                              size_t ws_stride) {
+  __shared__ float s_r[3][kThreads / 64];
+  const int item = blockIdx.y;
+  const int n = item_desc[item]->st.size;
+  if (n <= kSelectInBlock) return;  // select_small takes the logits
+  const int nb = lg_blocks(n);
+  if ((int)blockIdx.x >= nb) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float *lg = ws + (size_t)item * ws_stride;
+  float *st = lg + n + 4;
+  const int i0 = blockIdx.x * kLgTokens;
+  float lv[kLgPer];
+#pragma unroll
+  for (int k = 0; k < kLgPer; ++k) {
+    const int i = i0 + k * kThreads + tid;
+    lv[k] = i < n ? lg[i] : 0.0f;
+  }
+  float mx = -1e30f;
+  for (int b = tid; b < nb; b += kThreads)
+    if (st[4 * b] > mx) mx = st[4 * b];
+  for (int off = 32; off > 0; off >>= 1) {
+    const float y = __shfl_xor(mx, off);
+    if (y > mx) mx = y;
+  }
+  if (lane == 0) s_r[0][wave] = mx;
+  __syncthreads();
+  for (int w2 = 0; w2 < kThreads / 64; ++w2)
+    if (s_r[0][w2] > mx) mx = s_r[0][w2];
+  float e_lo = __builtin_inff(), e_hi = 0.0f;
+  int nan_e = 0;
+#pragma unroll
+  for (int k = 0; k < kLgPer; ++k) {
+    const int i = i0 + k * kThreads + tid;
+    if (i < n) {
+      const float e = expf_ref(lv[k] - mx);
+      lg[i] = e;
+      nan_e |= e != e;
+      e_lo = fminf(e_lo, e);
+      e_hi = fmaxf(e_hi, e);
+    }
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    e_lo = fminf(e_lo, __shfl_xor(e_lo, off));
+    e_hi = fmaxf(e_hi, __shfl_xor(e_hi, off));
+  }
+  nan_e = __syncthreads_or(nan_e);  // also orders s_r[0]'s reads before the writes below
+  if (lane == 0) {
+    s_r[1][wave] = e_lo;
+    s_r[2][wave] = e_hi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w2 = 0; w2 < kThreads / 64; ++w2) {
+      e_lo = fminf(e_lo, s_r[1][w2]);
+      e_hi = fmaxf(e_hi, s_r[2][w2]);
+    }
+    st[4 * blockIdx.x + 1] = e_lo;
+    st[4 * blockIdx.x + 2] = e_hi;
+    st[4 * blockIdx.x + 3] = nan_e ? 1.0f : 0.0f;
+  }
 }
 
 // Sort key of token i with probability p: unsigned order of the key is the
@@ -327,13 +441,6 @@ __device__ int mass_scan(const float *q, int m, float v_mass, float *mass) {
   }
   *mass = ms;
   return taken;
-}
-
-// Logical token t of an n-token ring lives in slot s0 + t (mod cap), with
-// s0 = (head - n) mod cap (attention.cpp:562-563).
-__device__ __forceinline__ int ring_slot(int s0, int t, int cap) {
-  const int s = s0 + t;
-  return s >= cap ? s - cap : s;
 }
 
 // Shared memory of the select kernel.  The small path (n <= kLdsSort) keeps
@@ -667,13 +774,14 @@ __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, fl
 
 // Sort of rings above kSelectInBlock and up to kItemSortMax tokens: a stable
 // LSD radix sort of each item's 32-bit keys key_hi(p) with the tokens as
-// payload.  The select kernel stores the keys less the item's smallest key,
-// so the digits cover only the bits of the key range: kRsBits a pass, at
-// most 3 passes (keys of probabilities in [0, 1] span less than 2^30; NaN
-// keys are all equal).  Ties keep token order, which is the order make_key
-// gives them.  Pass k is two launches over (blocks of kRsKeys positions) x items.
-// The count kernel: a block counts the pass's digits among its positions and
-// stores them at count[block][digit].  The scatter kernel: a block takes its
+// payload.  The keys are stored less the item's smallest key (which the
+// select kernel finds with 1/sum), so the digits cover only the bits of the
+// key range: kRsBits a pass, at most 3 passes (keys of probabilities in
+// [0, 1] span less than 2^30; NaN keys are all equal).  Ties keep token
+// order, which is the order make_key gives them.  Pass k is two launches
+// over (blocks of kRsKeys positions) x items.  The count kernel (at pass 0
+// it first writes the keys and tokens in token order): a block counts the
+// pass's digits among its positions and stores them at count[block][digit].  The scatter kernel: a block takes its
 // offsets from the item's counts (digits below, then the same digit in
 // blocks before it), ranks its keys stably in LDS (a ballot per digit bit
 // and running per-wave digit counts) and writes each key
@@ -713,14 +821,16 @@ struct RsPass {
   uint32_t *dk, *dtk;        // output keys and tokens
 };
 
+// np: the item's passes; kmin: its smallest key.
 __device__ __forceinline__ bool rs_pass(int pass, uint32_t *sort_ws, size_t item_words, int S,
-                                        RsPass &r) {
-  // one read of the header (the select kernel's): passes 0 for items it
+                                        RsPass &r, int &np, uint32_t &kmin) {
+  // one read of the header (the select kernel's): no tokens for items it
   // sorted itself
   r.reg = sort_ws + (size_t)blockIdx.y * item_words;
   const uint4 h = *reinterpret_cast<const uint4 *>(r.reg);
   const uint4 h1 = *reinterpret_cast<const uint4 *>(r.reg + 4);
-  if (pass >= (int)h.x) return false;
+  np = (int)h.x;
+  kmin = h1.y;
   r.n = (int)h1.z;
   r.G = (r.n + kRsKeys - 1) / kRsKeys;
   if ((int)blockIdx.x >= r.G) return false;
@@ -735,18 +845,42 @@ __device__ __forceinline__ bool rs_pass(int pass, uint32_t *sort_ws, size_t item
 }
 
 // Count kernel of one pass of the item sort (see above): grid (blocks, items).
+// Pass 0 also writes the sort's input: keys key_hi(e inv) less the smallest
+// key and tokens, in token order, from the exponentials and inv at lg[n] of
+// the item's workspace (ws) -- also for an item that takes no pass (every
+// key equal), whose cut reads them as they are.
 __global__ __launch_bounds__(kRsThreads) void sparse_rsort_count_kernel(int pass, uint32_t *sort_ws,
-                                                                        size_t item_words, int S) {
+                                                                        size_t item_words, int S,
+                                                                        const float *ws,
+                                                                        size_t ws_stride) {
   __shared__ uint32_t s_hist[kRsDigits];
   RsPass r;
-  if (!rs_pass(pass, sort_ws, item_words, S, r)) return;
+  int np;
+  uint32_t kmin;
+  if (!rs_pass(pass, sort_ws, item_words, S, r, np, kmin)) return;
   const int b = blockIdx.x, tid = threadIdx.x;
   uint32_t k[kRsRounds];
+  if (pass == 0) {
+    const float *lg = ws + (size_t)blockIdx.y * ws_stride;
+    const float inv = lg[r.n];
+    uint32_t *ka = r.reg + ItemSort::keys, *ta = ka + 2 * ItemSort::sa(S);
 #pragma unroll
-  for (int j = 0; j < kRsRounds; ++j) {
-    const int pos = b * kRsKeys + j * kRsThreads + tid;
-    k[j] = pos < r.n ? r.sk[pos] : 0u;
+    for (int j = 0; j < kRsRounds; ++j) {
+      const int pos = b * kRsKeys + j * kRsThreads + tid;
+      k[j] = pos < r.n ? key_hi(__fmul_rn(lg[pos], inv)) - kmin : 0u;
+      if (pos < r.n) {
+        ka[pos] = k[j];
+        ta[pos] = (uint32_t)pos;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kRsRounds; ++j) {
+      const int pos = b * kRsKeys + j * kRsThreads + tid;
+      k[j] = pos < r.n ? r.sk[pos] : 0u;
+    }
   }
+  if (pass >= np) return;
 #pragma unroll
   for (int j = 0; j < kRsDPT; ++j) s_hist[j * kRsThreads + tid] = 0u;
   __syncthreads();
@@ -773,7 +907,9 @@ __global__ __launch_bounds__(kRsThreads) void sparse_rsort_pass_kernel(int pass,
   __shared__ uint32_t s_off[kRsDigits];
   __shared__ uint32_t s_wsum[NW];
   RsPass rp;
-  if (!rs_pass(pass, sort_ws, item_words, S, rp)) return;
+  int np;
+  uint32_t kmin;
+  if (!rs_pass(pass, sort_ws, item_words, S, rp, np, kmin) || pass >= np) return;
   const int b = blockIdx.x, n = rp.n, sft = rp.sft;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int p0 = b * kRsKeys + wave * 64 * R + lane;  // this lane's position in round 0
@@ -860,17 +996,17 @@ __global__ __launch_bounds__(kRsThreads) void sparse_rsort_pass_kernel(int pass,
   }
 }
 
-// One block of kSelThreads per item: the sparse-V selection as per-token
-// weights.  n <= kSelectInBlock: select_small, all of it.  Larger n (keys != null):
-// the first of three steps.  This kernel takes the max, the exponentials and
-// their left-to-right sum (inv = 1/sum is kept at lg[n]) and writes the sort
-// keys (slot << 32) | key_hi(p), with the token as payload, into the item's
-// slot of S entries in a launch-wide array (padding: key_hi = ~0, after
-// everything); one device-wide stable radix sort of all slots (rocPRIM) puts
-// each item's keys in order inside its slot, p descending, ties older first;
-// sparse_cut_kernel then takes the cut and writes the weights.  Items at or
-// below kSelectInBlock in a launch that sorts fill their slot with padding.
-// sparse_vsum_kernel then sums the weighted V rows over many blocks and
+// One block of kSelThreads per item: the sparse-V selection.  n <=
+// kSelectInBlock: select_small, all of it, as per-token weights.  Larger n:
+// the exponentials (sparse_exp_kernel's) are added left to right (inv =
+// 1/sum is kept at lg[n]) and the sort keys written: for the item sort
+// (sort_ws), key_hi(p) less the smallest key with the tokens, in token order;
+// for the device-wide sort (keys), (slot << 32) | key_hi(p) with the tokens
+// in the item's slot of S entries of a launch-wide array (padding: key_hi =
+// ~0, after everything; items at or below kSelectInBlock fill their slot with
+// padding).  Either sort orders p descending, ties older first;
+// sparse_cut_kernel then takes the cut, sparse_vsum_kernel derives the
+// weights and sums the weighted V rows over many blocks, and
 // sparse_finish_kernel applies the inverse FWHT.  The V sum runs in token
 // order instead of the reference's sorted order, which changes only its
 // rounding; the selected set is the reference's.
@@ -893,7 +1029,10 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
     }
   }
   // items this kernel sorts itself take no item-sort pass
-  if (sort_ws && n <= kSelectInBlock && tid == 0) sort_ws[(size_t)item * item_words] = 0u;
+  if (sort_ws && n <= kSelectInBlock && tid == 0) {
+    sort_ws[(size_t)item * item_words] = 0u;
+    sort_ws[(size_t)item * item_words + 6] = 0u;
+  }
   if (n == 0) return;
   float *lg = ws + (size_t)item * ws_stride;
   const int s0 = (int)(((long long)d->st.head - n + cap) % cap);
@@ -904,29 +1043,19 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
     else select_small<8>(d, v_mass, lg, n, s0, sh);
     return;
   }
-  float *s_stage = sh.stage, *s_red = sh.red, *s_bcast = sh.bcast;
+  float *s_red = sh.red, *s_bcast = sh.bcast;
 
-  // 1. max with the reference's starting value and NaN-skipping compare
-  float mx = -1e30f;
-#pragma unroll 8
-  for (int i = tid; i < n; i += kSelThreads)
-    if (lg[i] > mx) mx = lg[i];
-  s_red[tid] = mx;
-  __syncthreads();
-  for (int w = blockDim.x / 2; w > 0; w >>= 1) {
-    if (tid < w && s_red[tid + w] > s_red[tid]) s_red[tid] = s_red[tid + w];
-    __syncthreads();
-  }
-  mx = s_red[0];
-  __syncthreads();
-
-  // 2. exponentials and their left-to-right sum (a NaN term makes it NaN)
+  // 1-2. the maximum and the exponentials come from the logits and exp
+  // kernels (lg holds the e), each block's NaN flag and e range at st; then
+  // the exponentials' left-to-right sum (a NaN term makes it NaN)
+  const float *st = lg + n + 4;
+  const int nb = lg_blocks(n);
   int nan_e = 0;
-#pragma unroll 8
-  for (int i = tid; i < n; i += kSelThreads) {
-    const float e = expf_ref(lg[i] - mx);
-    lg[i] = e;
-    nan_e |= e != e;
+  float e_lo = __builtin_inff(), e_hi = 0.0f;
+  for (int b = tid; b < nb; b += kSelThreads) {
+    nan_e |= st[4 * b + 3] != 0.0f;
+    e_lo = fminf(e_lo, st[4 * b + 1]);
+    e_hi = fmaxf(e_hi, st[4 * b + 2]);
   }
   if (__syncthreads_or(nan_e)) {
     if (tid == 0) s_bcast[0] = __builtin_nanf("");
@@ -947,19 +1076,11 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
     }
     return;
   }
-  // 3. the item sort's input: keys less the smallest key, tokens in token
-  // order, and the passes the key range needs.  p = e * inv is monotone in
-  // e, so the largest e gives the smallest key and the smallest e the
-  // largest (a NaN inv makes every key 0xFFFFFFFF).
+  // 3. the item sort's header: the passes the key range needs, the smallest
+  // key (the first count kernel writes the keys less it, from lg and inv).
+  // p = e * inv is monotone in e, so the largest e gives the smallest key and
+  // the smallest e the largest (a NaN inv makes every key 0xFFFFFFFF).
   uint32_t *reg = sort_ws + (size_t)item * item_words;
-  uint32_t *k_a = reg + ItemSort::keys, *t_a = k_a + 2 * ItemSort::sa(S);
-  float e_lo = __builtin_inff(), e_hi = 0.0f;
-#pragma unroll 8
-  for (int i = tid; i < n; i += kSelThreads) {
-    const float e = lg[i];
-    e_lo = fminf(e_lo, e);
-    e_hi = fmaxf(e_hi, e);
-  }
   for (int off = 32; off > 0; off >>= 1) {
     e_lo = fminf(e_lo, __shfl_xor(e_lo, off));
     e_hi = fmaxf(e_hi, __shfl_xor(e_hi, off));
@@ -974,11 +1095,6 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
     e_hi = fmaxf(e_hi, s_red[32 + w]);
   }
   const uint32_t kmin = key_hi(__fmul_rn(e_hi, inv)), kmax = key_hi(__fmul_rn(e_lo, inv));
-#pragma unroll 8
-  for (int i = tid; i < n; i += kSelThreads) {
-    k_a[i] = key_hi(__fmul_rn(lg[i], inv)) - kmin;
-    t_a[i] = (uint32_t)i;
-  }
   if (tid == 0) {
     const uint32_t range = kmax - kmin;
     const int bits = range ? 32 - __clz((int)range) : 0;
@@ -989,10 +1105,10 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
   }
 }
 
-// The cut and the weights of an item above kSelectInBlock tokens, over its sorted
-// keys: the item sort's final buffers (sort_ws != null: key_hi and tokens), or
-// the item's slot of the device-wide sort (keys: slot << 32 | key_hi, toks:
-// tokens).
+// The cut of an item above kSelectInBlock tokens, over its sorted keys: the
+// item sort's final buffers (ITEM: key_hi less the smallest key, and tokens),
+// or the item's slot of the device-wide sort (keys: slot << 32 | key_hi,
+// toks: tokens).  sparse_vsum_kernel derives the weights from it.
 template <bool ITEM>
 __global__ __launch_bounds__(kSelThreads) void sparse_cut_kernel(HeadDesc *const *item_desc,
                                                                  float v_mass, float *ws,
@@ -1009,11 +1125,9 @@ __global__ __launch_bounds__(kSelThreads) void sparse_cut_kernel(HeadDesc *const
   const int item = blockIdx.x;
   const int tid = threadIdx.x;
   const HeadDesc *d = item_desc[item];
-  const int n = d->st.size, cap = d->cap, P = d->padded;
+  const int n = d->st.size;
   if (n <= kSelectInBlock) return;  // select_small wrote its weights
   float *lg = ws + (size_t)item * ws_stride;
-  const int s0 = (int)(((long long)d->st.head - n + cap) % cap);
-  const float inv = lg[n];
   // sorted key i: 32-bit words at stride 2 (the low halves of the 64-bit
   // slot keys) or 1 (the item sort's)
   const uint32_t *kk;
@@ -1077,27 +1191,13 @@ __global__ __launch_bounds__(kSelThreads) void sparse_cut_kernel(HeadDesc *const
   const int cut = s_cut;
   const uint64_t last = s_last;
 
-  // 5. per-token weights in natural order: the selection is the cut first
-  // keys of the sorted order, i.e. every key up to the last one taken (keys
-  // are distinct); p_t is recomputed exactly as the key was made
-  const float isp = 1.0f / sqrtf((float)P);
-  constexpr int BT = 8;  // tokens per thread whose loads are in flight together
-  for (int t0 = tid; t0 < n; t0 += BT * kSelThreads) {
-    float lv[BT], vs[BT];
-#pragma unroll
-    for (int j = 0; j < BT; ++j) {
-      const int t = t0 + j * kSelThreads;
-      lv[j] = t < n ? lg[t] : 0.0f;
-      vs[j] = t < n ? d->v_scale[ring_slot(s0, t, cap)] : 0.0f;
-    }
-#pragma unroll
-    for (int j = 0; j < BT; ++j) {
-      const int t = t0 + j * kSelThreads;
-      if (t < n) {
-        const float p = __fmul_rn(lv[j], inv);
-        lg[t] = cut > 0 && make_key(p, t) <= last ? __fmul_rn(__fmul_rn(p, vs[j]), isp) : 0.0f;
-      }
-    }
+  // 5. the selection for sparse_vsum_kernel, which turns it into per-token
+  // weights: the cut first keys of the sorted order, i.e. every key up to
+  // the last one taken (keys are distinct)
+  if (tid == 0) {
+    lg[n + 1] = __uint_as_float(cut > 0 ? 1u : 0u);
+    lg[n + 2] = __uint_as_float((uint32_t)last);
+    lg[n + 3] = __uint_as_float((uint32_t)(last >> 32));
   }
 }
 
@@ -1257,6 +1357,9 @@ struct VUnit {
   static constexpr int bytes = VB == 3 ? 3 : 1;
 };
 
+// Tokens per sparse_vsum_kernel block (at most).
+constexpr int kVChunkMax = 256;
+
 // Weighted V sum of one block's chunk of tokens:
 //   part[item][split][j] = sum over t in the chunk of fma(CB_V[code_tj], w_t, .)
 // with w_t the selection weight (0 for tokens left out).  A row of P codes is
@@ -1267,7 +1370,7 @@ struct VUnit {
 // per lane), else 0 (any size, 4 tokens in flight).
 template <int VB, int PT>
 __global__ __launch_bounds__(kThreads) void sparse_vsum_kernel(HeadDesc *const *item_desc,
-                                                               const float *ws, size_t ws_stride,
+                                                               float *ws, size_t ws_stride,
                                                                int chunk, int n_splits,
                                                                float *partials) {
   constexpr int CPU = VUnit<VB>::codes, UB = VUnit<VB>::bytes;
@@ -1275,14 +1378,26 @@ __global__ __launch_bounds__(kThreads) void sparse_vsum_kernel(HeadDesc *const *
   constexpr int kMaxAcc = PT ? CPU : 16;
   __shared__ float s_cb[16];
   __shared__ float s_red[kThreads / 64][kMaxPadded];
+  __shared__ float s_w[kVChunkMax];  // the chunk's weights
   const int item = blockIdx.y, split = blockIdx.x;
   const HeadDesc *d = item_desc[item];
   const int n = d->st.size, cap = d->cap, P = d->padded, vpb = d->v_pb;
   const int t0 = split * chunk;
   if (t0 >= n) return;
   if (threadIdx.x < (1 << VB)) s_cb[threadIdx.x] = cbv<VB>(threadIdx.x);
-  const float *w = ws + (size_t)item * ws_stride;
+  float *w = ws + (size_t)item * ws_stride;
   const int s0 = (int)(((long long)d->st.head - n + cap) % cap);
+  // rings above kSelectInBlock: w holds the exponentials, and the cut
+  // kernel's selection sits at [n]: 1/sum, whether any token is taken, and
+  // the last sort key taken; the weight (p_t * vscale_t) / sqrt(p) of a
+  // selected token (p_t recomputed exactly as its key was made) is derived
+  // here and written back over its exponential
+  const bool derive = n > kSelectInBlock;
+  const float inv = derive ? w[n] : 1.0f;
+  const bool any = derive && __float_as_uint(w[n + 1]) != 0u;
+  const uint64_t last =
+      derive ? ((uint64_t)__float_as_uint(w[n + 3]) << 32) | __float_as_uint(w[n + 2]) : 0u;
+  const float isp = 1.0f / sqrtf((float)P);
   const int U = (P + CPU - 1) / CPU;
   const int TPI = U < 64 ? 64 / U : 1;
   const int R = U > 64 ? U / 64 : 1;  // units per lane (R * CPU <= kMaxAcc)
@@ -1292,9 +1407,23 @@ __global__ __launch_bounds__(kThreads) void sparse_vsum_kernel(HeadDesc *const *
   float acc[kMaxAcc];
 #pragma unroll
   for (int k = 0; k < kMaxAcc; ++k) acc[k] = 0.0f;
-  __syncthreads();
   const int t_end = t0 + chunk < n ? t0 + chunk : n;
   const uint8_t *vsrc = d->v_codes;
+  // the chunk's weights into LDS, a token a thread (derived once, not by
+  // every lane that reads a unit of the token's row)
+  for (int i = threadIdx.x; i < t_end - t0; i += kThreads) {
+    const int t = t0 + i;
+    float wt = w[t];
+    if (derive) {
+      const float p = __fmul_rn(wt, inv);
+      wt = any && make_key(p, t) <= last
+               ? __fmul_rn(__fmul_rn(p, d->v_scale[ring_slot(s0, t, cap)]), isp)
+               : 0.0f;
+      w[t] = wt;
+    }
+    s_w[i] = wt;
+  }
+  __syncthreads();
   // UNR tokens per step, their weights and code units requested before any
   // is used (rows of weight 0 still load: the step's loads stay in flight
   // together)
@@ -1307,7 +1436,7 @@ __global__ __launch_bounds__(kThreads) void sparse_vsum_kernel(HeadDesc *const *
 #pragma unroll
       for (int j = 0; j < UNR; ++j) {
         const int tj = t + j * step;
-        wt[j] = tj < t_end ? w[tj] : 0.0f;
+        wt[j] = tj < t_end ? s_w[tj - t0] : 0.0f;
         const uint8_t *row = vsrc + (size_t)ring_slot(s0, tj < t_end ? tj : t_end - 1, cap) * vpb;
 #pragma unroll
         for (int r = 0; r < kMaxAcc / CPU; ++r) {
@@ -1416,9 +1545,10 @@ __global__ __launch_bounds__(kThreads) void sparse_finish_kernel(HeadDesc *const
   }
 }
 
-// Per item: the logits, then the probabilities, then the weights (n floats),
-// and 1/sum at [n] for rings that sort outside the select kernel.
-size_t item_stride(int n) { return (size_t)n + 4; }
+// Per item: the logits, then the exponentials, then the weights (n floats),
+// 1/sum at [n] for rings that sort outside the select kernel, and the
+// logits blocks' statistics from [n + 4].
+size_t item_stride(int n) { return (size_t)n + 4 + 4 * (size_t)lg_blocks(n); }
 
 // Items per launch: the grid holds items in one dimension (at most 65,535).
 constexpr int kMaxItems = 65535;
@@ -1452,7 +1582,7 @@ SortSpace sort_space(int cnt, int S) {
 }  // namespace
 
 // Tokens per sparse_vsum_kernel block.
-constexpr int kVChunk = 256;
+constexpr int kVChunk = kVChunkMax;
 
 int vsum_splits(int n) { return (n + kVChunk - 1) / kVChunk; }
 
@@ -1485,7 +1615,7 @@ hipError_t launch_decode_sparse(HeadDesc *const *descs, int n_items, const Decod
     float *out = d_out + (size_t)c0 * sh.dim;
     float *w = ws + (size_t)c0 * stride;
     float *parts = parts_all + (size_t)c0 * splits * sh.padded;
-    const dim3 g1((n + kThreads - 1) / kThreads, cnt);
+    const dim3 g1(lg_blocks(n), cnt);
     if (n <= kFusedMax && (sh.padded == 64 || sh.padded == 128)) {
       // padded 128: the logits kernel's many blocks first, then the rest in
       // one block per item
@@ -1530,6 +1660,11 @@ hipError_t launch_decode_sparse(HeadDesc *const *descs, int n_items, const Decod
 #undef AQ_LOGITS
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    if (n > kSelectInBlock) {
+      sparse_exp_kernel<<<g1, kThreads, 0, s>>>(dsc, w, stride);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
     if (n <= kSelectInBlock) {
       sparse_select_kernel<<<cnt, kSelThreads, 0, s>>>(dsc, v_mass, w, stride, 0, nullptr, nullptr,
                                                        nullptr, 0);
@@ -1546,7 +1681,7 @@ hipError_t launch_decode_sparse(HeadDesc *const *descs, int n_items, const Decod
       if (e != hipSuccess) return e;
       const dim3 gp((n + kRsKeys - 1) / kRsKeys, cnt);
       for (int pass = 0; pass < kRsPasses; ++pass) {
-        sparse_rsort_count_kernel<<<gp, kRsThreads, 0, s>>>(pass, rs, iw, n);
+        sparse_rsort_count_kernel<<<gp, kRsThreads, 0, s>>>(pass, rs, iw, n, w, stride);
         sparse_rsort_pass_kernel<<<gp, kRsThreads, 0, s>>>(pass, rs, iw, n);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
