@@ -238,6 +238,33 @@ constexpr int kLgPer = 1;
 constexpr int kLgTokens = kThreads * kLgPer;
 __host__ __device__ constexpr int lg_blocks(int n) { return (n + kLgTokens - 1) / kLgTokens; }
 
+// The per-item workspace (floats, from lg): the n logits / exponentials /
+// weights and four scalars at [n] (1/sum, then the cut's selection), padded
+// to 16 bytes; kStat floats per logits block (its maximum logit, smallest and
+// largest exponential, NaN flag, then the exponentials' fp64 sum at 4-5);
+// then kSeqTab words per sum chunk (sparse_sum_classify_kernel's segment
+// table).  Rings above kSelectInBlock use all of it.
+constexpr int kStat = 8;
+constexpr int kSeqT = 2;  // terms per thread of a sum chunk (more blocks classify at once)
+constexpr int kSeqChunk = seqsum_detail::kBlock * kSeqT;  // terms per sum chunk
+static_assert(kSeqChunk % kLgTokens == 0, "sum chunks are whole logits blocks");
+// segment table of a chunk, flat (seq_walk_flat): [0] entries m (at most
+// kMaxSeg + 1: the chunk's first kMaxSeg segments, then its remaining terms
+// as one hardware segment), then start[], cls[], inc[], x0[], x1[] of
+// kTabEnt each
+constexpr int kTabEnt = seqsum_detail::kMaxSeg + 1;
+constexpr int kTabStart = 1, kTabCls = kTabStart + kTabEnt, kTabInc = kTabCls + kTabEnt,
+              kTabX0 = kTabInc + kTabEnt, kTabX1 = kTabX0 + kTabEnt,
+              kSeqTab = (kTabX1 + kTabEnt + 3) & ~3;
+// chunks walked together (their terms and concatenated tables staged in LDS)
+constexpr int kSeqWin = 4;
+__host__ __device__ constexpr int seq_chunks(int n) { return (n + kSeqChunk - 1) / kSeqChunk; }
+__host__ __device__ constexpr size_t lg_words(int n) { return ((size_t)n + 4 + 3) & ~(size_t)3; }
+__device__ __forceinline__ float *lg_stats(float *lg, int n) { return lg + lg_words(n); }
+__device__ __forceinline__ uint32_t *lg_tables(float *lg, int n) {
+  return reinterpret_cast<uint32_t *>(lg + lg_words(n) + (size_t)kStat * lg_blocks(n));
+}
+
 template <int PT, int KB>
 __global__ __launch_bounds__(kThreads) void sparse_logits_kernel(HeadDesc *const *item_desc,
                                                                  const float *__restrict__ queries,
@@ -284,7 +311,7 @@ __global__ __launch_bounds__(kThreads) void sparse_logits_kernel(HeadDesc *const
   if (tid == 0) {
     for (int w2 = 1; w2 < kThreads / 64; ++w2)
       if (s_m[w2] > m) m = s_m[w2];
-    lg[n + 4 + 4 * blockIdx.x] = m;
+    lg_stats(lg, n)[kStat * blockIdx.x] = m;
   }
 }
 
@@ -296,6 +323,7 @@ __global__ __launch_bounds__(kThreads) void sparse_logits_kernel(HeadDesc *const
 __global__ __launch_bounds__(kThreads) void sparse_exp_kernel(HeadDesc *const *item_desc, float *ws,
                                                               size_t ws_stride) {
   __shared__ float s_r[3][kThreads / 64];
+  __shared__ double s_d[kThreads / 64];
   const int item = blockIdx.y;
   const int n = item_desc[item]->st.size;
   if (n <= kSelectInBlock) return;  // select_small takes the logits
@@ -303,7 +331,7 @@ __global__ __launch_bounds__(kThreads) void sparse_exp_kernel(HeadDesc *const *i
   if ((int)blockIdx.x >= nb) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   float *lg = ws + (size_t)item * ws_stride;
-  float *st = lg + n + 4;
+  float *st = lg_stats(lg, n);
   const int i0 = blockIdx.x * kLgTokens;
   float lv[kLgPer];
 #pragma unroll
@@ -313,7 +341,7 @@ __global__ __launch_bounds__(kThreads) void sparse_exp_kernel(HeadDesc *const *i
   }
   float mx = -1e30f;
   for (int b = tid; b < nb; b += kThreads)
-    if (st[4 * b] > mx) mx = st[4 * b];
+    if (st[kStat * b] > mx) mx = st[kStat * b];
   for (int off = 32; off > 0; off >>= 1) {
     const float y = __shfl_xor(mx, off);
     if (y > mx) mx = y;
@@ -323,6 +351,7 @@ __global__ __launch_bounds__(kThreads) void sparse_exp_kernel(HeadDesc *const *i
   for (int w2 = 0; w2 < kThreads / 64; ++w2)
     if (s_r[0][w2] > mx) mx = s_r[0][w2];
   float e_lo = __builtin_inff(), e_hi = 0.0f;
+  double esum = 0.0;
   int nan_e = 0;
 #pragma unroll
   for (int k = 0; k < kLgPer; ++k) {
@@ -333,16 +362,19 @@ __global__ __launch_bounds__(kThreads) void sparse_exp_kernel(HeadDesc *const *i
       nan_e |= e != e;
       e_lo = fminf(e_lo, e);
       e_hi = fmaxf(e_hi, e);
+      esum += (double)e;
     }
   }
   for (int off = 32; off > 0; off >>= 1) {
     e_lo = fminf(e_lo, __shfl_xor(e_lo, off));
     e_hi = fmaxf(e_hi, __shfl_xor(e_hi, off));
+    esum += __shfl_xor(esum, off);
   }
   nan_e = __syncthreads_or(nan_e);  // also orders s_r[0]'s reads before the writes below
   if (lane == 0) {
     s_r[1][wave] = e_lo;
     s_r[2][wave] = e_hi;
+    s_d[wave] = esum;
   }
   __syncthreads();
   if (tid == 0) {
@@ -350,9 +382,65 @@ __global__ __launch_bounds__(kThreads) void sparse_exp_kernel(HeadDesc *const *i
       e_lo = fminf(e_lo, s_r[1][w2]);
       e_hi = fmaxf(e_hi, s_r[2][w2]);
     }
-    st[4 * blockIdx.x + 1] = e_lo;
-    st[4 * blockIdx.x + 2] = e_hi;
-    st[4 * blockIdx.x + 3] = nan_e ? 1.0f : 0.0f;
+    double t = 0.0;
+    for (int w2 = 0; w2 < kThreads / 64; ++w2) t += s_d[w2];
+    float *sb = st + kStat * blockIdx.x;
+    sb[1] = e_lo;
+    sb[2] = e_hi;
+    sb[3] = nan_e ? 1.0f : 0.0f;
+    *reinterpret_cast<double *>(sb + 4) = t;
+  }
+}
+
+// The fp64 prediction of the left-to-right sum before each chunk of
+// kSeqChunk exponentials comes from the exp kernel's block sums, so every
+// chunk of a ring is classified at once (seq_classify, one block a chunk,
+// the bound counting the terms since the sum's start) into its segment table;
+// the select kernel then walks the chunks in order with the exact sum.  The
+// walk checks every prediction it uses, so the result is the chain's
+// whatever the tables say.  Grid (chunks, items).
+__global__ __launch_bounds__(kSelThreads) void sparse_sum_classify_kernel(HeadDesc *const *item_desc,
+                                                                          float *ws, size_t ws_stride) {
+  using namespace seqsum_detail;
+  constexpr int T = kSeqT;
+  __shared__ SeqShared sh;
+  __shared__ double s_p[kWaves];
+  const int item = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = item_desc[item]->st.size;
+  if (n <= kSelectInBlock) return;
+  const int c0 = blockIdx.x * kSeqChunk;
+  if (c0 >= n) return;
+  float *lg = ws + (size_t)item * ws_stride;
+  const double *bs = reinterpret_cast<const double *>(lg_stats(lg, n) + 4);  // stride kStat / 2
+  const int j0 = tid * T, cn = n - c0 < kSeqChunk ? n - c0 : kSeqChunk;
+  float x[T];
+#pragma unroll
+  for (int k = 0; k < T; ++k) x[k] = j0 + k < cn ? lg[c0 + j0 + k] : 0.0f;
+  double p = 0.0;
+  for (int b = tid; b < c0 / kLgTokens; b += kSelThreads) p += bs[(size_t)b * (kStat / 2)];
+  for (int off = 32; off > 0; off >>= 1) p += __shfl_xor(p, off);
+  if (lane == 0) s_p[wave] = p;
+  __syncthreads();
+  double P0 = 0.0;
+  for (int w = 0; w < kWaves; ++w) P0 += s_p[w];
+  int cls[T];
+  uint32_t r[T];
+  uint64_t ex;
+  seq_classify<T>(x, cn, c0, P0, c0, sh, cls, r, ex);
+  uint32_t *tab = lg_tables(lg, n) + (size_t)blockIdx.x * kSeqTab;
+  const int ns_all = sh.nseg, ns = ns_all < kMaxSeg ? ns_all : kMaxSeg;
+  const int m = ns + (ns_all > kMaxSeg ? 1 : 0);
+  if (tid == 0) tab[0] = (uint32_t)m;
+  for (int i = tid; i < m; i += kSelThreads) {
+    const int st = sh.seg_start[i];
+    tab[kTabStart + i] = (uint32_t)st;
+    const int c = i < ns ? sh.seg_cls[i] : kUnc;  // past kMaxSeg: the rest, term by term
+    const uint64_t d = i < ns ? sh.seg_r[i + 1] - sh.seg_r[i] : 0u;
+    tab[kTabCls + i] = (uint32_t)c;
+    tab[kTabInc + i] = d >= kTop ? kTop : (uint32_t)d;
+    // a hardware segment's first two terms (it has at least one)
+    tab[kTabX0 + i] = __float_as_uint(c == kUnc ? lg[st] : 0.0f);
+    tab[kTabX1 + i] = __float_as_uint(c == kUnc && st + 1 < n ? lg[st + 1] : 0.0f);
   }
 }
 
@@ -447,9 +535,21 @@ __device__ int mass_scan(const float *q, int m, float v_mass, float *mass) {
 // 32-bit keys, 16-bit token indices and 16 x kSelThreads 16-bit radix counts;
 // the large path keeps its sort keys in the workspace.
 struct SelectShared {
-  uint32_t key[kLdsSort];                 // also the exponentials, as floats
-  uint16_t idx[kLdsSort];
-  uint16_t cnt[16 * kSelThreads];         // cnt[digit * kSelThreads + thread]
+  union {
+    struct {
+      uint32_t key[kLdsSort];          // also the exponentials, as floats
+      uint16_t idx[kLdsSort];
+      uint16_t cnt[16 * kSelThreads];  // cnt[digit * kSelThreads + thread]
+    };
+    // rings above kSelectInBlock: a window's segment list (seq_walk_flat)
+    struct {
+      int w_start[kSeqWin * kTabEnt + 1];
+      int w_cls[kSeqWin * kTabEnt];
+      uint32_t w_inc[kSeqWin * kTabEnt];
+      float w_x0[kSeqWin * kTabEnt];
+      float w_x1[kSeqWin * kTabEnt];
+    };
+  };
   __align__(16) float stage[kStage];
   float red[kSelThreads];
   uint32_t wsum[kSelThreads / 64];
@@ -1048,19 +1148,83 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
   // 1-2. the maximum and the exponentials come from the logits and exp
   // kernels (lg holds the e), each block's NaN flag and e range at st; then
   // the exponentials' left-to-right sum (a NaN term makes it NaN)
-  const float *st = lg + n + 4;
+  const float *st = lg_stats(lg, n);
   const int nb = lg_blocks(n);
   int nan_e = 0;
   float e_lo = __builtin_inff(), e_hi = 0.0f;
   for (int b = tid; b < nb; b += kSelThreads) {
-    nan_e |= st[4 * b + 3] != 0.0f;
-    e_lo = fminf(e_lo, st[4 * b + 1]);
-    e_hi = fmaxf(e_hi, st[4 * b + 2]);
+    nan_e |= st[kStat * b + 3] != 0.0f;
+    e_lo = fminf(e_lo, st[kStat * b + 1]);
+    e_hi = fmaxf(e_hi, st[kStat * b + 2]);
   }
   if (__syncthreads_or(nan_e)) {
     if (tid == 0) s_bcast[0] = __builtin_nanf("");
   } else {
-    const float sv = block_seq_sum<8>([lg](int i) { return lg[i]; }, n, 0.0f, __builtin_inff(), sh.seq).s;
+    // the walk over sparse_sum_classify_kernel's chunk tables, kSeqWin
+    // chunks at a time: their terms and concatenated tables staged in LDS
+    // (the next window's requested before this one's walk)
+    using namespace seqsum_detail;
+    static_assert(kSeqWin * kSeqChunk == kBlock * kMaxT, "a window fills the terms' LDS");
+    constexpr int WT = kSeqWin * kSeqT;  // terms per thread and window
+    float *xs = sh.seq.xs;
+    int *w_start = sh.w_start, *w_cls = sh.w_cls;
+    uint32_t *w_inc = sh.w_inc;
+    float *w_x0 = sh.w_x0, *w_x1 = sh.w_x1;
+    const uint32_t *tabs = lg_tables(lg, n);
+    const int nch = seq_chunks(n);
+    const int j0 = tid * WT;
+    // a window's terms (this thread's) and table entries (entry tid of each
+    // chunk's), returned by value so they stay in registers
+    struct Fetched {
+      float x[WT];
+      uint32_t start[kSeqWin], cls[kSeqWin], inc[kSeqWin], x0[kSeqWin], x1[kSeqWin], m[kSeqWin];
+    };
+    auto fetch = [&](int c) -> Fetched {  // the window starting at chunk c
+      Fetched f;
+      const int w0 = c * kSeqChunk;
+#pragma unroll
+      for (int k = 0; k < WT; ++k) f.x[k] = w0 + j0 + k < n ? lg[w0 + j0 + k] : 0.0f;
+#pragma unroll
+      for (int h = 0; h < kSeqWin; ++h) {
+        const uint32_t *tab = tabs + (size_t)(c + h) * kSeqTab;
+        const bool have = c + h < nch;
+        f.m[h] = have ? tab[0] : 0u;
+        const bool mine = have && tid < kTabEnt;
+        f.start[h] = mine ? tab[kTabStart + tid] : 0u;
+        f.cls[h] = mine ? tab[kTabCls + tid] : 0u;
+        f.inc[h] = mine ? tab[kTabInc + tid] : 0u;
+        f.x0[h] = mine ? tab[kTabX0 + tid] : 0u;
+        f.x1[h] = mine ? tab[kTabX1 + tid] : 0u;
+      }
+      return f;
+    };
+    float sv = 0.0f;
+    Fetched F = fetch(0);
+    for (int c = 0; c < nch; c += kSeqWin) {
+      const int w0 = c * kSeqChunk, wn = n - w0 < kSeqWin * kSeqChunk ? n - w0 : kSeqWin * kSeqChunk;
+#pragma unroll
+      for (int k = 0; k < WT; ++k) xs[j0 + k] = F.x[k];
+      int m = 0;
+#pragma unroll
+      for (int h = 0; h < kSeqWin; ++h) {
+        if (tid < (int)F.m[h]) {
+          w_start[m + tid] = (int)F.start[h];
+          w_cls[m + tid] = (int)F.cls[h];
+          w_inc[m + tid] = F.inc[h];
+          w_x0[m + tid] = __uint_as_float(F.x0[h]);
+          w_x1[m + tid] = __uint_as_float(F.x1[h]);
+        }
+        m += (int)F.m[h];
+      }
+      if (tid == 0) w_start[m] = w0 + wn;
+      __syncthreads();
+      if (c + kSeqWin < nch) F = fetch(c + kSeqWin);
+      sv = seq_walk_flat(xs, w0, wn, w_start, w_cls, w_inc, w_x0, w_x1, m, sv);
+      if (tid == 0) s_bcast[1] = sv;
+      __syncthreads();
+      sv = s_bcast[1];
+      __syncthreads();  // the window's LDS is refilled next
+    }
     if (tid == 0) s_bcast[0] = 1.0f / sv;
   }
   __syncthreads();
@@ -1548,7 +1712,9 @@ __global__ __launch_bounds__(kThreads) void sparse_finish_kernel(HeadDesc *const
 // Per item: the logits, then the exponentials, then the weights (n floats),
 // 1/sum at [n] for rings that sort outside the select kernel, and the
 // logits blocks' statistics from [n + 4].
-size_t item_stride(int n) { return (size_t)n + 4 + 4 * (size_t)lg_blocks(n); }
+size_t item_stride(int n) {
+  return lg_words(n) + (size_t)kStat * lg_blocks(n) + (size_t)kSeqTab * seq_chunks(n);
+}
 
 // Items per launch: the grid holds items in one dimension (at most 65,535).
 constexpr int kMaxItems = 65535;
@@ -1662,6 +1828,7 @@ hipError_t launch_decode_sparse(HeadDesc *const *descs, int n_items, const Decod
     if (e != hipSuccess) return e;
     if (n > kSelectInBlock) {
       sparse_exp_kernel<<<g1, kThreads, 0, s>>>(dsc, w, stride);
+      sparse_sum_classify_kernel<<<dim3(seq_chunks(n), cnt), kSelThreads, 0, s>>>(dsc, w, stride);
       e = hipGetLastError();
       if (e != hipSuccess) return e;
     }
