@@ -180,7 +180,134 @@ static Res model(const std::vector<float> &x, float s, float stop, int T) {
   }
 }
 
+static long long g_gchunks = 0, g_gredo = 0, g_gtail = 0;
+
+// The pre-classified path of the sparse-V softmax sum (sparse.hip:
+// sparse_sum_classify_kernel, then seq_walk_flat in the select kernel), with
+// no stop: chunks of kBlock T terms classified from the fp64 prefix of every
+// term before them (not the exact sum at the chunk) with the bound counting
+// the terms since the sum's start; each chunk's flat list holds its first
+// kMaxSeg segments and then the rest of the chunk as one hardware segment;
+// windows of W chunks are walked together, a failed check redoing the whole
+// window term by term.  bias != 1 scales the prefix, a planted misprediction
+// that the walk's checks must catch (the redo then gives the chain's sum).
+static float model_global(const std::vector<float> &x, int T, int W, double bias = 1.0) {
+  const int n = (int)x.size(), C = kBlock * T;
+  struct Ent {
+    int start, cls;
+    uint32_t inc;
+  };
+  std::vector<std::vector<Ent>> lists;
+  double Pc = 0.0;  // fp64 prefix before the chunk
+  for (int c0 = 0; c0 < n; c0 += C) {
+    const int cn = n - c0 < C ? n - c0 : C;
+    ++g_gchunks;
+    std::vector<int> cls(cn);
+    std::vector<uint32_t> r(cn);
+    double P = Pc * bias;
+    for (int j0 = 0; j0 < cn; j0 += T) {
+      const int nv = cn - j0 < T ? cn - j0 : T;
+      const int jb = c0 + j0;  // terms since the sum's start
+      double loc = 0.0;
+      for (int k = 0; k < nv; ++k) loc += (double)x[c0 + j0 + k];
+      const int u = range_class(P, loc, jb + nv);
+      const int E = u == kUnc ? edge_of(P, loc, jb + nv) : kUnc;
+      const double del = range_del(P, loc, jb + nv);
+      double Pj = P;
+      for (int k = 0; k < nv; ++k) {
+        const float xj = x[c0 + j0 + k];
+        int c;
+        uint32_t rj = 0u;
+        if (u != kUnc) {
+          c = scaled_incr(xj, u, rj) ? u : kUnc;
+        } else if (E != kUnc) {
+          c = split_class(Pj, (double)xj, del, E);
+          if (c != kUnc && !scaled_incr(xj, c, rj)) c = kUnc;
+        } else {
+          c = term_class(Pj, xj, jb + k);
+          if (c != kUnc && !term_incr(xj, c, rj)) c = kUnc;
+        }
+        cls[j0 + k] = c;
+        r[j0 + k] = c == kUnc ? 0u : rj;
+        Pj += (double)xj;
+      }
+      P += loc;
+    }
+    for (int j = 0; j < cn; ++j) Pc += (double)x[c0 + j];  // the true prefix
+    std::vector<Ent> L;
+    int pc = kNoClass;
+    uint64_t R = 0, Rseg = 0;
+    for (int j = 0; j < cn; ++j) {
+      if (cls[j] != pc) {
+        if (!L.empty()) {
+          const uint64_t d = R - Rseg;
+          L.back().inc = d >= kTop ? kTop : (uint32_t)d;
+        }
+        L.push_back({c0 + j, cls[j], 0u});
+        Rseg = R;
+      }
+      pc = cls[j];
+      R += r[j];
+    }
+    {
+      const uint64_t d = R - Rseg;
+      L.back().inc = d >= kTop ? kTop : (uint32_t)d;
+    }
+    if ((int)L.size() > kMaxSeg) {
+      ++g_gtail;
+      const int st = L[kMaxSeg].start;
+      L.resize(kMaxSeg);
+      L.push_back({st, kUnc, 0u});
+    }
+    lists.push_back(L);
+  }
+  float s = 0.0f;
+  for (size_t c = 0; c < lists.size(); c += (size_t)W) {
+    const int w0 = (int)c * C, w1 = std::min(n, (int)(c + W) * C);
+    std::vector<Ent> L;
+    for (size_t h = c; h < c + W && h < lists.size(); ++h) L.insert(L.end(), lists[h].begin(), lists[h].end());
+    uint32_t wb = fbits(s);
+    bool redo = false;
+    for (size_t k = 0; k < L.size(); ++k) {
+      const int end = k + 1 < L.size() ? L[k + 1].start : w1;
+      if (L[k].cls == kUnc) {
+        float w = bfloat(wb);
+        for (int i = L[k].start; i < end; ++i) w = w + x[i];
+        wb = fbits(w);
+        continue;
+      }
+      const bool ok = (wb >> 23) == (uint32_t)(L[k].cls + 150) && (wb & 0x7FFFFFu) + L[k].inc < 0x800000u;
+      if (!ok) redo = true;
+      else wb += L[k].inc;
+    }
+    if (redo) {
+      ++g_gredo;
+      float w = s;
+      for (int i = w0; i < w1; ++i) w = w + x[i];
+      wb = fbits(w);
+    }
+    s = bfloat(wb);
+  }
+  return s;
+}
+
 static long long g_cases = 0, g_bad = 0;
+
+// No stop: the pre-classified path of the softmax sum against the chain.
+static void check_global(const std::vector<float> &x, const char *what) {
+  const Res a = chain(x, 0.0f, INFINITY);
+  for (int T : {2, 8})
+    for (double bias : {1.0, 1.05}) {
+      const float b = model_global(x, T, T == 2 ? 4 : 1, bias);
+      ++g_cases;
+      if (fbits(a.s) != fbits(b)) {
+        if (g_bad < 10)
+          std::printf("MISMATCH (pre-classified) %s n=%zu T=%d bias=%g: chain %a model %a\n", what,
+                      x.size(), T, bias, (double)a.s, (double)b);
+        ++g_bad;
+      }
+    }
+}
 
 static void check(const std::vector<float> &x, float s0, float stop, const char *what) {
   const Res a = chain(x, s0, stop);
@@ -214,6 +341,7 @@ int main() {
         }
         for (int i = 0; i < n; ++i) e[i] = std::exp(l[i] - mx);
         check(e, 0.0f, inf, "softmax sum");
+        check_global(e, "softmax sum");
         const float sv = chain(e, 0.0f, inf).s, inv = 1.0f / sv;
         std::vector<float> p(n);
         for (int i = 0; i < n; ++i) p[i] = e[i] * inv;
@@ -238,28 +366,35 @@ int main() {
       std::vector<float> t(n);
       for (int i = 0; i < n; ++i) t[i] = (float)(1 + (rng() % 3));
       check(t, 16777216.0f, inf, "integers over 2^24");
+      check_global(t, "small integers");
       check(t, 8388608.0f, inf, "integers over 2^23");
       for (int i = 0; i < n; ++i) t[i] = std::ldexp(1.0f, -(int)(rng() % 4));
       check(t, 4194304.0f, inf, "dyadic over 2^22");
       check(t, 0.0f, inf, "dyadic from 0");
+      check_global(t, "dyadic");
       for (int i = 0; i < n; ++i) t[i] = 0.5f + (float)(rng() % 4) * 0.25f;
       check(t, 0.0f, (float)n * 0.6f, "dyadic with a stop");
       // subnormals and zeros
       for (int i = 0; i < n; ++i) t[i] = bfloat((uint32_t)(rng() % 0x800000u));
       check(t, 0.0f, inf, "subnormals");
+      check_global(t, "subnormals");
       for (int i = 0; i < n; ++i) t[i] = (rng() % 3 == 0) ? -0.0f : (rng() % 2 ? 0.0f : 1e-38f);
       check(t, 0.0f, inf, "zeros and -0");
+      check_global(t, "zeros and -0");
       // wide exponent range
       for (int i = 0; i < n; ++i) t[i] = std::ldexp((float)(0.5 + 0.5 * ud(rng)), (int)(rng() % 120) - 60);
       check(t, 0.0f, inf, "wide range");
+      check_global(t, "wide range");
       check(t, 1.0f, 3.0e17f, "wide range with a stop");
       // uniform terms with a non-zero start
       for (int i = 0; i < n; ++i) t[i] = (float)ud(rng);
       check(t, 123.456f, inf, "uniform from 123.456");
+      check_global(t, "uniform");
       check(t, 0.0f, (float)n * 0.25f, "uniform with a stop");
     }
   }
-  std::printf("%lld cases, %lld mismatches, %lld of %lld chunks redone, %lld with a serial tail\n",
-              g_cases, g_bad, g_redo, g_chunks, g_tail);
+  std::printf("%lld cases, %lld mismatches, %lld of %lld chunks redone, %lld with a serial tail; "
+              "pre-classified: %lld windows redone, %lld of %lld chunks past %d segments\n",
+              g_cases, g_bad, g_redo, g_chunks, g_tail, g_gredo, g_gtail, g_gchunks, kMaxSeg);
   return g_bad == 0 ? 0 : 1;
 }
