@@ -1344,10 +1344,14 @@ __global__ __launch_bounds__(kSelThreads) void sparse_cut_kernel(HeadDesc *const
     }
   } else {
     const SeqResult rq = block_seq_sum<8>(quad, n_quads, 0.0f, v_mass, s_seq);
-    const int i1 = 4 * rq.count;
-    const SeqResult rs = block_seq_sum<8>([skey, i1](int i) { return key_p(skey(i1 + i)); }, n - i1,
-                                          rq.s, v_mass, s_seq);
-    if (tid == 0) s_cut = i1 + rs.count;
+    // the single tokens run only after every whole quad, i.e. over the last
+    // n % 4 tokens at most (once the mass reaches v_mass they add nothing)
+    if (tid == 0) {
+      int ii = 4 * rq.count;
+      float mass = rq.s;
+      for (; ii < n && mass < v_mass; ++ii) mass = __fadd_rn(mass, key_p(skey(ii)));
+      s_cut = ii;
+    }
   }
   __syncthreads();
   if (tid == 0) s_last = s_cut > 0 ? skey(s_cut - 1) : 0;
