@@ -18,10 +18,13 @@
 // tiles with an online softmax; a block writes (max, sum, acc[p]) and the
 // finalize kernel merges splits and applies the inverse FWHT.
 //
-// LUT kernel (padded 64 or 128): one lane per token.
+// LUT kernel (padded 64 or 128; 256 with quantised K and V): one lane per
+// token.
 //   K: byte lookup table in LDS, LUT[j][b] = the contribution of code byte j
 //      with value b (2 codes at 4 bits, 4 at 2 bits, a 6-bit code pair at 3
-//      bits), so a token costs one LDS read per code byte.
+//      bits), so a token costs one LDS read per code byte; at padded 256 the
+//      2- and 4-bit table holds nibbles instead (one read per 4 bits of
+//      codes), the byte table being 128 KB there.
 //   V: per-lane accumulators acc[p] in VGPRs, fed from a codebook-only table
 //      (byte -> 4 floats at 2 bits, byte -> 2 floats at 4 bits, 6-bit pair ->
 //      2 floats at 3 bits); reduced across lanes once per block.
@@ -100,7 +103,8 @@ __device__ __forceinline__ uint32_t pair3(const uint32_t *w, int g, int m) {
 // code pair m of group g, 6-bit value v at word (4g + m) * 64 + v.
 template <int P, int KB>
 struct KLut {
-  static constexpr int size = (KB == 4 || KB == 2) ? 256 * 64 : KB == 3 ? (P / 2) * 64 : 1;
+  static constexpr int size = (KB == 4 || KB == 2) ? (P <= 128 ? 256 * 64 : (KB == 4 ? P : P / 2) * 16)
+                              : KB == 3 ? (P / 2) * 64 : 1;
 };
 template <int VB>
 struct VLut {
@@ -229,6 +233,29 @@ __device__ void build_klut_fixed(int32_t *lut, const float *qr, float f) {
     for (int lo = 0; lo < 16; ++lo) lut[(h * 16 + lo) * 64 + j] = (int32_t)(a + b[lo]);
   }
 }
+
+// Fixed-point K table of padded 256 and up (2- and 4-bit codes), one entry
+// per code unit and nibble value: a unit is a 4-bit code, or a pair of 2-bit
+// codes (2u, 2u + 1); byte j of a row holds units 2j (high nibble) and 2j + 1
+// (low nibble).  Entry (u, v) = trunc(f * the unit's contribution qr . CB[v])
+// with f as in build_klut_fixed, at byte (u >> 2) * 256 + v * 16 + (u & 3) * 4:
+// the nibble's own bits, masked with 0xF0, give the register part of the
+// address (v * 16, distinct banks for distinct values), and the unit the
+// instruction's immediate offset.  All lanes look up the same unit at once.
+template <int P, int KB>
+__device__ void build_klut_nib(int32_t *lut, const float *qr, float f) {
+  constexpr int U = KB == 4 ? P : P / 2;
+  for (int e = threadIdx.x; e < U * 16; e += blockDim.x) {
+    const int u = e >> 4, v = e & 15;
+    float c;
+    if constexpr (KB == 4) c = (qr[u] * f) * cbv<4>(v);
+    else c = (qr[2 * u] * f) * cbv<2>(v >> 2) + (qr[2 * u + 1] * f) * cbv<2>(v & 3);
+    lut[((u >> 2) * 16 + v) * 4 + (u & 3)] = (int32_t)c;
+  }
+}
+
+// Byte offset of unit u's row in build_klut_nib's table.
+__host__ __device__ constexpr int nib_off(int u) { return (u >> 2) * 256 + (u & 3) * 4; }
 
 // Codebook tables for V; distinct entries never share an LDS bank.
 // 2-bit: nibble n (two codes) -> float2 at byte 16n; 4-bit: nibble n -> float
@@ -639,7 +666,7 @@ __device__ __forceinline__ void transpose_segments(uint32_t *x) {
 //   4-bit: nibble (1 code)  -> float, 16 entries
 //   3-bit: code             -> float, 8 entries
 template <int P, int KB, int VB, bool RAW>
-__global__ __launch_bounds__(kLutThreads, (KB == 2 || KB == 4) ? 4 : 2) void decode_lut_kernel(
+__global__ __launch_bounds__(kLutThreads, P <= 128 && (KB == 2 || KB == 4) ? 4 : 2) void decode_lut_kernel(
     HeadDesc *const *item_desc, const float *__restrict__ queries, int chunk, int n_splits,
     float *__restrict__ partials, float *__restrict__ outs) {
   constexpr bool KQ = KB != 16;
@@ -708,7 +735,8 @@ __global__ __launch_bounds__(kLutThreads, (KB == 2 || KB == 4) ? 4 : 2) void dec
   // jj = (4i+k) ^ x.  A word xr[i] holds 4*jj for k = 0..3 in its bytes
   // (lx0 = 4x in every byte, XORed with the static part); v_perm joins a code
   // byte b and 4*jj into the table offset b*256 + 4*jj.
-  constexpr bool KPERM = KQ && (KB == 2 || KB == 4);
+  constexpr bool KPERM = KQ && (KB == 2 || KB == 4) && P <= 128;
+  constexpr bool NIB = KQ && (KB == 2 || KB == 4) && P >= 256;  // build_klut_nib's table
   constexpr uint32_t kXMask = (uint32_t)kperm_mask(P, KB);
   const uint32_t lx0 = (4u * ((uint32_t)lane & kXMask)) * 0x01010101u;
   // Row offsets are 32-bit (the host routes rings of 4 GiB and more to the
@@ -725,7 +753,7 @@ __global__ __launch_bounds__(kLutThreads, (KB == 2 || KB == 4) ? 4 : 2) void dec
   load_query<P>(s_q, queries + (size_t)item * dim, dim, KQ, signs);
   // fixed-point scale of the K table (2/4-bit keys): f and 1/f
   __shared__ float s_fix[2];
-  if constexpr (KPERM) {
+  if constexpr (KPERM || NIB) {
     if (threadIdx.x < 64) {
       float a = 0.0f;
 #pragma unroll
@@ -739,7 +767,8 @@ __global__ __launch_bounds__(kLutThreads, (KB == 2 || KB == 4) ? 4 : 2) void dec
       }
     }
     __syncthreads();
-    build_klut_fixed<P, KB>(reinterpret_cast<int32_t *>(s_klut), s_q, s_fix[0]);
+    if constexpr (NIB) build_klut_nib<P, KB>(reinterpret_cast<int32_t *>(s_klut), s_q, s_fix[0]);
+    else build_klut_fixed<P, KB>(reinterpret_cast<int32_t *>(s_klut), s_q, s_fix[0]);
   } else if constexpr (KQ) {
     build_klut<P, KB>(s_klut, s_q);
   }
@@ -751,7 +780,7 @@ __global__ __launch_bounds__(kLutThreads, (KB == 2 || KB == 4) ? 4 : 2) void dec
   // reference's natural-unit logits and expf, bit for bit.
   constexpr float kLog2e = 1.44269504088896340736f;
   const float attn_s = KQ ? kLog2e / (sqrtf((float)dim) * (float)P) : 1.0f / sqrtf((float)dim);
-  const float attn_fix = KPERM ? attn_s * s_fix[1] : attn_s;  // undoes the table's fixed point
+  const float attn_fix = KPERM || NIB ? attn_s * s_fix[1] : attn_s;  // undoes the table's fixed point
   const float isp = VQ ? 1.0f / sqrtf((float)P) : 1.0f;
   const uint32_t vmask = 0xF0u;
   auto wexp = [](float z) -> float {
@@ -772,6 +801,28 @@ __global__ __launch_bounds__(kLutThreads, (KB == 2 || KB == 4) ? 4 : 2) void dec
 #pragma unroll
         for (int m = 0; m < 4; ++m) p4[m] += s_klut[(4 * g + m) * 64 + pair3(kcw, g, m)];
       dot = ((p4[0] + p4[1]) + (p4[2] + p4[3])) * attn_s * kscale;
+    } else if constexpr (NIB) {
+      // two lookups per code byte: the high nibble's offset is the byte
+      // masked with 0xF0, the low nibble's the byte of the word shifted left
+      // by 4, masked the same way (one SDWA and each)
+      const uint8_t *lb = reinterpret_cast<const uint8_t *>(s_klut);
+      int32_t p4[4] = {0, 0, 0, 0};
+#pragma unroll
+      for (int i = 0; i < KW; ++i) {
+        const uint32_t wh = kcw[i], wl = kcw[i] << 4;
+        uint32_t ah[4], al[4];
+        vq_addr<0>(wh, wl, 0xF0u, ah[0], al[0]);
+        vq_addr<1>(wh, wl, 0xF0u, ah[1], al[1]);
+        vq_addr<2>(wh, wl, 0xF0u, ah[2], al[2]);
+        vq_addr<3>(wh, wl, 0xF0u, ah[3], al[3]);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int u = 8 * i + 2 * k;
+          p4[k] = p4[k] + *reinterpret_cast<const int32_t *>(lb + nib_off(u) + ah[k]) +
+                  *reinterpret_cast<const int32_t *>(lb + nib_off(u + 1) + al[k]);
+        }
+      }
+      dot = (float)((p4[0] + p4[1]) + (p4[2] + p4[3])) * (attn_fix * kscale);
     } else if constexpr (KQ) {
       // selector k: byte 0 <- byte k of xr[i], byte 1 <- code byte k, bytes 2-3 <- 0.
       // xr[i] is rebuilt per tile (one XOR each) rather than held in 16
@@ -1252,6 +1303,11 @@ hipError_t dispatch_lut(const DecodeShape &sh, dim3 grid, HeadDesc *const *descs
   }
   if constexpr (RAW) {
     AQ_LUT(16, 16)
+  } else if constexpr (P >= 256) {
+    // quantised K and V only (lut_eligible)
+    AQ_LUT(4, 2) AQ_LUT(4, 3) AQ_LUT(4, 4)
+    AQ_LUT(3, 2) AQ_LUT(3, 3) AQ_LUT(3, 4)
+    AQ_LUT(2, 2) AQ_LUT(2, 3) AQ_LUT(2, 4)
   } else {
     AQ_LUT(4, 2) AQ_LUT(4, 3) AQ_LUT(4, 4) AQ_LUT(4, 16)
     AQ_LUT(3, 2) AQ_LUT(3, 3) AQ_LUT(3, 4) AQ_LUT(3, 16)
@@ -1282,10 +1338,13 @@ hipError_t dispatch_generic(const DecodeShape &sh, dim3 grid, HeadDesc *const *d
   return hipErrorInvalidValue;
 }
 
-// The LUT kernel serves padded 64/128 (raw mirrors only when unpadded);
-// everything else takes the generic kernel.
+// The LUT kernel serves padded 64/128 (raw mirrors only when unpadded) and
+// padded 256 with quantised K and V; everything else takes the generic
+// kernel.
 bool lut_eligible(const DecodeShape &sh) {
-  if (!((sh.padded == 64 || sh.padded == 128) && (!sh.raw || sh.dim == sh.padded))) return false;
+  const bool q256 = sh.padded == 256 && !sh.raw && sh.k_bits != 16 && sh.v_bits != 16;
+  if (!(q256 || ((sh.padded == 64 || sh.padded == 128) && (!sh.raw || sh.dim == sh.padded))))
+    return false;
   // the LUT kernel addresses rows with 32-bit byte offsets
   const long long row = sh.raw ? 4LL * sh.padded
                                : std::max(packed_bytes(sh.padded, sh.k_bits), packed_bytes(sh.padded, sh.v_bits));
@@ -1370,6 +1429,8 @@ hipError_t launch_decode_items(HeadDesc *const *descs, int n_items, const Decode
     if (sh.padded == 64)
       e = raw ? dispatch_lut<64, true>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, d_out, s)
               : dispatch_lut<64, false>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, d_out, s);
+    else if (sh.padded == 256)
+      e = dispatch_lut<256, false>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, d_out, s);
     else
       e = raw ? dispatch_lut<128, true>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, d_out, s)
               : dispatch_lut<128, false>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, d_out, s);

@@ -144,6 +144,18 @@ DECODE_CASES = [
     (96, 4, 2, 256, 300),
     (256, 3, 2, 200, 260),
     (32, 2, 2, 100, 77),
+    # padded 256 through the LUT kernel (nibble K table at 2/4 bits, pair
+    # table at 3 bits), every quantised K/V pair: a wrapped ring over several
+    # splits, a ring shorter than one tile, an unpadded dim
+    (256, 4, 2, 3000, 5000),
+    (256, 4, 3, 300, 300),
+    (256, 4, 4, 100, 40),
+    (256, 2, 2, 700, 700),
+    (256, 2, 3, 500, 600),
+    (256, 2, 4, 256, 256),
+    (256, 3, 3, 512, 512),
+    (256, 3, 4, 1000, 1000),
+    (200, 4, 2, 600, 777),
 ]
 
 
