@@ -1315,10 +1315,17 @@ __global__ __launch_bounds__(kSelThreads) void sparse_cut_kernel(HeadDesc *const
   // 4. the cut: whole quads while mass < v_mass, then single tokens; NaN
   // probabilities (sorted last) keep the one-lane chain
   const int n_quads = n / 4;  // quads with ii + 3 < n
-  auto quad = [skey](int k) {
+  auto quad = [skey, kk, kmin](int k) {
     const int q = 4 * k;
-    return __fadd_rn(__fadd_rn(__fadd_rn(key_p(skey(q)), key_p(skey(q + 1))), key_p(skey(q + 2))),
-                     key_p(skey(q + 3)));
+    if constexpr (ITEM) {
+      // the quad's four keys are adjacent and 16-byte aligned: one load
+      const uint4 h = *reinterpret_cast<const uint4 *>(kk + q);
+      return __fadd_rn(__fadd_rn(__fadd_rn(hi_p(h.x + kmin), hi_p(h.y + kmin)), hi_p(h.z + kmin)),
+                       hi_p(h.w + kmin));
+    } else {
+      return __fadd_rn(__fadd_rn(__fadd_rn(key_p(skey(q)), key_p(skey(q + 1))), key_p(skey(q + 2))),
+                       key_p(skey(q + 3)));
+    }
   };
   if (kk[ks * (n - 1)] + kmin == 0xFFFFFFFFu) {
     float mass = 0.0f;
