@@ -356,9 +356,10 @@ __device__ __forceinline__ void encode_row(const HeadDesc *d, const RingState st
   encode_vec<P, B>(buf, d, side, slot, inv_sqrt_p, sqrt_p, s_q4);
 }
 
-// Three waves per SIMD (168 VGPRs, a few values spilled outside the codec's
-// loops) instead of two at the compiler's own 192-200: measured on config 5's
-// bulk append, K side 1,101 -> 1,030 us, V side 996 -> 988 us.
+// Three waves per SIMD (168 VGPRs: two 64-bit values go to scratch before the
+// codec and come back for the stores after it) instead of two at the
+// compiler's own 192-200: measured on config 5's bulk append, K side 1,101 ->
+// 1,030 us, V side 996 -> 988 us.
 template <int P, int B, bool UNIFORM>
 __global__ __launch_bounds__(128, 3) void append_kernel(HeadDesc *const *descs, int n_ctx,
                                                      int side, const float *__restrict__ src,
