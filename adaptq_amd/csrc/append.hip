@@ -162,14 +162,28 @@ __device__ __forceinline__ void load_wave_rows(const float *wave_rows, int lane,
 // when CLAMP, packed MSB-first into little-endian words
 // (quantizer.cpp:156-209): 4 bits = two codes per byte, high nibble first;
 // 2 bits = four per byte; 3 bits = eight per 24-bit big-endian group.
-template <int P, int B, bool CLAMP>
+// BD (2 bits): buf holds the values before the two scalings and the codes
+// come from quantize_bd2 (thresholds q0 < q1 < q2); the clamp, when CLAMP, is
+// then applied to the codes: a code is a nondecreasing function of the value,
+// so the code of the clamped value is the code clamped to
+// [code(nclip), code(clip)] (passed as cl, ch).
+template <int P, int B, bool CLAMP, bool BD = false>
 __device__ __forceinline__ void pack_codes(const float (&buf)[P], uint32_t (&w)[Row<P, B>::words],
-                                           const Q4Entry *s_q4, float nclip, float clip) {
+                                           const Q4Entry *s_q4, float nclip, float clip,
+                                           float q0 = 0.0f, float q1 = 0.0f, float q2 = 0.0f,
+                                           uint32_t cl = 0u, uint32_t ch = 0u) {
+  static_assert(!BD || B == 2, "b-domain codes for 2 bits");
 #pragma unroll
   for (int i = 0; i < P; ++i) {
-    // the reference's two-sided clamp is the median for finite values
-    const float v = CLAMP ? __builtin_amdgcn_fmed3f(buf[i], nclip, clip) : buf[i];
-    const uint32_t q = B == 4 ? quantize_ss4(v, s_q4) : B == 3 ? quantize_ss3(v) : quantize_ss2(v);
+    uint32_t q;
+    if constexpr (BD) {
+      q = quantize_bd2(buf[i], q0, q1, q2);
+      if constexpr (CLAMP) q = q < cl ? cl : q > ch ? ch : q;
+    } else {
+      // the reference's two-sided clamp is the median for finite values
+      const float v = CLAMP ? __builtin_amdgcn_fmed3f(buf[i], nclip, clip) : buf[i];
+      q = B == 4 ? quantize_ss4(v, s_q4) : B == 3 ? quantize_ss3(v) : quantize_ss2(v);
+    }
     // Bit position of code i inside the little-endian word stream.
     int byte, shift;
     if constexpr (B == 4) {
@@ -204,9 +218,13 @@ __device__ __forceinline__ void pack_codes(const float (&buf)[P], uint32_t (&w)[
 // Encode one vector (P values in buf, zero-padded) of side `side` into ring
 // slot `slot`: the reference's quantize_into (quantizer.cpp:53-137) on the
 // lane's own registers, then the row and its scale leave as whole stores.
-template <int P, int B>
+// BD (2 bits): q0..q2 are the thresholds of the values before the two
+// scalings (quant.hpp, BdThr); a wave whose clamp is inert codes those values
+// and skips the scalings.
+template <int P, int B, bool BD = false>
 __device__ __forceinline__ void encode_vec(float (&buf)[P], const HeadDesc *d, int side, int slot,
-                                           float inv_sqrt_p, float sqrt_p, const Q4Entry *s_q4) {
+                                           float inv_sqrt_p, float sqrt_p, const Q4Entry *s_q4,
+                                           float q0 = 0.0f, float q1 = 0.0f, float q2 = 0.0f) {
   uint8_t *codes = side == 0 ? d->k_codes : d->v_codes;
   float *scales = side == 0 ? d->k_scale : d->v_scale;
 
@@ -246,9 +264,6 @@ __device__ __forceinline__ void encode_vec(float (&buf)[P], const HeadDesc *d, i
         }
       }
     }
-#pragma unroll
-    for (int i = 0; i < P; ++i) buf[i] = __fmul_rn(__fmul_rn(buf[i], inv_sqrt_p), sqrt_p);
-
     // The clamp to +-3 sigma (quantizer.cpp:81-89) can change a code only if
     // clip = 3 sigma is not above the largest threshold (0.9816 / 1.7484 /
     // 2.1476 for 2 / 3 / 4 bits): then every |v| > clip codes as clip does.
@@ -266,18 +281,40 @@ __device__ __forceinline__ void encode_vec(float (&buf)[P], const HeadDesc *d, i
 #pragma unroll
     for (int k = 0; k < Row<P, B>::words; ++k) w[k] = 0u;
     bool nan_row;
-    if (clamp_inert) {
-      // A NaN anywhere in the input reaches every element through the FWHT.
-      nan_row = buf[0] != buf[0];
-      pack_codes<P, B, false>(buf, w, s_q4, 0.0f, 0.0f);
-    } else {
-      float s2 = 0.0f;
+    // A NaN anywhere in the input reaches every element through the FWHT.
+    if constexpr (BD) {
+      // codes of the values before the scalings by 1/sqrt(p) and sqrt(p)
+      if (clamp_inert) {
+        nan_row = buf[0] != buf[0];
+        pack_codes<P, B, false, true>(buf, w, s_q4, 0.0f, 0.0f, q0, q1, q2);
+      } else {
+        float s2 = 0.0f;
 #pragma unroll
-      for (int i = 0; i < P; ++i) s2 = __fadd_rn(s2, __fmul_rn(buf[i], buf[i]));
-      const float sigma = sqrtf(__fadd_rn(s2 / (float)P, 1e-12f));
-      const float clip = __fmul_rn(3.0f, sigma);
-      nan_row = s2 != s2;
-      pack_codes<P, B, true>(buf, w, s_q4, -clip, clip);
+        for (int i = 0; i < P; ++i) {
+          const float v = __fmul_rn(__fmul_rn(buf[i], inv_sqrt_p), sqrt_p);
+          s2 = __fadd_rn(s2, __fmul_rn(v, v));
+        }
+        const float sigma = sqrtf(__fadd_rn(s2 / (float)P, 1e-12f));
+        const float clip = __fmul_rn(3.0f, sigma);
+        nan_row = s2 != s2;
+        pack_codes<P, B, true, true>(buf, w, s_q4, 0.0f, 0.0f, q0, q1, q2, quantize<B>(-clip),
+                                     quantize<B>(clip));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < P; ++i) buf[i] = __fmul_rn(__fmul_rn(buf[i], inv_sqrt_p), sqrt_p);
+      if (clamp_inert) {
+        nan_row = buf[0] != buf[0];
+        pack_codes<P, B, false>(buf, w, s_q4, 0.0f, 0.0f);
+      } else {
+        float s2 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < P; ++i) s2 = __fadd_rn(s2, __fmul_rn(buf[i], buf[i]));
+        const float sigma = sqrtf(__fadd_rn(s2 / (float)P, 1e-12f));
+        const float clip = __fmul_rn(3.0f, sigma);
+        nan_row = s2 != s2;
+        pack_codes<P, B, true>(buf, w, s_q4, -clip, clip);
+      }
     }
     // A NaN row: every code is the NaN code.
     if (nan_row) {
@@ -309,11 +346,12 @@ __device__ __forceinline__ void encode_vec(float (&buf)[P], const HeadDesc *d, i
 // old one, and no commit_kernel follows.
 // Encode token t of context c (ring state st as read before any commit) for
 // one side; the caller has placed the thread on (c, t).
-template <int P, int B, bool UNIFORM>
+template <int P, int B, bool UNIFORM, bool BD = false>
 __device__ __forceinline__ void encode_row(const HeadDesc *d, const RingState st, int c, int t,
                                            int side, const float *__restrict__ src, int n_tok,
                                            int dim, float inv_sqrt_p, float sqrt_p,
-                                           const Q4Entry *s_q4) {
+                                           const Q4Entry *s_q4, float q0 = 0.0f, float q1 = 0.0f,
+                                           float q2 = 0.0f) {
   const int cap = d->cap;
   const float *x = src + ((size_t)c * n_tok + t) * dim;
 
@@ -353,18 +391,24 @@ __device__ __forceinline__ void encode_row(const HeadDesc *d, const RingState st
   }
   if (!write_ring) return;
 
-  encode_vec<P, B>(buf, d, side, slot, inv_sqrt_p, sqrt_p, s_q4);
+  encode_vec<P, B, BD>(buf, d, side, slot, inv_sqrt_p, sqrt_p, s_q4, q0, q1, q2);
 }
 
 // Three waves per SIMD (168 VGPRs: two 64-bit values go to scratch before the
 // codec and come back for the stores after it) instead of two at the
 // compiler's own 192-200: measured on config 5's bulk append, K side 1,101 ->
 // 1,030 us, V side 996 -> 988 us.
+//
+// 2-bit codes come from the values before the two scalings (bd: the
+// thresholds for this launch's inv_sqrt_p and sqrt_p, quant.hpp): two
+// multiplies and the sign-split key fewer per element; measured on config 5's
+// bulk append, V side 988 -> 874 us.
 template <int P, int B, bool UNIFORM>
 __global__ __launch_bounds__(128, 3) void append_kernel(HeadDesc *const *descs, int n_ctx,
                                                      int side, const float *__restrict__ src,
                                                      int n_tok, int dim, float inv_sqrt_p,
-                                                     float sqrt_p, int commit) {
+                                                     float sqrt_p, int commit, BdThr bd) {
+  constexpr bool BD = B == 2;
   // 4-bit codes: the bucket table of quantize_ss4, built before any lane leaves
   __shared__ Q4Entry s_q4[B == 4 ? kQ4Entries : 1];
   if constexpr (B == 4) {
@@ -395,7 +439,8 @@ __global__ __launch_bounds__(128, 3) void append_kernel(HeadDesc *const *descs, 
   if constexpr (UNIFORM) {
     if (t >= n_tok) return;
   }
-  encode_row<P, B, UNIFORM>(d, st, c, t, side, src, n_tok, dim, inv_sqrt_p, sqrt_p, s_q4);
+  encode_row<P, B, UNIFORM, BD>(d, st, c, t, side, src, n_tok, dim, inv_sqrt_p, sqrt_p, s_q4,
+                                bd.q2[0], bd.q2[1], bd.q2[2]);
 }
 
 // Both sides of one token per head in one launch (n_tok == 1, lanes over
@@ -708,6 +753,8 @@ hipError_t launch_side_as(HeadDesc *const *descs, int n_ctx, int side, int bits,
                           int n_tok, int dim, int commit, hipStream_t s) {
   const float sp = sqrtf((float)P);
   const float isp = 1.0f / sp;
+  // the 2-bit thresholds of the values before the scalings, found once
+  static const BdThr bd = bd_thresholds(isp, sp);
   dim3 grid;
   if (U) {
     grid = dim3((unsigned)((n_tok + 127) / 128), (unsigned)n_ctx);
@@ -716,10 +763,10 @@ hipError_t launch_side_as(HeadDesc *const *descs, int n_ctx, int side, int bits,
     grid = dim3((unsigned)((total + 127) / 128));
   }
   switch (bits) {
-    case 2: append_kernel<P, 2, U><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp, commit); break;
-    case 3: append_kernel<P, 3, U><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp, commit); break;
-    case 4: append_kernel<P, 4, U><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp, commit); break;
-    case 16: append_kernel<P, 16, U><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp, commit); break;
+    case 2: append_kernel<P, 2, U><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp, commit, bd); break;
+    case 3: append_kernel<P, 3, U><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp, commit, bd); break;
+    case 4: append_kernel<P, 4, U><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp, commit, bd); break;
+    case 16: append_kernel<P, 16, U><<<grid, 128, 0, s>>>(descs, n_ctx, side, src, n_tok, dim, isp, sp, commit, bd); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

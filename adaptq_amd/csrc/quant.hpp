@@ -142,4 +142,54 @@ AQ_HD inline uint32_t quantize_ss2(float v) {
   return u ^ (x.s & 3u);
 }
 
+// 2-bit codes from the rotated value before its two scalings.  The reference
+// codes v = fl(fl(b * c) * d), c = 1/sqrt(p) and d = sqrt(p) as floats
+// (fwht.cpp:60-66, quantizer.cpp:73-75), with quantize<2>: the count of
+// thresholds t with v >= t.  Rounding is monotone, so v(b) is nondecreasing
+// in b and v >= t holds exactly when b >= alpha_t, the least float b whose v
+// reaches t (for t = 0: the most negative b whose v is -0, as -0 >= 0).
+// BdThr holds alpha_t of the three 2-bit thresholds, ascending, found by
+// bisection over the floats with the same two roundings.  Equality with
+// quantize<2>(v(b)) over every float b is checked on the host
+// (tests/cpp/quant_exhaustive.cpp).
+struct BdThr {
+  float q2[3];
+};
+
+AQ_HD inline uint32_t quantize_bd2(float v, float q0, float q1, float q2) {
+  return (v >= q0 ? 1u : 0u) + (v >= q1 ? 1u : 0u) + (v >= q2 ? 1u : 0u);
+}
+
+// Host: the thresholds for c = 1/sqrt(p), d = sqrt(p) as the launch passes them.
+namespace bd_detail {
+inline float key_float(long long k) {
+  const uint32_t u = k >= 0 ? (uint32_t)k : 0x80000000u | (uint32_t)(-k);
+  float f;
+  __builtin_memcpy(&f, &u, 4);
+  return f;
+}
+inline float scaled(float b, float c, float d) {
+  volatile float y = b * c;  // two roundings, as the reference
+  volatile float v = y * d;
+  return v;
+}
+// least ordered key (k >= 0: bits k; k < 0: -|bits|) whose float f has
+// v(f) >= t; true at +inf since c, d > 0
+inline long long least(float t, float c, float d) {
+  long long lo = -0x7F800000LL, hi = 0x7F800000LL;
+  while (lo < hi) {
+    const long long m = lo + (hi - lo) / 2;
+    if (scaled(key_float(m), c, d) >= t) hi = m;
+    else lo = m + 1;
+  }
+  return lo;
+}
+}  // namespace bd_detail
+
+inline BdThr bd_thresholds(float c, float d) {
+  BdThr b{};
+  for (int j = 0; j < 3; ++j) b.q2[j] = bd_detail::key_float(bd_detail::least(thr<2>(j), c, d));
+  return b;
+}
+
 }  // namespace aq

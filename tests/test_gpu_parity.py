@@ -109,6 +109,77 @@ def test_append_clamp_paths(oracle, dim, kb, vb):
     _ring_equal(g, o)
 
 
+@pytest.mark.parametrize("dim,kb,vb", [(128, 4, 2), (128, 2, 4), (64, 4, 2), (64, 2, 2),
+                                       (32, 4, 4), (96, 4, 2), (128, 3, 2)])
+def test_bulk_append_kernel_rows(oracle, dim, kb, vb):
+    """The lane-per-vector append kernel (a whole-MHA flush of 48 heads x 384
+    tokens, above the one-wave kernel's 16,384 vectors).  It codes 2- and
+    4-bit values before the scalings by 1/sqrt(p) and sqrt(p), against
+    thresholds moved through both roundings, and clamps codes rather than
+    values on the sigma path.  Waves of 64 tokens per head: normal rows; one
+    tiny row among normal ones; rows around the s = 1e-10 bound; single
+    spikes; Hadamard rows far above 3 sigma; rows whose rotation cancels to
+    exact and signed zeros and denormal values (x0 = +-x1 under the head's
+    signs plus one tiny entry), where v = fl(fl(b / sqrt p) * sqrt p) is -0
+    for tiny negative b.  Codes and scales bit-exact for every head."""
+    from adaptq_amd import _lib
+    from golden import inputs as I
+    from gpu_head import err
+    L = _lib.lib
+    print(f"bulk append kernel dim={dim} k{kb}v{vb}", flush=True)
+    H, T, seed = 48, 6 * 64, 1234 + dim
+    rng = np.random.default_rng(dim * 31 + kb * 5 + vb)
+    refs = [oracle.head(dim, kb, vb, T, I.mha_seed(seed, h)) for h in range(H)]
+    K = rng.standard_normal((T, H, dim)).astype(np.float32)
+    V = rng.standard_normal((T, H, dim)).astype(np.float32)
+    tiny = np.array([1e-45, -1e-45, 3e-45, -4e-45, 1e-42, -1e-40, 7e-39, -2e-38, 1e-36,
+                     -1e-30, 0.0, -0.0], np.float32)
+    b = np.sqrt(1e-10 / dim)
+    idx = np.arange(dim)
+    for h in range(H):
+        D = refs[h].signs().astype(np.float32)[:dim]
+        K[64 + h % 64, h] *= np.float32(1e-7)
+        V[64 + (h * 7) % 64, h] *= np.float32(1e-30)
+        K[128:192, h] *= np.float32(b) * np.linspace(0.98, 1.02, 64, dtype=np.float32)[:, None]
+        V[128:192, h] *= np.float32(b) * np.linspace(1.02, 0.98, 64, dtype=np.float32)[:, None]
+        for t in range(192, 256):  # spikes, or Hadamard rows (one value far above 3 sigma)
+            if t % 2:
+                K[t, h] = 0.0
+                V[t, h] = 0.0
+                K[t, h, t % dim] = np.float32(rng.uniform(0.1, 5.0))
+                V[t, h, (3 * t) % dim] = np.float32(-rng.uniform(0.1, 5.0))
+            else:
+                hj = np.array([(-1) ** bin(i & (t % dim)).count("1") for i in idx], np.float32)
+                K[t, h] = D * hj * np.float32(rng.uniform(0.5, 2.0))
+                V[t, h] = D * hj[::-1].copy() * np.float32(-rng.uniform(0.5, 2.0))
+        for t in range(256, T):  # cancellations to zeros and denormals
+            for X, off in ((K, 0), (V, 5)):
+                a = np.float32(rng.uniform(0.5, 2.0)) * (1 if t % 3 else -1)
+                x = np.zeros(dim, np.float32)
+                x[0] = a
+                x[1] = a * D[0] * D[1] * (1 if (t + off) % 4 else -1)
+                x[2] = tiny[(t + off + h) % len(tiny)]
+                if (t + h) % 5 == 0:
+                    x[3:] = np.float32(-0.0)
+                X[t, h] = x
+    m = L.adaptq_mha_create(H, dim, kb, vb, T, seed, 0.0, 0)
+    assert m, err()
+    for t in range(T):
+        assert L.adaptq_mha_append_all(m, _lib.fptr(np.ascontiguousarray(K[t])),
+                                       _lib.fptr(np.ascontiguousarray(V[t])), t) == 0, err()
+        for h in range(H):
+            refs[h].append(K[t, h], V[t, h], t)
+    # the whole-MHA call flushes the staged rows of all heads in one launch
+    q = rng.standard_normal((H, dim)).astype(np.float32)
+    out = np.zeros((H, dim), np.float32)
+    assert L.adaptq_mha_compute_all(m, _lib.fptr(q), _lib.fptr(out)) == T, err()
+    for h in range(H):
+        _ring_equal(GpuHead.wrap(L.adaptq_mha_head(m, h), dim), refs[h])
+    for h in (0, 17, H - 1):
+        assert rel_err(out[h], refs[h].compute(q[h])[0]) <= TOL, h
+    L.adaptq_mha_destroy(m)
+
+
 def test_append_special_values(oracle):
     dim, cap = 64, 32
     rows = [np.zeros(dim, np.float32), np.full(dim, np.nan, np.float32),

@@ -1,9 +1,11 @@
 """The append kernel's quantisers (quantize4_tab and the sign-split
 quantize_ss2/3/4 in adaptq_amd/csrc/quant.hpp) equal the reference's binary
 search (quantize<B>) on every float bit pattern (every finite one for the
-sign-split forms), and the oracle's quantize_fast on a stride of them: the
-header is compiled for the host by tests/cpp/quant_exhaustive.cpp (~10 s on 8
-threads)."""
+sign-split forms), and the oracle's quantize_fast on a stride of them; the
+2-bit quantiser of the values before the scalings (quantize_bd2) equals
+quantize<2> of the twice-rounded scaled value on every finite float for every
+padded size up to 128: the header is compiled for the host by
+tests/cpp/quant_exhaustive.cpp (~50 s on 8 threads)."""
 import os
 import shutil
 import subprocess
