@@ -158,6 +158,15 @@ __device__ __forceinline__ void load_wave_rows(const float *wave_rows, int lane,
   }
 }
 
+// A pointer the caller knows to be equal across the wave, as scalar registers.
+template <class T>
+__device__ __forceinline__ T *wave_uniform(T *p) {
+  const uint64_t u = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+  return reinterpret_cast<T *>(((uint64_t)hi << 32) | lo);
+}
+
 // Codebook indices of the P values in buf (finite), clamped to [nclip, clip]
 // when CLAMP, packed MSB-first into little-endian words
 // (quantizer.cpp:156-209): 4 bits = two codes per byte, high nibble first;
@@ -221,12 +230,19 @@ __device__ __forceinline__ void pack_codes(const float (&buf)[P], uint32_t (&w)[
 // BD (2 bits): q0..q2 are the thresholds of the values before the two
 // scalings (quant.hpp, BdThr); a wave whose clamp is inert codes those values
 // and skips the scalings.
-template <int P, int B, bool BD = false>
+// U: the wave's rows are all of one head, so the ring's base pointers are
+// held in scalar registers across the codec (not in four VGPRs, which the
+// three-wave register budget would spill).
+template <int P, int B, bool BD = false, bool U = false>
 __device__ __forceinline__ void encode_vec(float (&buf)[P], const HeadDesc *d, int side, int slot,
                                            float inv_sqrt_p, float sqrt_p, const Q4Entry *s_q4,
                                            float q0 = 0.0f, float q1 = 0.0f, float q2 = 0.0f) {
   uint8_t *codes = side == 0 ? d->k_codes : d->v_codes;
   float *scales = side == 0 ? d->k_scale : d->v_scale;
+  if constexpr (U) {
+    codes = wave_uniform(codes);
+    scales = wave_uniform(scales);
+  }
 
   if constexpr (B == 16) {
     uint32_t w[Row<P, 16>::words];
@@ -391,7 +407,10 @@ __device__ __forceinline__ void encode_row(const HeadDesc *d, const RingState st
   }
   if (!write_ring) return;
 
-  encode_vec<P, B, BD>(buf, d, side, slot, inv_sqrt_p, sqrt_p, s_q4, q0, q1, q2);
+  // scalar base pointers where the codec would otherwise spill them (4-bit
+  // codes: K side 1,035 -> 1,011 us on config 5; the 2-bit codec fits without)
+  encode_vec<P, B, BD, UNIFORM && B == 4>(buf, d, side, slot, inv_sqrt_p, sqrt_p, s_q4, q0, q1,
+                                           q2);
 }
 
 // Three waves per SIMD (168 VGPRs: two 64-bit values go to scratch before the
