@@ -180,6 +180,49 @@ def test_bulk_append_kernel_rows(oracle, dim, kb, vb):
     L.adaptq_mha_destroy(m)
 
 
+@pytest.mark.parametrize("dim,kb,vb", [(128, 4, 2), (64, 2, 4), (32, 2, 2)])
+def test_bulk_append_lanes_over_heads(oracle, dim, kb, vb):
+    """The lane-per-vector append kernel with fewer than 64 tokens per head
+    (400 heads x 48 tokens: lanes run over (head, token) pairs, so a wave mixes
+    heads): normal rows, tiny rows, and rows whose rotation cancels to zeros
+    and denormal values.  Codes and scales bit-exact for every head."""
+    from adaptq_amd import _lib
+    from golden import inputs as I
+    from gpu_head import err
+    L = _lib.lib
+    print(f"bulk append lanes over heads dim={dim} k{kb}v{vb}", flush=True)
+    H, T, seed = 400, 48, 99 + dim
+    rng = np.random.default_rng(dim * 17 + kb + vb)
+    refs = [oracle.head(dim, kb, vb, T, I.mha_seed(seed, h)) for h in range(H)]
+    K = rng.standard_normal((T, H, dim)).astype(np.float32)
+    V = rng.standard_normal((T, H, dim)).astype(np.float32)
+    tiny = np.array([1e-45, -1e-45, -3e-45, 1e-40, -7e-39, 0.0, -0.0], np.float32)
+    for h in range(0, H, 3):
+        D = refs[h].signs().astype(np.float32)[:dim]
+        for t in range(h % 5, T, 4):
+            for X, off in ((K, 0), (V, 3)):
+                x = np.zeros(dim, np.float32)
+                x[0] = np.float32(rng.uniform(0.5, 2.0))
+                x[1] = x[0] * D[0] * D[1] * (1 if (t + off) % 2 else -1)
+                x[2] = tiny[(t + off + h) % len(tiny)]
+                X[t, h] = x
+        K[(h * 7) % T, h] *= np.float32(1e-7)
+        V[(h * 11) % T, h] *= np.float32(1e-30)
+    m = L.adaptq_mha_create(H, dim, kb, vb, T, seed, 0.0, 0)
+    assert m, err()
+    for t in range(T):
+        assert L.adaptq_mha_append_all(m, _lib.fptr(np.ascontiguousarray(K[t])),
+                                       _lib.fptr(np.ascontiguousarray(V[t])), t) == 0, err()
+        for h in range(H):
+            refs[h].append(K[t, h], V[t, h], t)
+    q = rng.standard_normal((H, dim)).astype(np.float32)
+    out = np.zeros((H, dim), np.float32)
+    assert L.adaptq_mha_compute_all(m, _lib.fptr(q), _lib.fptr(out)) == T, err()
+    for h in range(H):
+        _ring_equal(GpuHead.wrap(L.adaptq_mha_head(m, h), dim), refs[h])
+    L.adaptq_mha_destroy(m)
+
+
 def test_append_special_values(oracle):
     dim, cap = 64, 32
     rows = [np.zeros(dim, np.float32), np.full(dim, np.nan, np.float32),
