@@ -413,10 +413,11 @@ __device__ __forceinline__ void encode_row(const HeadDesc *d, const RingState st
                                            q2);
 }
 
-// Three waves per SIMD (168 VGPRs: two 64-bit values go to scratch before the
-// codec and come back for the stores after it) instead of two at the
-// compiler's own 192-200: measured on config 5's bulk append, K side 1,101 ->
-// 1,030 us, V side 996 -> 988 us.
+// Three waves per SIMD instead of two at the compiler's own 192-200 VGPRs:
+// measured on config 5's bulk append, K side 1,101 -> 1,030 us, V side 996 ->
+// 988 us.  Within the 168-VGPR budget the 4-bit codec keeps one dword in
+// scratch (with its ring pointers in scalar registers) and the 2-bit codec
+// needs 155 VGPRs.
 //
 // 2-bit codes come from the values before the two scalings (bd: the
 // thresholds for this launch's inv_sqrt_p and sqrt_p, quant.hpp): two
