@@ -14,6 +14,9 @@
 // below 2^-4 or from 4 up use the end buckets, which hold no threshold.
 // Equality with quantize<4> over every float is checked on the host
 // (tests/cpp/quant_exhaustive.cpp).
+// quantize_ss2/3/4: the sign-split forms of the append kernels (below).
+// quantize_bd2: 2-bit codes of a value before its scalings by 1/sqrt(p) and
+// sqrt(p), against thresholds moved through both roundings (below).
 #pragma once
 
 #include "codebook.hpp"
