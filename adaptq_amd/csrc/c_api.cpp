@@ -117,6 +117,12 @@ struct DevSync {
   int n_caller = 0;
   int evict = 0;
   void *scratch = nullptr;  // this device's address of the static scratch
+  // Allocation-free decodes share `scratch`: each call's stream waits for the
+  // event recorded after the previous call (static_mu orders the
+  // wait / launch / record sequences of concurrent host threads).
+  std::mutex static_mu;
+  hipEvent_t static_ev = nullptr;
+  bool static_used = false;
 };
 
 DevSync g_dev[kMaxDevices];
@@ -133,16 +139,19 @@ hipError_t ensure_lib(DevSync *d) {
   // blocking (synchronises with the null stream), default priority
   hipError_t e = hipStreamCreateWithFlags(&s, hipStreamDefault);
   if (e != hipSuccess) return e;
-  hipEvent_t ev = nullptr;
+  hipEvent_t ev = nullptr, sev = nullptr;
   e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&sev, hipEventDisableTiming);
   void *sp = nullptr;
   if (e == hipSuccess) e = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));
   if (e != hipSuccess) {
     if (ev) (void)hipEventDestroy(ev);
+    if (sev) (void)hipEventDestroy(sev);
     (void)hipStreamDestroy(s);
     return e;
   }
   d->lib_ev = ev;
+  d->static_ev = sev;
   d->scratch = sp;
   d->lib = s;
   return hipSuccess;
@@ -1603,11 +1612,17 @@ int adaptq_plan_compute_device_static(adaptq_plan_t h, const float *d_queries, f
       !require_pointer(d_outs, fn, "d_outs"))
     return -1;
   Plan *p = static_cast<Plan *>(h);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (capturing(s)) {
+    // the ordering event below cannot be waited on from inside a capture
+    set_errorf(fn, "not supported on a stream under HIP graph capture");
+    return -1;
+  }
   std::lock_guard<std::mutex> gp(p->mu);
   if (!plan_scan(p, fn, false)) return -1;
   DevSync *d = dev_sync(p->device);
   void *ws = d ? d->scratch : nullptr;  // the device's address of `scratch`, set up at creation
-  if (!ws) {
+  if (!ws || !d->static_ev) {
     set_errorf(fn, "the device's static scratch is not set up");
     return -1;
   }
@@ -1622,8 +1637,25 @@ int adaptq_plan_compute_device_static(adaptq_plan_t h, const float *d_queries, f
     return -1;
   }
   DeviceGuard g(p->device);
-  return plan_launch_decode(p, d_queries, d_outs, static_cast<float *>(ws),
-                            static_cast<hipStream_t>(stream), fn);
+  // calls on any stream or thread of this device run one after another on
+  // the device: this call's work waits for the previous call's, and the
+  // next call waits for this one's
+  std::lock_guard<std::mutex> gs(d->static_mu);
+  if (d->static_used && hip_fail(hipStreamWaitEvent(s, d->static_ev, 0), fn)) return -1;
+  const int rc = plan_launch_decode(p, d_queries, d_outs, static_cast<float *>(ws), s, fn);
+  // recorded also after a failed launch sequence, part of which may have run
+  if (hip_fail(hipEventRecord(d->static_ev, s), fn)) return -1;
+  d->static_used = true;
+  return rc;
+}
+
+long long adaptq_plan_workspace_bytes(adaptq_plan_t h) {
+  const char *fn = "adaptq_plan_workspace_bytes";
+  if (!require_handle(h, fn)) return -1;
+  Plan *p = static_cast<Plan *>(h);
+  std::lock_guard<std::mutex> gp(p->mu);
+  if (!plan_scan(p, fn, false)) return -1;
+  return p->mixed ? 0 : (long long)(plan_ws_floats(p) * 4);
 }
 
 int adaptq_plan_compute_device(adaptq_plan_t h, const float *d_queries, float *d_outs,

@@ -1722,9 +1722,12 @@ __global__ __launch_bounds__(kThreads) void sparse_finish_kernel(HeadDesc *const
 
 // Per item: the logits, then the exponentials, then the weights (n floats),
 // 1/sum at [n] for rings that sort outside the select kernel, and the
-// logits blocks' statistics from [n + 4].
+// logits blocks' statistics from [n + 4]; the sum chunks' segment tables
+// only when some ring is longer than kSelectInBlock (the one-block selection
+// of shorter rings sums on one lane and never reads them).
 size_t item_stride(int n) {
-  return lg_words(n) + (size_t)kStat * lg_blocks(n) + (size_t)kSeqTab * seq_chunks(n);
+  return lg_words(n) + (size_t)kStat * lg_blocks(n) +
+         (n > kSelectInBlock ? (size_t)kSeqTab * seq_chunks(n) : 0);
 }
 
 // Items per launch: the grid holds items in one dimension (at most 65,535).

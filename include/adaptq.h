@@ -271,20 +271,34 @@ int adaptq_plan_compute_device(adaptq_plan_t plan, const float *d_queries,
                                float *d_outs, void *stream);
 
 /* Extension, no counterpart in the reference.  For callers that cannot
- * allocate memory during a call (code under HIP graph capture, tight serving
- * loops, harnesses that forbid hipMalloc): adaptq_plan_compute_device with
- * its workspace in a static device array of the library (8 MiB per GPU, held
- * until the process ends) instead of memory the plan allocates.  The call
- * makes no hipMalloc/hipFree or other allocation.  Same results as
- * adaptq_plan_compute_device.  Returns -1 with a message when the decode
- * needs more than 8 MiB of workspace (dense plans need none when a context's
- * ring fits one block per item, about 512 items or more at padded 64/128;
- * sparse-V needs about 4 bytes per cached token per context) or when a
- * context holds staged host appends (flush them first).  Every call on a GPU
- * shares that GPU's array: calls that overlap in time on one GPU (different
- * streams or threads) race and must be serialised by the caller. */
+ * allocate memory during a call (tight serving loops, harnesses that forbid
+ * hipMalloc): adaptq_plan_compute_device with its workspace in a static
+ * device array of the library (8 MiB per GPU, held until the process ends)
+ * instead of memory the plan allocates.  The call makes no hipMalloc/hipFree
+ * or other allocation.  Same results as adaptq_plan_compute_device.  Returns
+ * -1 with a message when the decode needs more than 8 MiB of workspace
+ * (adaptq_plan_workspace_bytes tells), when a context holds staged host
+ * appends (flush them first), or on a stream under HIP graph capture (not
+ * supported).  Every call on a GPU shares that GPU's array; calls from
+ * different streams or threads are ordered on the device, each call's work
+ * waiting for the previous call's (an event per GPU), so they never overlap
+ * on the GPU and give the same results as the allocating form. */
 int adaptq_plan_compute_device_static(adaptq_plan_t plan, const float *d_queries,
                                       float *d_outs, void *stream);
+
+/* Extension, no counterpart in the reference.  The bytes of device workspace
+ * the plan's next decode needs in its current state (0 when it needs none or
+ * when its contexts take different branches): what
+ * adaptq_plan_compute_device allocates and adaptq_plan_compute_device_static
+ * takes from its 8 MiB array.  Dense plans need none when each context's ring
+ * fits one block per item (about 512 contexts or more at padded 64/128), else
+ * (padded + 4) * 4 bytes per context and split; sparse-V plans need about
+ * 4 + 4 * padded / 256 bytes per token of the longest ring per context up to
+ * 8,192 tokens, about 25 + 4 * padded / 256 bytes per token plus 131 KB per
+ * context up to 65,536 tokens, and more for the device-wide sort beyond.
+ * Returns -1 on error (a null handle, or a context with staged host
+ * appends). */
+long long adaptq_plan_workspace_bytes(adaptq_plan_t plan);
 
 #ifdef __cplusplus
 }

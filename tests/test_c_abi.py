@@ -102,6 +102,9 @@ def test_null_handles(lib):
     lib.adaptq_plan_destroy(None)
     assert lib.adaptq_plan_compute_device(None, None, None, None) == -1
     assert lib.adaptq_plan_append_device(None, None, None, 1, 0, None) == -1
+    assert lib.adaptq_plan_compute_device_static(None, None, None, None) == -1
+    assert lib.adaptq_plan_workspace_bytes(None) == -1
+    assert lib.adaptq_last_error() == b"adaptq_plan_workspace_bytes: null handle"
 
 
 def test_error_is_thread_local(lib):

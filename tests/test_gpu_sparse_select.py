@@ -10,8 +10,8 @@ the fused one-block kernel (rings up to 3,072 tokens at padded 64/128), the
 in-LDS radix sort of the select kernel (up to 8,192 tokens), the per-item
 multi-block radix sort plus cut kernel above that (up to 65,536 tokens: a
 wrapped 32,768-token ring, exact ties across sort blocks, every probability
-equal) and the device-wide sort beyond, at v_mass 0.95 / 0.999 / 0.9999 and
-with peaked queries.
+equal) and the device-wide sort beyond (a plain and a wrapped ring), at
+v_mass 0.95 / 0.999 / 0.9999 and with peaked queries.
 """
 import numpy as np
 import pytest
@@ -96,7 +96,7 @@ def test_selection_paths(oracle, dim, kb, vb, n_tok, v_mass, peak):
 
 def test_wrapped_long_ring_selection(oracle):
     """Config 4's ring under Engine defaults (d128 K4/V4, capacity 32,768,
-    40,000 tokens: 7,232 evictions): the device-wide sort over a wrapped
+    40,000 tokens: 7,232 evictions): the per-item radix sort over a wrapped
     ring."""
     rng = np.random.default_rng(7)
     g, o = fill(128, 4, 4, 32768, 7, 40000, 0.95, oracle, rng)
@@ -132,6 +132,16 @@ def test_device_wide_sort_selection(oracle):
     g, o = fill(64, 2, 2, 70000, 29, 70000, 0.95, oracle, rng)
     q = rng.standard_normal(64).astype(np.float32)
     check_selection(g, o, q, "n=70000")
+
+
+def test_device_wide_sort_wrapped_selection(oracle):
+    """A wrapped ring above the item sort's limit (capacity 66,000, 70,000
+    tokens appended: 4,000 evictions) takes the device-wide sort."""
+    rng = np.random.default_rng(66)
+    g, o = fill(64, 4, 2, 66000, 31, 70000, 0.95, oracle, rng)
+    assert g.info()["head"] == o.info()["head"] == 4000
+    q = rng.standard_normal(64).astype(np.float32)
+    check_selection(g, o, q, "cap=66000 n=70000 wrapped")
 
 
 def test_student_t_selection(oracle):
