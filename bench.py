@@ -571,7 +571,15 @@ def secondary(L, last_error, torch, np, stream, reps=20, which=("C1", "C2", "C3"
         ok(L.adaptq_mha_append_all_device(md[0], dp(kd), dp(vd), ntok, 0, sp))
         usd = span(lambda: ok(L.adaptq_mha_compute_all_device(md[0], dp(qd[0]), dp(od[0]), sp)))
         res["C4"] = {
-            "append_40000": rate(app_us, nh * ntok * append_bytes_per_token(128, 128, 4, 4)),
+            # the 7,232 tokens per head that the same call evicts are read but
+            # never coded or stored (a row that is overwritten within the
+            # call is not encoded): bytes = every row read + the survivors'
+            # codes and scales written
+            "append_40000": dict(
+                rate(app_us, nh * (ntok * 8 * 128 + cap * (append_bytes_per_token(128, 128, 4, 4)
+                                                           - 8 * 128))),
+                rows_read_per_head=ntok, rows_encoded_per_head=cap,
+                rows_evicted_in_call_not_encoded_per_head=ntok - cap),
             "queries_64_one_launch": dict(rate(us, nq * per_query), per_query_bytes=per_query),
             "query_1": rate(us1, per_query),
             "query_1_engine_defaults_sparse_v": rate(usd, per_query),
