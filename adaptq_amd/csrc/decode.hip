@@ -877,7 +877,10 @@ __global__ __launch_bounds__(kLutThreads, P <= 128 && (KB == 2 || KB == 4) ? 4 :
     load_row_o<KNB>(k_rows, tn * KNB, kc);
     ksc = k_scale[tn];
   }
-  for (; base < t_end; base += kStride) {
+  // the last tile has no next tile: its V phase runs without the next
+  // tile's loads and K phase (a separate copy keeps the loop branch-free)
+  auto step = [&](auto last_tag) {
+    constexpr bool LAST = decltype(last_tag)::value;
     const bool valid = base + lane < t_end;
 
     // ---- online softmax (wave-uniform reference maximum) ----
@@ -913,12 +916,14 @@ __global__ __launch_bounds__(kLutThreads, P <= 128 && (KB == 2 || KB == 4) ? 4 :
 #pragma unroll
       for (int i = 0; i < VW; ++i) x[i] = vw[i];
       transpose_segments<SPLIT, SW>(x);
+      if constexpr (!LAST) {
       // past the end every lane reads the last row (one line)
       const uint32_t tn = (uint32_t)min(base + kStride + lane, t_end - 1);
       __builtin_amdgcn_s_setprio(2);
       load_row_o<VNB>(v_rows, tn * VNB, vw);
       vsc = v_scale[tn];
       __builtin_amdgcn_s_setprio(0);
+      }
     }
 
     // ---- V phase of this tile, then the K phase of the next ----
@@ -944,6 +949,7 @@ __global__ __launch_bounds__(kLutThreads, P <= 128 && (KB == 2 || KB == 4) ? 4 :
         }
       }
     }
+    if constexpr (!LAST) {
     logit = tile_logit(kc, ksc, base + kStride);
     if constexpr (KQ) {
       const uint32_t tn2 = (uint32_t)min(base + 2 * kStride + lane, t_end - 1);
@@ -952,7 +958,10 @@ __global__ __launch_bounds__(kLutThreads, P <= 128 && (KB == 2 || KB == 4) ? 4 :
       ksc = k_scale[tn2];
       __builtin_amdgcn_s_setprio(0);
     }
-  }
+      }
+  };
+  for (; base + kStride < t_end; base += kStride) step(std::false_type{});
+  if (base < t_end) step(std::true_type{});
 
   // ---- block merge: waves -> one (m, l, acc) ----
   // l_run: every token's e is held by its own lane once.
