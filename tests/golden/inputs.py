@@ -135,3 +135,26 @@ def codec_inputs(dim: int, family: str, n: int = 8) -> np.ndarray:
         x[2] *= np.float32(1e-20)
         x[3, ::2] = -0.0
     return np.ascontiguousarray(x, np.float32)
+
+
+# ------------------------------------------------- sparse-V ties at the cut
+# Rings whose probabilities tie exactly at the mass cut, one per selection
+# path (fused <= 3,072 tokens, in-LDS sort <= 8,192, per-item radix sort <=
+# 65,536, device-wide sort beyond): "zero" decodes a zero query (every
+# logit 0, every probability 1/n); "rep" repeats 97 key vectors (equal codes
+# and scales, so equal probabilities within each group of keys).
+TIE_CASES = [(n, kind) for n in (2048, 5000, 20000, 70000) for kind in ("zero", "rep")]
+TIE_SHAPE = dict(dim=64, k_bits=4, v_bits=2, v_mass=0.95)
+
+
+def tie_inputs(n: int, kind: str):
+    """(K [n][64], V [n][64], q [64], seed of the head's signs)."""
+    rng = np.random.default_rng([6, n, ("zero", "rep").index(kind)])
+    dim = TIE_SHAPE["dim"]
+    if kind == "zero":
+        K = _normal(rng, (n, dim))
+    else:
+        K = _normal(rng, (97, dim))[np.arange(n) % 97]
+    V = _normal(rng, (n, dim))
+    q = np.zeros(dim, np.float32) if kind == "zero" else _normal(rng, (dim,))
+    return np.ascontiguousarray(K), V, q, 1000 + n

@@ -19,6 +19,8 @@ inputs.py that makes them) and the reference's outputs:
   config2.npz        outputs of config 2 (all 24 layers x 14 heads)
   config3.npz        outputs of config 3 at steps 0, 1, 127, 255
   config4.npz        ring state around the wrap point and 8 query outputs
+  ties.npz           sparse-V outputs of inputs.TIE_CASES (probabilities tied
+                     exactly at the mass cut)
 
 Outputs are given for (v_mass, hybrid_thresh) = (0, 0) -- pure packed-KV
 decode -- and (0.95, 512), the Python Engine defaults.
@@ -251,14 +253,28 @@ def gen_config4(r: Ref):
     save("config4.npz", **out)
 
 
+def gen_ties(r: Ref):
+    c = I.TIE_SHAPE
+    out = {}
+    for n, kind in I.TIE_CASES:
+        K, V, q, seed = I.tie_inputs(n, kind)
+        hd = r.head(c["dim"], c["k_bits"], c["v_bits"], n, seed, c["v_mass"], 0)
+        for t in range(n):
+            hd.append(K[t], V[t], t)
+        out[f"out_{kind}{n}"] = hd.compute(q)[0]
+    save("ties.npz", **out)
+
+
 def main():
     if not Ref.available:
         sys.exit("oracle/_ref/libadaptq_ref.so is missing: run `make -C oracle ref` "
                  "(needs /root/reference)")
     r = Ref()
+    only = sys.argv[1:]  # generator names, e.g. gen_ties; default: all
     for fn in (gen_rademacher, gen_fwht, gen_quantize_fast, gen_codec, gen_config1,
-               gen_config2, gen_config3, gen_config4):
-        fn(r)
+               gen_config2, gen_config3, gen_config4, gen_ties):
+        if not only or fn.__name__ in only:
+            fn(r)
 
 
 if __name__ == "__main__":
