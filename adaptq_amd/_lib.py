@@ -71,6 +71,8 @@ SIGNATURES = {
     "adaptq_plan_compute_device_static": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p,
                                                     C.c_void_p]),
     "adaptq_plan_workspace_bytes": (C.c_longlong, [C.c_void_p]),
+    "adaptq_mha_append_compute_all_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,
+                                                       C.c_void_p, C.c_void_p, C.c_void_p]),
 }
 
 FEAT_AVX2, FEAT_HYBRID, FEAT_SPARSE_V, FEAT_HIP = 1, 2, 4, 8

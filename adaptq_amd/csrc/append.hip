@@ -20,6 +20,7 @@
 //   ring insert, mirror                   ring_buffer.cpp:105-119, attention.cpp:338-366
 #include <algorithm>
 
+#include "encode_one.hpp"
 #include "launch.hpp"
 #include "quant.hpp"
 
@@ -92,16 +93,6 @@ struct Row {
   static constexpr int bytes = B == 16 ? 4 * P : (P * B + 7) / 8;
   static constexpr int words = (bytes + 3) / 4;
 };
-
-// The packed word k of a row whose codes are all the NaN code (1 / 3 / 7 for
-// 2 / 3 / 4 bits): 0x55 and 0x77 bytes; 3-bit rows repeat the 24-bit group
-// 011 x 8 = bytes 6D B6 DB.
-template <int B>
-__device__ __forceinline__ uint32_t nan_word(int k) {
-  if constexpr (B == 2) return 0x55555555u;
-  else if constexpr (B == 4) return 0x77777777u;
-  else return k % 3 == 0 ? 0x6DDBB66Du : k % 3 == 1 ? 0xB66DDBB6u : 0xDBB66DDBu;
-}
 
 // The 64 consecutive rows of a wave (P floats each), loaded 64 bytes of a row
 // per group of lanes.  Lanes form 16 groups of 4 members: lane bits 4 and 5
@@ -503,7 +494,6 @@ __global__ __launch_bounds__(128) void append_one_kernel(HeadDesc *const *descs,
                                                          const float *__restrict__ vals, int dim,
                                                          int n_tok, float inv_sqrt_p,
                                                          float sqrt_p) {
-  constexpr int E = P / 64;
   __shared__ Q4Entry s_q4[(KB == 4 || VB == 4) ? kQ4Entries : 1];
   __shared__ __align__(16) float s_sq[2][P];
   __shared__ uint8_t s_code[2][P];
@@ -518,133 +508,8 @@ __global__ __launch_bounds__(128) void append_one_kernel(HeadDesc *const *descs,
   const int cap = d->cap;
   if (n_tok == 1 && threadIdx.x == 0) d->st = ring_after(st, 1, cap, d->hyb);
   const float *x = (side == 0 ? keys : vals) + ((size_t)c * n_tok + t) * dim;
-  if (t < mirror_count(st, n_tok, cap, d->hyb)) {
-    float *m = (side == 0 ? d->raw_k : d->raw_v) + (size_t)(st.raw_count + t) * dim;
-    for (int i = lane; i < dim; i += 64) m[i] = x[i];
-  }
-  if (cap <= 0 || t < n_tok - cap) return;  // overwritten within this append
-  const int slot = (int)(((long long)st.head + t) % cap);
-  float v[E];
-#pragma unroll
-  for (int e = 0; e < E; ++e) v[e] = lane + 64 * e < dim ? x[lane + 64 * e] : 0.0f;
-  const int B = side == 0 ? KB : VB;
-  uint8_t *codes = side == 0 ? d->k_codes : d->v_codes;
-  float *scales = side == 0 ? d->k_scale : d->v_scale;
-  auto seq_sumsq = [&](const float (&u)[E]) {
-    // left to right over the P squares (every lane runs the same chain)
-#pragma unroll
-    for (int e = 0; e < E; ++e) s_sq[side][lane + 64 * e] = __fmul_rn(u[e], u[e]);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const float4 *q4 = reinterpret_cast<const float4 *>(s_sq[side]);
-    float acc = 0.0f;
-#pragma unroll
-    for (int b = 0; b < P / 16; ++b) {
-      float4 r[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) r[k] = q4[4 * b + k];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        acc = __fadd_rn(acc, r[k].x);
-        acc = __fadd_rn(acc, r[k].y);
-        acc = __fadd_rn(acc, r[k].z);
-        acc = __fadd_rn(acc, r[k].w);
-      }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();  // s_sq is read by every lane before it is rewritten
-    return acc;
-  };
-  if (B == 16) {
-    float *row = reinterpret_cast<float *>(codes + (size_t)slot * 4 * P);
-#pragma unroll
-    for (int e = 0; e < E; ++e) row[lane + 64 * e] = v[e];
-    if (lane == 0) scales[slot] = 1.0f;
-    return;
-  }
-  const float s = seq_sumsq(v);
-  const float norm = sqrtf(__fadd_rn(s, 1e-12f));
-  const float inv = 1.0f / norm;
-#pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const int i = lane + 64 * e;
-    const uint32_t flip = (~d->signs[i >> 5] >> (i & 31)) << 31;
-    v[e] = __uint_as_float(__float_as_uint(__fmul_rn(v[e], inv)) ^ flip);
-  }
-#pragma unroll
-  for (int len = 1; len < 64 && len < P; len <<= 1) {
-    const bool upper = (lane & len) != 0;
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const float o = __shfl_xor(v[e], len, 64);
-      v[e] = upper ? __fsub_rn(o, v[e]) : __fadd_rn(v[e], o);
-    }
-  }
-  if constexpr (E == 2) {
-    const float lo = v[0], hi = v[1];
-    v[0] = __fadd_rn(lo, hi);
-    v[1] = __fsub_rn(lo, hi);
-  }
-#pragma unroll
-  for (int e = 0; e < E; ++e) v[e] = __fmul_rn(__fmul_rn(v[e], inv_sqrt_p), sqrt_p);
-  // the clamp (see encode_vec): inert when s >= 1e-10
-  bool nan_row;
-  if (s >= 1e-10f) {
-    nan_row = __shfl(v[0], 0, 64) != __shfl(v[0], 0, 64);
-  } else {
-    const float s2 = seq_sumsq(v);
-    const float sigma = sqrtf(__fadd_rn(s2 / (float)P, 1e-12f));
-    const float clip = __fmul_rn(3.0f, sigma);
-#pragma unroll
-    for (int e = 0; e < E; ++e) v[e] = __builtin_amdgcn_fmed3f(v[e], -clip, clip);
-    nan_row = s2 != s2;
-  }
-#pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const uint32_t q = B == 4 ? quantize_ss4(v[e], s_q4) : B == 3 ? quantize_ss3(v[e]) : quantize_ss2(v[e]);
-    s_code[side][lane + 64 * e] = (uint8_t)q;
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  const int nw = P * B / 32;  // words of the row
-  if (lane < nw) {
-    const uint8_t *cd = s_code[side];
-    uint32_t w = 0u;
-    if (nan_row) {
-      w = B == 2 ? nan_word<2>(lane) : B == 4 ? nan_word<4>(lane) : nan_word<3>(lane);
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int b = 4 * lane + j;  // byte b of the row, MSB-first codes
-        uint32_t byte;
-        if (B == 4) {
-          byte = ((uint32_t)cd[2 * b] << 4) | cd[2 * b + 1];
-        } else if (B == 2) {
-          byte = ((uint32_t)cd[4 * b] << 6) | ((uint32_t)cd[4 * b + 1] << 4) |
-                 ((uint32_t)cd[4 * b + 2] << 2) | cd[4 * b + 3];
-        } else {
-          const int g = b / 3;  // 24-bit big-endian group of 8 codes
-          uint32_t grp = 0u;
-#pragma unroll
-          for (int k = 0; k < 8; ++k) grp |= (uint32_t)cd[8 * g + k] << (21 - 3 * k);
-          byte = (grp >> (16 - 8 * (b % 3))) & 255u;
-        }
-        w |= byte << (8 * j);
-      }
-    }
-    uint32_t *row = reinterpret_cast<uint32_t *>(codes + (size_t)slot * (P * B / 8));
-    const uint32_t xm = side == 0 ? (uint32_t)kperm_mask(P, B) : 0u;
-    if (xm != 0u) {
-      // the K row's XOR byte order (kperm_mask): word i, bytes permuted by x & 3, at i ^ (x >> 2)
-      const uint32_t xx = (uint32_t)slot & xm;
-      row[(uint32_t)lane ^ (xx >> 2)] = __builtin_amdgcn_perm(0u, w, 0x03020100u ^ ((xx & 3u) * 0x01010101u));
-    } else {
-      row[lane] = w;
-    }
-  }
-  if (lane == 0) scales[slot] = norm;
+  encode_one_row<P, KB, VB>(d, st, n_tok, t, x, dim, side, lane, inv_sqrt_p, sqrt_p, s_q4,
+                            s_sq[side], s_code[side], nullptr, nullptr);
 }
 
 // Same codec for padded dimensions above 128: identical float steps in the

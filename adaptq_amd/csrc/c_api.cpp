@@ -602,16 +602,85 @@ void append_locked(Ctx *c, const float *key, const float *val) {
 
 enum class Mode { Dense, Hybrid, Sparse };
 
-Mode mode_of(const Ctx *c) {
-  const int n = c->st.size;
-  if (c->hyb > 0 && n <= c->hyb && c->st.raw_count == n) return Mode::Hybrid;
+// The branch a context with ring state st takes (attention.cpp:480-660).
+Mode mode_at(const Ctx *c, const aq::RingState &st) {
+  const int n = st.size;
+  if (c->hyb > 0 && n <= c->hyb && st.raw_count == n) return Mode::Hybrid;
   if (c->v_mass > 0.0f && c->k_bits != 16 && c->v_bits != 16) return Mode::Sparse;
   return Mode::Dense;
+}
+
+Mode mode_of(const Ctx *c) { return mode_at(c, c->st); }
+
+// The shape of a dense decode step over contexts like c whose rings hold n
+// tokens after the step's append, when one fused launch takes it.
+bool step_shape(const Ctx *c, int n_items, int n_after, aq::DecodeShape *sh) {
+  *sh = aq::DecodeShape{c->dim, c->padded, c->k_bits, c->v_bits, false, n_after};
+  return c->cap > 0 && aq::decode_step_supported(n_items, *sh);
+}
+
+aq::StepAppend step_rows(const Ctx *c, const float *k, const float *v) {
+  const float sp = sqrtf((float)c->padded);  // as launch_append passes them
+  return aq::StepAppend{k, v, 1.0f / sp, sp};
+}
+
+// The item list of nq decodes of context c (caller holds c->mu).
+bool ensure_items(Ctx *c, int nq, const char *fn) {
+  if (nq <= c->items_uploaded) return true;
+  if (hip_fail(c->d_items.ensure(sizeof(void *) * (size_t)nq), fn)) return false;
+  std::vector<aq::HeadDesc *> items((size_t)nq, c->d_desc);
+  if (hip_fail(hipMemcpy(c->d_items.p, items.data(), sizeof(void *) * nq, hipMemcpyHostToDevice), fn))
+    return false;
+  c->items_uploaded = nq;
+  return true;
+}
+
+// One staged token and one query, the reference's per-step calls
+// (attention.cpp:338-366 then :480-660): append and decode in one launch
+// (launch_decode_step) when the step is a dense decode the fused kernel
+// takes (caller holds c->mu).  Returns -2, having changed nothing, when it
+// is not; the ring size, or -1 on error, otherwise.
+int step_locked(Ctx *c, const float *query, float *out, const char *fn) {
+  const aq::RingState after = aq::ring_after(c->st, 1, c->cap, c->hyb);
+  aq::DecodeShape sh;
+  if (mode_at(c, after) != Mode::Dense || !step_shape(c, 1, after.size, &sh)) return -2;
+  DeviceGuard g(c->device);
+  if (hip_fail(lib_wait(c->device, c->stage_seq), fn)) return -1;  // pinned rows reused
+  const size_t d = (size_t)c->dim;
+  const size_t io = align256(d * 4);
+  if (hip_fail(c->h_stage.ensure(2 * d * 4), fn) || hip_fail(c->h_io.ensure(2 * io), fn) ||
+      !ensure_items(c, 1, fn))
+    return -1;
+  float *pk = static_cast<float *>(c->h_stage.p);
+  std::memcpy(pk, c->stage_k.data(), d * 4);
+  std::memcpy(pk + d, c->stage_v.data(), d * 4);
+  const float *dk = static_cast<const float *>(c->h_stage.dp);
+  std::memcpy(c->h_io.p, query, d * 4);
+  const float *dq = static_cast<const float *>(c->h_io.dp);
+  float *dout = reinterpret_cast<float *>(static_cast<uint8_t *>(c->h_io.dp) + io);
+  hipStream_t s;
+  hipError_t e = lib_begin(c->device, &s);
+  if (e == hipSuccess)
+    e = aq::launch_decode_step(static_cast<aq::HeadDesc **>(c->d_items.p), 1, sh,
+                               step_rows(c, dk, dk + d), dq, dout, s);
+  if (hip_fail(e, fn)) return -1;
+  c->stage_seq = lib_end(c->device);
+  c->st = after;
+  c->staged = 0;
+  c->stage_k.clear();
+  c->stage_v.clear();
+  if (hip_fail(lib_wait(c->device, c->stage_seq), fn)) return -1;
+  std::memcpy(out, static_cast<uint8_t *>(c->h_io.p) + io, d * 4);
+  return after.size;
 }
 
 // Synchronous decode of nq queries against one head (caller holds c->mu).
 // Queries and outputs pass through pinned memory the kernels read and write.
 int compute_locked(Ctx *c, const float *queries, int nq, float *outs, const char *fn) {
+  if (nq == 1 && c->staged == 1) {
+    const int r = step_locked(c, queries, outs, fn);
+    if (r != -2) return r;
+  }
   if (!flush_locked(c, fn)) return -1;
   const int n = c->st.size;
   if (n == 0) {
@@ -623,13 +692,7 @@ int compute_locked(Ctx *c, const float *queries, int nq, float *outs, const char
   aq::DecodeShape sh{c->dim, c->padded, c->k_bits, c->v_bits, mode == Mode::Hybrid, n};
   const size_t io = align256((size_t)nq * c->dim * 4);
   if (hip_fail(c->h_io.ensure(2 * io), fn)) return -1;  // no kernel uses it between calls
-  if (nq > c->items_uploaded) {
-    if (hip_fail(c->d_items.ensure(sizeof(void *) * (size_t)nq), fn)) return -1;
-    std::vector<aq::HeadDesc *> items((size_t)nq, c->d_desc);
-    if (hip_fail(hipMemcpy(c->d_items.p, items.data(), sizeof(void *) * nq, hipMemcpyHostToDevice), fn))
-      return -1;
-    c->items_uploaded = nq;
-  }
+  if (!ensure_items(c, nq, fn)) return -1;
   const size_t wsf = mode == Mode::Sparse ? aq::sparse_workspace_floats(nq, sh)
                                           : aq::decode_multi_workspace_floats(nq, 1, sh);
   if (hip_fail(c->d_ws.ensure(wsf * 4), fn)) return -1;
@@ -860,6 +923,31 @@ int launch_all_locked(Mha *m, const float *dq, float *dout, hipStream_t s, const
                                 static_cast<float *>(m->d_ws.p), s);
   if (hip_fail(e, fn)) return -1;
   return n;
+}
+
+// A decode step over every head of an MHA whose heads each take one token
+// (rows k, v [n_heads][dim], device or pinned memory) and one query: one
+// fused launch (launch_decode_step) when every head's ring holds the same
+// number of tokens after the append and the step is a dense decode the fused
+// kernel takes (caller holds all head locks, nothing staged).  Returns -2,
+// having launched nothing, when it is not; the common ring size, or -1.
+int step_all_locked(Mha *m, const float *dk, const float *dv, const float *dq, float *dout,
+                    hipStream_t s, const char *fn) {
+  const Ctx *c0 = m->heads[0];
+  const aq::RingState a0 = aq::ring_after(c0->st, 1, c0->cap, c0->hyb);
+  for (const Ctx *c : m->heads) {
+    const aq::RingState a = aq::ring_after(c->st, 1, c->cap, c->hyb);
+    if (c->staged != 0 || a.size != a0.size || mode_at(c, a) != Mode::Dense) return -2;
+  }
+  aq::DecodeShape sh;
+  if (!step_shape(c0, m->n_heads, a0.size, &sh)) return -2;
+  if (hip_fail(aq::launch_decode_step(static_cast<aq::HeadDesc **>(m->d_list.p), m->n_heads, sh,
+                                      step_rows(c0, dk, dv), dq, dout, s),
+               fn))
+    return -1;
+  for (Ctx *c : m->heads) c->st = aq::ring_after(c->st, 1, c->cap, c->hyb);
+  bump_epoch();
+  return a0.size;
 }
 
 }  // namespace
@@ -1116,15 +1204,56 @@ int adaptq_mha_compute_all(adaptq_mha_t h, const float *queries, float *outs) {
   Mha *m = static_cast<Mha *>(h);
   std::lock_guard<std::mutex> gm(m->mu);
   HeadLocks locks(m);
-  if (!flush_all_locked(m, fn)) return -1;
   const int H = m->n_heads, dim = m->heads[0]->dim;
   DeviceGuard g(m->device);
+  // one staged token per head (the Engine's decode step): the append rides in
+  // the decode launch when the step allows it
+  bool step = true;
+  for (const Ctx *c : m->heads) step = step && c->staged == 1;
+  const float *sk = nullptr;
+  if (step) {
+    if (hip_fail(lib_wait(m->device, m->stage_seq), fn)) return -1;  // pinned rows reused
+    if (hip_fail(m->h_stage.ensure(2 * (size_t)H * dim * 4), fn)) return -1;
+    float *pk = static_cast<float *>(m->h_stage.p);
+    for (int i = 0; i < H; ++i) {
+      std::memcpy(pk + (size_t)i * dim, m->heads[i]->stage_k.data(), (size_t)dim * 4);
+      std::memcpy(pk + (size_t)(H + i) * dim, m->heads[i]->stage_v.data(), (size_t)dim * 4);
+    }
+    sk = static_cast<const float *>(m->h_stage.dp);
+  }
   // queries and outputs through pinned memory the kernels read and write
   const size_t io = align256((size_t)H * dim * 4);
   if (hip_fail(m->h_io.ensure(2 * io), fn)) return -1;  // no kernel uses it between calls
   std::memcpy(m->h_io.p, queries, (size_t)H * dim * 4);
   const float *dq = static_cast<const float *>(m->h_io.dp);
   float *dout = reinterpret_cast<float *>(static_cast<uint8_t *>(m->h_io.dp) + io);
+  if (step) {
+    // the staged rows were copied out: the heads hold nothing staged while
+    // the step is tried, and take the rows back when it does not run
+    std::vector<int> held((size_t)H);
+    for (int i = 0; i < H; ++i) {
+      held[i] = m->heads[i]->staged;
+      m->heads[i]->staged = 0;
+    }
+    hipStream_t s;
+    int n = hip_fail(lib_begin(m->device, &s), fn)
+                ? -1
+                : step_all_locked(m, sk, sk + (size_t)H * dim, dq, dout, s, fn);
+    if (n >= 0) {
+      m->stage_seq = lib_end(m->device);
+      for (Ctx *c : m->heads) {
+        c->stage_k.clear();
+        c->stage_v.clear();
+      }
+      if (hip_fail(lib_wait(m->device, m->stage_seq), fn)) return -1;
+      std::memcpy(outs, static_cast<uint8_t *>(m->h_io.p) + io, (size_t)H * dim * 4);
+      clear_error();
+      return n;
+    }
+    for (int i = 0; i < H; ++i) m->heads[i]->staged = held[i];
+    if (n == -1) return -1;
+  }
+  if (!flush_all_locked(m, fn)) return -1;
   hipStream_t s;
   if (hip_fail(lib_begin(m->device, &s), fn)) return -1;
   int n = launch_all_locked(m, dq, dout, s, fn);
@@ -1194,6 +1323,43 @@ int adaptq_mha_compute_all_device(adaptq_mha_t h, const float *d_queries, float 
     set_error("adaptq_mha_compute_all_device: heads differ in ring size or branch; "
               "use adaptq_mha_compute_all");
     return -1;
+  }
+  if (n >= 0 && hip_fail(caller_end(m->device, s), fn)) return -1;
+  return n;
+}
+
+int adaptq_mha_append_compute_all_device(adaptq_mha_t h, const float *d_keys,
+                                         const float *d_vals, int token_pos,
+                                         const float *d_queries, float *d_outs, void *stream) {
+  (void)token_pos;
+  const char *fn = "adaptq_mha_append_compute_all_device";
+  if (!require_handle(h, fn) || !require_pointer(d_keys, fn, "d_keys") ||
+      !require_pointer(d_vals, fn, "d_vals") || !require_pointer(d_queries, fn, "d_queries") ||
+      !require_pointer(d_outs, fn, "d_outs"))
+    return -1;
+  Mha *m = static_cast<Mha *>(h);
+  std::lock_guard<std::mutex> gm(m->mu);
+  HeadLocks locks(m);
+  if (!flush_all_locked(m, fn)) return -1;
+  DeviceGuard g(m->device);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (hip_fail(caller_begin(m->device, s), fn)) return -1;
+  int n = step_all_locked(m, d_keys, d_vals, d_queries, d_outs, s, fn);
+  if (n == -2) {  // the append and the decode as two launches
+    const Ctx *c0 = m->heads[0];
+    if (hip_fail(aq::launch_append(static_cast<aq::HeadDesc **>(m->d_list.p), m->n_heads, c0->dim,
+                                   c0->padded, c0->k_bits, c0->v_bits, d_keys, d_vals, 1, s),
+                 fn))
+      return -1;
+    for (Ctx *c : m->heads) c->st = aq::ring_after(c->st, 1, c->cap, c->hyb);
+    bump_epoch();
+    n = launch_all_locked(m, d_queries, d_outs, s, fn);
+    if (n == -2) {
+      (void)caller_end(m->device, s);
+      set_error("adaptq_mha_append_compute_all_device: heads differ in ring size or branch "
+                "(the token was appended); use adaptq_mha_compute_all");
+      return -1;
+    }
   }
   if (n >= 0 && hip_fail(caller_end(m->device, s), fn)) return -1;
   return n;

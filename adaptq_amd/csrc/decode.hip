@@ -32,6 +32,7 @@
 // group; used for shapes the LUT kernel does not cover.
 #include <algorithm>
 
+#include "encode_one.hpp"
 #include "launch.hpp"
 
 namespace aq {
@@ -665,10 +666,20 @@ __device__ __forceinline__ void transpose_segments(uint32_t *x) {
 //   2-bit: nibble (2 codes) -> float2, 16 entries
 //   4-bit: nibble (1 code)  -> float, 16 entries
 //   3-bit: code             -> float, 8 entries
-template <int P, int KB, int VB, bool RAW>
+//
+// FUSE (a decode step, launch_decode_step): the launch first appends one token
+// per item, app.k/app.v [item][dim]: waves 1 and 2 encode its key and value
+// rows with the one-row codec (encode_one.hpp) into the ring, and into LDS,
+// while wave 0 rotates the query; the decode covers the ring after the
+// append.  Row loads issued before the new rows are written may return the
+// slot's old bytes, so the lanes whose token is the new slot take its rows
+// and scales from the LDS copies (one tile per kernel, a wave-uniform
+// branch).  One block per item (n_splits == 1), quantised K and V at padded
+// 64, no raw mirror decode.
+template <int P, int KB, int VB, bool RAW, bool FUSE = false>
 __global__ __launch_bounds__(kLutThreads, P <= 128 && (KB == 2 || KB == 4) ? 4 : 2) void decode_lut_kernel(
     HeadDesc *const *item_desc, const float *__restrict__ queries, int chunk, int n_splits,
-    float *__restrict__ partials, float *__restrict__ outs) {
+    float *__restrict__ partials, float *__restrict__ outs, StepAppend app) {
   constexpr bool KQ = KB != 16;
   constexpr bool VQ = VB != 16;
   constexpr int KNB = RAW ? 4 * P : RowBytes<P, KB>::value;
@@ -693,7 +704,16 @@ __global__ __launch_bounds__(kLutThreads, P <= 128 && (KB == 2 || KB == 4) ? 4 :
   const AQ_AS4 HeadDesc *d =
       (const AQ_AS4 HeadDesc *)((const AQ_AS4 uint64_t *)item_desc)[item];
   const int dim = d->dim;
-  const int n = d->st.size;
+  static_assert(!FUSE || (KB != 16 && VB != 16 && !RAW && P == 64), "fused step: quantised K and V");
+  RingState st0{};  // FUSE: the ring state before the step's append
+  int new_slot = -1;
+  if constexpr (FUSE) {
+    st0.head = d->st.head;
+    st0.size = d->st.size;
+    st0.raw_count = d->st.raw_count;
+    new_slot = st0.head;
+  }
+  const int n = FUSE ? ring_after(st0, 1, d->cap, d->hyb).size : d->st.size;
   const int t_begin = split * chunk;
   const int t_end = min(n, t_begin + chunk);
   float *part = partials + ((size_t)item * n_splits + split) * (P + 4);
@@ -751,6 +771,29 @@ __global__ __launch_bounds__(kLutThreads, P <= 128 && (KB == 2 || KB == 4) ? 4 :
   }
 
   load_query<P>(s_q, queries + (size_t)item * dim, dim, KQ, signs);
+  // FUSE: waves 1 and 2 encode the step's key and value rows (LDS scratch of
+  // the codec, its 4-bit bucket table per wave, the stored rows' copies)
+  constexpr bool kQ4 = FUSE && (KB == 4 || VB == 4);
+  __shared__ Q4Entry s_app_q4[kQ4 ? 2 : 1][kQ4 ? kQ4Entries : 1];
+  __shared__ __align__(16) float s_app_sq[FUSE ? 2 : 1][FUSE ? P : 1];
+  __shared__ uint8_t s_app_code[FUSE ? 2 : 1][FUSE ? P : 1];
+  __shared__ uint32_t s_app_row[FUSE ? 2 : 1][FUSE ? (KW > VW ? KW : VW) : 1];
+  __shared__ float s_app_scale[2];
+  if constexpr (FUSE) {
+    if (wave == 1 || wave == 2) {
+      const int side = wave - 1;
+      if constexpr (kQ4) {
+        for (int i = lane; i < kQ4Entries; i += 64) s_app_q4[side][i] = q4s_entry(i);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+      const float *x = (side == 0 ? app.k : app.v) + (size_t)item * dim;
+      encode_one_row<P, KB, VB>(item_desc[item], st0, 1, 0, x, dim, side, lane, app.inv_sqrt_p,
+                                app.sqrt_p, s_app_q4[kQ4 ? side : 0], s_app_sq[side],
+                                s_app_code[side], s_app_row[side], &s_app_scale[side]);
+    }
+  }
   // fixed-point scale of the K table (2/4-bit keys): f and 1/f
   __shared__ float s_fix[2];
   if constexpr (KPERM || NIB) {
@@ -789,8 +832,20 @@ __global__ __launch_bounds__(kLutThreads, P <= 128 && (KB == 2 || KB == 4) ? 4 :
   };
 
   // Logit of the token of this lane in the tile at tile_base (K row kc).
-  auto tile_logit = [&](const uint32_t *kcw, float kscale, int tile_base) -> float {
+  auto tile_logit = [&](const uint32_t *kc_in, float kscale, int tile_base) -> float {
     const int tt = tile_base + lane;
+    uint32_t kcw[KW];
+#pragma unroll
+    for (int i = 0; i < KW; ++i) kcw[i] = kc_in[i];
+    if constexpr (FUSE) {
+      // the lanes whose (clamped) row is the step's new slot: its LDS copy
+      if (tile_base <= new_slot && new_slot < tile_base + kTile) {
+        const bool mine = min(tt, t_end - 1) == new_slot;
+#pragma unroll
+        for (int i = 0; i < KW; ++i) kcw[i] = mine ? s_app_row[0][i] : kcw[i];
+        kscale = mine ? s_app_scale[0] : kscale;
+      }
+    }
     float dot;
     if constexpr (KQ && KB == 3) {
       float p4[4];
@@ -882,6 +937,15 @@ __global__ __launch_bounds__(kLutThreads, P <= 128 && (KB == 2 || KB == 4) ? 4 :
   auto step = [&](auto last_tag) {
     constexpr bool LAST = decltype(last_tag)::value;
     const bool valid = base + lane < t_end;
+    if constexpr (FUSE) {
+      // this tile's V rows: the new slot's from its LDS copy (see tile_logit)
+      if (base <= new_slot && new_slot < base + kTile) {
+        const bool mine = min(base + lane, t_end - 1) == new_slot;
+#pragma unroll
+        for (int i = 0; i < VW; ++i) vw[i] = mine ? s_app_row[1][i] : vw[i];
+        vsc = mine ? s_app_scale[1] : vsc;
+      }
+    }
 
     // ---- online softmax (wave-uniform reference maximum) ----
     // Quantised K: the reference maximum moves only when a logit exceeds it
@@ -1009,6 +1073,10 @@ __global__ __launch_bounds__(kLutThreads, P <= 128 && (KB == 2 || KB == 4) ? 4 :
       s_q[i] = a;
     }
     __syncthreads();
+    if constexpr (FUSE) {
+      // the step's ring state, once every wave has read the old one
+      if (threadIdx.x == 0) item_desc[item]->st = ring_after(st0, 1, d->cap, d->hyb);
+    }
     finish_item<VQ && !RAW>(s_q, P, dim, L, signs, outs + (size_t)item * dim, RAW, n);
     return;
   }
@@ -1307,7 +1375,8 @@ hipError_t dispatch_lut(const DecodeShape &sh, dim3 grid, HeadDesc *const *descs
                         int chunk, int splits, float *part, float *out, hipStream_t s) {
 #define AQ_LUT(KB_, VB_)                                                                         \
   if (sh.k_bits == KB_ && sh.v_bits == VB_) {                                                     \
-    decode_lut_kernel<P, KB_, VB_, RAW><<<grid, kLutThreads, 0, s>>>(descs, q, chunk, splits, part, out); \
+    decode_lut_kernel<P, KB_, VB_, RAW><<<grid, kLutThreads, 0, s>>>(descs, q, chunk, splits, part, out, \
+                                                                   StepAppend{});                    \
     return hipGetLastError();                                                                     \
   }
   if constexpr (RAW) {
@@ -1425,6 +1494,42 @@ hipError_t launch_decode(HeadDesc *const *descs, int n_items, const DecodeShape 
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
+}
+
+template <int P>
+hipError_t dispatch_lut_step(const DecodeShape &sh, dim3 grid, HeadDesc *const *descs,
+                             const float *q, int chunk, float *out, const StepAppend &app,
+                             hipStream_t s) {
+#define AQ_STEP(KB_, VB_)                                                                        \
+  if (sh.k_bits == KB_ && sh.v_bits == VB_) {                                                     \
+    decode_lut_kernel<P, KB_, VB_, false, true><<<grid, kLutThreads, 0, s>>>(descs, q, chunk, 1,  \
+                                                                            nullptr, out, app);   \
+    return hipGetLastError();                                                                     \
+  }
+  AQ_STEP(4, 2) AQ_STEP(4, 3) AQ_STEP(4, 4)
+  AQ_STEP(3, 2) AQ_STEP(3, 3) AQ_STEP(3, 4)
+  AQ_STEP(2, 2) AQ_STEP(2, 3) AQ_STEP(2, 4)
+#undef AQ_STEP
+  return hipErrorNotSupported;
+}
+
+bool decode_step_supported(int n_items, const DecodeShape &sh) {
+  // padded 64 only: at 128 the fused kernels spill (the key rows of 16
+  // words and the codec's registers), and rings there rarely plan one block
+  // per item
+  return n_items > 0 && n_items <= kMaxItemsPerLaunch && !sh.raw && sh.k_bits != 16 &&
+         sh.v_bits != 16 && sh.padded == 64 && lut_eligible(sh) &&
+         decode_plan(n_items, sh).splits == 1;
+}
+
+hipError_t launch_decode_step(HeadDesc *const *descs, int n_items, const DecodeShape &sh,
+                              const StepAppend &app, const float *d_q, float *d_out,
+                              hipStream_t s) {
+  if (n_items <= 0) return hipSuccess;
+  if (!decode_step_supported(n_items, sh)) return hipErrorNotSupported;
+  const SplitPlan sp = decode_plan(n_items, sh);
+  const dim3 grid(1, n_items);
+  return dispatch_lut_step<64>(sh, grid, descs, d_q, sp.chunk, d_out, app, s);
 }
 
 hipError_t launch_decode_items(HeadDesc *const *descs, int n_items, const DecodeShape &sh,

@@ -17,6 +17,14 @@ hipError_t launch_append(HeadDesc *const *d_descs, int n_ctx, int dim, int padde
 // Zero a head's device ring state (reset).
 hipError_t launch_reset_state(HeadDesc *const *d_descs, int n_ctx, hipStream_t stream);
 
+// The token a decode step appends before it decodes (launch_decode_step):
+// key and value rows [n_items][dim] fp32 (device or pinned host memory) and
+// the codec's two scalings 1/sqrt(padded), sqrt(padded) as floats.
+struct StepAppend {
+  const float *k, *v;
+  float inv_sqrt_p, sqrt_p;
+};
+
 struct DecodeShape {
   int dim, padded, k_bits, v_bits;
   bool raw;   // hybrid branch: exact fp32 attention over the raw mirror
@@ -32,6 +40,19 @@ size_t decode_workspace_floats(int n_items, const DecodeShape &shape);
 hipError_t launch_decode(HeadDesc *const *d_item_desc, int n_items, const DecodeShape &shape,
                          const float *d_queries, float *d_outs, float *d_workspace,
                          hipStream_t stream);
+
+// One decode step in one launch where the shape allows it: append the token
+// app.k/app.v[i] to item i's ring (as launch_append with one token), then
+// decode as launch_decode.  shape.max_n is the largest ring size after the
+// append.  Returns hipErrorNotSupported, having launched nothing, unless the
+// shape takes the LUT kernel with quantised K and V at padded 64, one block
+// per item, no hybrid branch; the caller then appends and decodes with two
+// launches.  Items must name distinct contexts of capacity > 0.
+hipError_t launch_decode_step(HeadDesc *const *d_item_desc, int n_items, const DecodeShape &shape,
+                              const StepAppend &app, const float *d_queries, float *d_outs,
+                              hipStream_t stream);
+// Whether launch_decode_step takes n_items items of this shape.
+bool decode_step_supported(int n_items, const DecodeShape &shape);
 
 // Merge of split partials (m, l, acc[padded]) per item, laid out
 // [item][split][padded + 4], into outputs [item][dim]: log-sum-exp weights,

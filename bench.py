@@ -335,8 +335,10 @@ def secondary(L, last_error, torch, np, stream, reps=20, which=("C1", "C2", "C3"
       C3: 22 layers x 4 heads d64 (layer 0 K16/V2, others K3/V2), Student-t(4)
           / sqrt 2: 1024-token bulk append (median of 5), then 256 steps of
           (append 1 + decode) for every layer; µs per step, host wall clock included;
-          per-layer calls (as the reference's Engine makes them) and two
-          plans (layer 0, layers 1-21) per step.
+          per-layer calls (as the reference's Engine makes them: an append
+          and a decode call per layer), one step call per layer
+          (adaptq_mha_append_compute_all_device) and two plans (layer 0,
+          layers 1-21) per step.
       C4: 8 heads d128 K4/V4, cap 32768, 40000 tokens appended (7232
           evictions), 64 queries per head in one launch, one query, and one
           query under Engine defaults (the sparse-V branch)."""
@@ -516,6 +518,29 @@ def secondary(L, last_error, torch, np, stream, reps=20, which=("C1", "C2", "C3"
             c3[name] = {"us_per_step": wall / steps, "gpu_us_per_step": a.elapsed_time(b) * 1e3 / steps,
                         "bulk_append_us": append_us, "decode_bytes_256_steps": step_bytes,
                         "calls_per_step": 2 * nl}
+            free(ms)
+
+            # the same steps with one call per layer and step
+            # (adaptq_mha_append_compute_all_device: the append inside the
+            # decode launch where the step allows it)
+            ms = stack([(nh, 64, 16 if l == 0 else 3, 2, 1280, l, vm, hyb) for l in range(nl)])
+            bulk_append()
+            torch.cuda.synchronize()
+            a.record(stream)
+            t0 = time.perf_counter()
+            for s in range(steps):
+                ps = pp[s]
+                for l, m in enumerate(ms):
+                    kp, vp, qp = ps[l]
+                    r = L.adaptq_mha_append_compute_all_device(m, kp, vp, n0 + s, qp, op[l], sp)
+                    if r < 0:
+                        raise RuntimeError(last_error())
+            b.record(stream)
+            torch.cuda.synchronize()
+            wall = (time.perf_counter() - t0) * 1e6
+            c3[name + "_step_calls"] = {"us_per_step": wall / steps,
+                                        "gpu_us_per_step": a.elapsed_time(b) * 1e3 / steps,
+                                        "calls_per_step": nl}
             free(ms)
 
             # the same steps through two plans (layer 0, layers 1-21): one append

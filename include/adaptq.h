@@ -184,6 +184,21 @@ int adaptq_mha_append_all_device(adaptq_mha_t mha, const float *d_keys,
 int adaptq_mha_compute_all_device(adaptq_mha_t mha, const float *d_queries,
                                   float *d_outs, void *stream);
 
+/* Extension, no counterpart in the reference.  One decode step for every
+ * head: append one token (d_keys, d_vals: device [n_heads][dim]) as
+ * adaptq_mha_append_all_device with one token, then attention as
+ * adaptq_mha_compute_all_device (d_queries -> d_outs, device [n_heads][dim]),
+ * asynchronous on `stream`.  Same ring bytes and outputs as those two calls
+ * (attention.cpp:338-366 then :480-660); where the step is a dense decode at
+ * padded 64 with quantised K and V and one block per head, the append runs
+ * inside the decode launch (one launch instead of two).  Returns the ring
+ * size after the append, or -1 (the token is appended when only the decode
+ * fails, e.g. heads that differ in ring size or branch). */
+int adaptq_mha_append_compute_all_device(adaptq_mha_t mha, const float *d_keys,
+                                         const float *d_vals, int token_pos,
+                                         const float *d_queries, float *d_outs,
+                                         void *stream);
+
 /* ---- ggml operator forms ----
  * Replace the forward functions of the reference's ggml integration
  * (integration/ggml_operator_patch.md:6-117: GGML_OP_ADAPTQ_APPEND and

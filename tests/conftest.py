@@ -57,3 +57,13 @@ def ref():
     if not Ref.available:
         pytest.skip("oracle/_ref not built (needs /root/reference)")
     return Ref()
+
+
+@pytest.fixture(scope="session")
+def torch_dev():
+    """torch with its HIP runtime (device buffers and streams for the
+    device-form calls)."""
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("needs a HIP GPU")
+    return torch
