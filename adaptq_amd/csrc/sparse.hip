@@ -23,14 +23,12 @@
 // the sort (a stable radix sort in LDS) and the cut, and turns the selection
 // into per-token weights.  Above, a grid computes the exponentials, one block
 // per item their left-to-right sum and the sort keys, a per-item radix sort
-// over many blocks (up to 65,536 tokens; above, one device-wide rocPRIM
-// sort) orders them, and one block per item takes the cut.  A grid over
+// over many blocks orders them, and one block per item takes the cut.  A grid over
 // (token chunks, items) sums the weighted V rows (deriving the weights from
 // the cut above 8,192 tokens); one block per item adds the chunks and
 // applies the inverse FWHT.  Short rings (up to 3,072 tokens) run the last
 // three steps in one block per item, at padded 64 the logits too
 // (sparse_fused_kernel).
-#include <rocprim/device/device_radix_sort.hpp>
 #include <type_traits>
 
 #include "expf_ref.hpp"
@@ -44,10 +42,10 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kSelThreads = 1024;
 // Rings up to kSelectInBlock tokens are selected inside the select kernel
-// (radix sort in LDS); longer ones sort device-wide between two kernels
+// (radix sort in LDS); longer ones sort over many blocks between two kernels
 // (measured, 8 heads d128: 12,000 tokens 242 -> 198 us and 16,384 tokens
-// 264 -> 237 us sorted device-wide; at 8,192 tokens and below the in-block
-// sort is as fast or faster).
+// 264 -> 237 us sorted outside the select kernel; at 8,192 tokens and below
+// the in-block sort is as fast or faster).
 constexpr int kSelectInBlock = 8192;
 constexpr int kLdsSort = kSelectInBlock;  // keys the select kernel sorts in LDS
 constexpr int kStage = 4096;    // floats per LDS staging chunk
@@ -872,23 +870,24 @@ __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, fl
   }
 }
 
-// Sort of rings above kSelectInBlock and up to kItemSortMax tokens: a stable
-// LSD radix sort of each item's 32-bit keys key_hi(p) with the tokens as
-// payload.  The keys are stored less the item's smallest key (which the
-// select kernel finds with 1/sum), so the digits cover only the bits of the
-// key range: kRsBits a pass, at most 3 passes (keys of probabilities in
-// [0, 1] span less than 2^30; NaN keys are all equal).  Ties keep token
-// order, which is the order make_key gives them.  Pass k is two launches
-// over (blocks of kRsKeys positions) x items.  The count kernel (at pass 0
-// it first writes the keys and tokens in token order): a block counts the
-// pass's digits among its positions and stores them at count[block][digit].  The scatter kernel: a block takes its
-// offsets from the item's counts (digits below, then the same digit in
-// blocks before it), ranks its keys stably in LDS (a ballot per digit bit
-// and running per-wave digit counts) and writes each key
-// to offset[digit] + its rank among the block's keys of that digit.  Nothing
-// crosses blocks inside a launch (device-wide atomics on the counts, and a
-// last-block scan behind device-scope fences, each measured 3-5x slower than
-// the two launches).  Longer rings use one device-wide rocPRIM sort instead.
+// Sort of rings above kSelectInBlock tokens: a stable LSD radix sort of each
+// item's 32-bit keys key_hi(p) with the tokens as payload.  The keys are
+// stored less the item's smallest key (which the select kernel finds with
+// 1/sum), so the digits cover only the bits of the key range: kRsBits a
+// pass, at most 3 passes (keys of probabilities in [0, 1] span less than
+// 2^30; NaN keys are all equal).  Ties keep token order, which is the order
+// make_key gives them.  Pass k runs over (blocks of kRsKeys positions) x
+// items.  The count kernel (at pass 0 it first writes the keys and tokens in
+// token order): a block counts the pass's digits among its positions and
+// stores them at count[block][digit].  Above kRsSuper blocks the super kernel
+// adds them per superblock of kRsSuper blocks.  The scatter kernel: a block
+// takes its offsets from the item's counts (digits below, then the same digit
+// in blocks before it: whole superblocks' sums, then the blocks of its own
+// superblock), ranks its keys stably in LDS (a ballot per digit bit and
+// running per-wave digit counts) and writes each key to offset[digit] + its
+// rank among the block's keys of that digit.  Nothing crosses blocks inside a
+// launch (device-wide atomics on the counts, and a last-block scan behind
+// device-scope fences, each measured 3-5x slower than the separate launches).
 constexpr int kRsThreads = 512;
 constexpr int kRsRounds = 4;
 constexpr int kRsWaves = kRsThreads / 64;
@@ -897,19 +896,30 @@ constexpr int kRsBits = 10;
 constexpr int kRsPasses = 3;
 constexpr int kRsDigits = 1 << kRsBits;
 constexpr int kRsDPT = kRsDigits / kRsThreads;  // digits per thread
-constexpr int kItemSortMax = 65536;
-constexpr int kRsMaxBlocks = kItemSortMax / kRsKeys;
-constexpr int kRsBins = kRsDigits * kRsMaxBlocks;  // (block, digit) counts
+constexpr int kRsSuper = 32;                    // blocks per superblock
 static_assert(kRsDigits % kRsThreads == 0, "whole digits per thread");
 
-// Word offsets inside an item's sort region (uint32): a header (0: passes,
-// 5: the smallest key, 6: tokens; pass k takes bits kRsBits k and up), the counts ((block, digit),
-// block-major), then keys A, keys B, tokens A, tokens B of Sa = align64(S)
-// words.
+__host__ __device__ constexpr int rs_blocks(int S) { return (S + kRsKeys - 1) / kRsKeys; }
+// superblocks of a ring of S tokens (0 when the scatter sums every block)
+__host__ __device__ constexpr int rs_supers(int S) {
+  return rs_blocks(S) > kRsSuper ? (rs_blocks(S) + kRsSuper - 1) / kRsSuper : 0;
+}
+
+// Word offsets inside an item's sort region (uint32), for rings of at most S
+// tokens: a header (0: passes, 5: the smallest key, 6: tokens; pass k takes
+// bits kRsBits k and up), the counts ((block, digit), block-major), the
+// superblock sums ((superblock, digit)), then keys A, keys B, tokens A,
+// tokens B of Sa = align64(S) words.
 struct ItemSort {
-  static constexpr size_t cnt = 16, keys = cnt + kRsBins;
-  static constexpr size_t sa(int S) { return ((size_t)S + 63) & ~(size_t)63; }
-  static constexpr size_t words(int S) { return keys + 4 * sa(S); }
+  static constexpr size_t cnt = 16;
+  __host__ __device__ static constexpr size_t sup(int S) {
+    return cnt + (size_t)kRsDigits * rs_blocks(S);
+  }
+  __host__ __device__ static constexpr size_t keys(int S) {
+    return sup(S) + (size_t)kRsDigits * rs_supers(S);
+  }
+  __host__ __device__ static constexpr size_t sa(int S) { return ((size_t)S + 63) & ~(size_t)63; }
+  __host__ __device__ static constexpr size_t words(int S) { return keys(S) + 4 * sa(S); }
 };
 
 // The item sort's state for one (item, pass): false when the item does not
@@ -937,10 +947,11 @@ __device__ __forceinline__ bool rs_pass(int pass, uint32_t *sort_ws, size_t item
   r.sft = pass * kRsBits;
   const size_t Sa = ItemSort::sa(S);
   const int in = pass & 1, out = in ^ 1;
-  r.sk = r.reg + ItemSort::keys + in * Sa;
-  r.stk = r.reg + ItemSort::keys + (2 + in) * Sa;
-  r.dk = r.reg + ItemSort::keys + out * Sa;
-  r.dtk = r.reg + ItemSort::keys + (2 + out) * Sa;
+  const size_t k0 = ItemSort::keys(S);
+  r.sk = r.reg + k0 + in * Sa;
+  r.stk = r.reg + k0 + (2 + in) * Sa;
+  r.dk = r.reg + k0 + out * Sa;
+  r.dtk = r.reg + k0 + (2 + out) * Sa;
   return true;
 }
 
@@ -963,7 +974,7 @@ __global__ __launch_bounds__(kRsThreads) void sparse_rsort_count_kernel(int pass
   if (pass == 0) {
     const float *lg = ws + (size_t)blockIdx.y * ws_stride;
     const float inv = lg[r.n];
-    uint32_t *ka = r.reg + ItemSort::keys, *ta = ka + 2 * ItemSort::sa(S);
+    uint32_t *ka = r.reg + ItemSort::keys(S), *ta = ka + 2 * ItemSort::sa(S);
 #pragma unroll
     for (int j = 0; j < kRsRounds; ++j) {
       const int pos = b * kRsKeys + j * kRsThreads + tid;
@@ -994,6 +1005,29 @@ __global__ __launch_bounds__(kRsThreads) void sparse_rsort_count_kernel(int pass
     r.reg[ItemSort::cnt + (size_t)b * kRsDigits + j * kRsThreads + tid] = s_hist[j * kRsThreads + tid];
 }
 
+// Superblock sums of one pass of the item sort (see above): grid
+// (superblocks, items), for items of more than kRsSuper blocks; thread t adds
+// digits 2t, 2t + 1 over the superblock's blocks.
+__global__ __launch_bounds__(kRsThreads) void sparse_rsort_super_kernel(int pass, uint32_t *sort_ws,
+                                                                        size_t item_words, int S) {
+  uint32_t *reg = sort_ws + (size_t)blockIdx.y * item_words;
+  const int np = (int)reg[0], n = (int)reg[6];
+  const int G = rs_blocks(n), B = blockIdx.x;
+  if (pass >= np || G <= kRsSuper || B * kRsSuper >= G) return;
+  static_assert(kRsDPT == 2, "two digits (one uint2) per thread");
+  const uint2 *c = reinterpret_cast<const uint2 *>(reg + ItemSort::cnt) + threadIdx.x;
+  const int b0 = B * kRsSuper, b1 = min(G, b0 + kRsSuper);
+  uint32_t a0 = 0u, a1 = 0u;
+#pragma unroll 8
+  for (int b = b0; b < b1; ++b) {
+    const uint2 v = c[(size_t)b * (kRsDigits / 2)];
+    a0 += v.x;
+    a1 += v.y;
+  }
+  reinterpret_cast<uint2 *>(reg + ItemSort::sup(S))[(size_t)B * (kRsDigits / 2) + threadIdx.x] =
+      make_uint2(a0, a1);
+}
+
 // Scatter kernel of one pass of the item sort (see above): grid (blocks, items).
 // Wave w of the block owns positions w 64 R .. w 64 R + 64 R - 1 of its
 // range, 64 a round: a key's rank among the block's keys of its digit is the
@@ -1021,25 +1055,42 @@ __global__ __launch_bounds__(kRsThreads) void sparse_rsort_pass_kernel(int pass,
     tk[r] = valid ? rp.stk[p0 + 64 * r] : 0u;
   }
   // this block's offsets: thread t takes digits 2t, 2t + 1, adds each one's
-  // counts over every block (total) and over the blocks before this one; an
-  // exclusive scan of the totals over the digits gives each digit's start
+  // counts over every block (total) and over the blocks before this one (up
+  // to kRsSuper blocks one by one; beyond, whole superblocks' sums and then
+  // the blocks of this block's superblock); an exclusive scan of the totals
+  // over the digits gives each digit's start
   static_assert(kRsDPT == 2, "two digits (one uint2) per thread");
   {
     const uint2 *c = reinterpret_cast<const uint2 *>(rp.reg + ItemSort::cnt) + tid;
     uint32_t tot[2] = {0u, 0u}, pre[2] = {0u, 0u};
-    for (int j0 = 0; j0 < rp.G; j0 += 8) {
-      uint2 v[8];
+    // sums of n_part rows of uint2 (stride kRsDigits / 2) from src: all into
+    // tot, the first n_pre also into pre
+    auto add_rows = [&](const uint2 *src, int n_part, int n_pre, bool into_tot) {
+      for (int j0 = 0; j0 < n_part; j0 += 8) {
+        uint2 v[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        v[j] = j0 + j < rp.G ? c[(size_t)(j0 + j) * (kRsDigits / 2)] : make_uint2(0u, 0u);
+        for (int j = 0; j < 8; ++j)
+          v[j] = j0 + j < n_part ? src[(size_t)(j0 + j) * (kRsDigits / 2)] : make_uint2(0u, 0u);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const bool before = j0 + j < b;
-        pre[0] += before ? v[j].x : 0u;
-        pre[1] += before ? v[j].y : 0u;
-        tot[0] += v[j].x;
-        tot[1] += v[j].y;
+        for (int j = 0; j < 8; ++j) {
+          const bool before = j0 + j < n_pre;
+          pre[0] += before ? v[j].x : 0u;
+          pre[1] += before ? v[j].y : 0u;
+          if (into_tot) {
+            tot[0] += v[j].x;
+            tot[1] += v[j].y;
+          }
+        }
       }
+    };
+    if (rp.G <= kRsSuper) {
+      add_rows(c, rp.G, b, true);
+    } else {
+      const uint2 *sc = reinterpret_cast<const uint2 *>(rp.reg + ItemSort::sup(S)) + tid;
+      const int Bb = b / kRsSuper;
+      add_rows(sc, (rp.G + kRsSuper - 1) / kRsSuper, Bb, true);
+      add_rows(c + (size_t)Bb * kRsSuper * (kRsDigits / 2), b - Bb * kRsSuper, b - Bb * kRsSuper,
+               false);
     }
     const uint32_t mine = tot[0] + tot[1];
     uint32_t incl = mine;
@@ -1099,12 +1150,9 @@ __global__ __launch_bounds__(kRsThreads) void sparse_rsort_pass_kernel(int pass,
 // One block of kSelThreads per item: the sparse-V selection.  n <=
 // kSelectInBlock: select_small, all of it, as per-token weights.  Larger n:
 // the exponentials (sparse_exp_kernel's) are added left to right (inv =
-// 1/sum is kept at lg[n]) and the sort keys written: for the item sort
-// (sort_ws), key_hi(p) less the smallest key with the tokens, in token order;
-// for the device-wide sort (keys), (slot << 32) | key_hi(p) with the tokens
-// in the item's slot of S entries of a launch-wide array (padding: key_hi =
-// ~0, after everything; items at or below kSelectInBlock fill their slot with
-// padding).  Either sort orders p descending, ties older first;
+// 1/sum is kept at lg[n]) and the item sort's header written (its keys,
+// key_hi(p) less the smallest key with the tokens in token order, come from
+// its first count kernel); the sort orders p descending, ties older first;
 // sparse_cut_kernel then takes the cut, sparse_vsum_kernel derives the
 // weights and sums the weighted V rows over many blocks, and
 // sparse_finish_kernel applies the inverse FWHT.  The V sum runs in token
@@ -1112,8 +1160,7 @@ __global__ __launch_bounds__(kRsThreads) void sparse_rsort_pass_kernel(int pass,
 // rounding; the selected set is the reference's.
 __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *const *item_desc,
                                                                     float v_mass, float *ws,
-                                                                    size_t ws_stride, int S,
-                                                                    uint64_t *keys, uint32_t *toks,
+                                                                    size_t ws_stride,
                                                                     uint32_t *sort_ws,
                                                                     size_t item_words) {
   __shared__ SelectShared sh;
@@ -1121,13 +1168,6 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
   const int tid = threadIdx.x;
   const HeadDesc *d = item_desc[item];
   const int n = d->st.size, cap = d->cap;
-  const uint64_t slot_hi = (uint64_t)item << 32;
-  if (keys && n <= kSelectInBlock) {
-    for (int i = tid; i < S; i += blockDim.x) {
-      keys[(size_t)item * S + i] = slot_hi | 0xFFFFFFFFu;
-      toks[(size_t)item * S + i] = 0u;
-    }
-  }
   // items this kernel sorts itself take no item-sort pass
   if (sort_ws && n <= kSelectInBlock && tid == 0) {
     sort_ws[(size_t)item * item_words] = 0u;
@@ -1231,15 +1271,6 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
   const float inv = s_bcast[0];
   if (tid == 0) lg[n] = inv;
 
-  if (!sort_ws) {
-    // 3. sort keys and tokens into the item's slot
-#pragma unroll 8
-    for (int i = tid; i < S; i += kSelThreads) {
-      keys[(size_t)item * S + i] = slot_hi | (i < n ? key_hi(__fmul_rn(lg[i], inv)) : 0xFFFFFFFFu);
-      toks[(size_t)item * S + i] = (uint32_t)i;
-    }
-    return;
-  }
   // 3. the item sort's header: the passes the key range needs, the smallest
   // key (the first count kernel writes the keys less it, from lg and inv).
   // p = e * inv is monotone in e, so the largest e gives the smallest key and
@@ -1269,16 +1300,12 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
   }
 }
 
-// The cut of an item above kSelectInBlock tokens, over its sorted keys: the
-// item sort's final buffers (ITEM: key_hi less the smallest key, and tokens),
-// or the item's slot of the device-wide sort (keys: slot << 32 | key_hi,
-// toks: tokens).  sparse_vsum_kernel derives the weights from it.
-template <bool ITEM>
+// The cut of an item above kSelectInBlock tokens, over its sorted keys (the
+// item sort's final buffers: key_hi less the smallest key, and tokens).
+// sparse_vsum_kernel derives the weights from it.
 __global__ __launch_bounds__(kSelThreads) void sparse_cut_kernel(HeadDesc *const *item_desc,
                                                                  float v_mass, float *ws,
                                                                  size_t ws_stride, int S,
-                                                                 const uint64_t *keys,
-                                                                 const uint32_t *toks,
                                                                  const uint32_t *sort_ws,
                                                                  size_t item_words) {
   __shared__ float s_stage[kStage];
@@ -1292,42 +1319,26 @@ __global__ __launch_bounds__(kSelThreads) void sparse_cut_kernel(HeadDesc *const
   const int n = d->st.size;
   if (n <= kSelectInBlock) return;  // select_small wrote its weights
   float *lg = ws + (size_t)item * ws_stride;
-  // sorted key i: 32-bit words at stride 2 (the low halves of the 64-bit
-  // slot keys) or 1 (the item sort's)
-  const uint32_t *kk;
-  const uint32_t *tt;
-  constexpr int ks = ITEM ? 1 : 2;
-  uint32_t kmin = 0u;
-  if constexpr (ITEM) {
-    const uint32_t *reg = sort_ws + (size_t)item * item_words;
-    const size_t fin = reg[0] & 1u, Sa = ItemSort::sa(S);  // the last pass's output
-    kk = reg + ItemSort::keys + fin * Sa;
-    tt = reg + ItemSort::keys + (2 + fin) * Sa;
-    kmin = reg[5];
-  } else {
-    kk = reinterpret_cast<const uint32_t *>(keys + (size_t)item * S);
-    tt = toks + (size_t)item * S;
-  }
+  // sorted key i (the last pass's output)
+  const uint32_t *reg = sort_ws + (size_t)item * item_words;
+  const size_t fin = reg[0] & 1u, Sa = ItemSort::sa(S);
+  const uint32_t *kk = reg + ItemSort::keys(S) + fin * Sa;
+  const uint32_t *tt = reg + ItemSort::keys(S) + (2 + fin) * Sa;
+  const uint32_t kmin = reg[5];
   auto skey = [kk, tt, kmin](int i) -> uint64_t {
-    return ((uint64_t)(kk[ks * i] + kmin) << 32) | tt[i];
+    return ((uint64_t)(kk[i] + kmin) << 32) | tt[i];
   };
 
   // 4. the cut: whole quads while mass < v_mass, then single tokens; NaN
   // probabilities (sorted last) keep the one-lane chain
   const int n_quads = n / 4;  // quads with ii + 3 < n
-  auto quad = [skey, kk, kmin](int k) {
-    const int q = 4 * k;
-    if constexpr (ITEM) {
-      // the quad's four keys are adjacent and 16-byte aligned: one load
-      const uint4 h = *reinterpret_cast<const uint4 *>(kk + q);
-      return __fadd_rn(__fadd_rn(__fadd_rn(hi_p(h.x + kmin), hi_p(h.y + kmin)), hi_p(h.z + kmin)),
-                       hi_p(h.w + kmin));
-    } else {
-      return __fadd_rn(__fadd_rn(__fadd_rn(key_p(skey(q)), key_p(skey(q + 1))), key_p(skey(q + 2))),
-                       key_p(skey(q + 3)));
-    }
+  auto quad = [kk, kmin](int k) {
+    // the quad's four keys are adjacent and 16-byte aligned: one load
+    const uint4 h = *reinterpret_cast<const uint4 *>(kk + 4 * k);
+    return __fadd_rn(__fadd_rn(__fadd_rn(hi_p(h.x + kmin), hi_p(h.y + kmin)), hi_p(h.z + kmin)),
+                     hi_p(h.w + kmin));
   };
-  if (kk[ks * (n - 1)] + kmin == 0xFFFFFFFFu) {
+  if (kk[n - 1] + kmin == 0xFFFFFFFFu) {
     float mass = 0.0f;
     int ii = 0;
     bool open = true;  // thread 0: the quad loop has not stopped
@@ -1733,31 +1744,7 @@ size_t item_stride(int n) {
 // Items per launch: the grid holds items in one dimension (at most 65,535).
 constexpr int kMaxItems = 65535;
 
-// Launch-wide sort of rings above kSelectInBlock: chunk items' slots of S keys
-// (64-bit) and tokens (32-bit), in and out, then rocPRIM's scratch.
-struct SortSpace {
-  size_t keys_floats, toks_floats, temp_bytes, floats;
-};
-
-int item_bits(int cnt) {
-  int b = 0;
-  while ((1 << b) < cnt) ++b;
-  return b;
-}
-
 size_t align64(size_t x) { return (x + 63) & ~(size_t)63; }
-
-SortSpace sort_space(int cnt, int S) {
-  SortSpace sp{};
-  const size_t m = (size_t)cnt * S;
-  sp.keys_floats = align64(2 * m);
-  sp.toks_floats = align64(m);
-  (void)rocprim::radix_sort_pairs(nullptr, sp.temp_bytes, (const uint64_t *)nullptr,
-                                  (uint64_t *)nullptr, (const uint32_t *)nullptr,
-                                  (uint32_t *)nullptr, m, 0u, 32u + (unsigned)item_bits(cnt));
-  sp.floats = 2 * sp.keys_floats + 2 * sp.toks_floats + align64((sp.temp_bytes + 3) / 4);
-  return sp;
-}
 
 }  // namespace
 
@@ -1770,8 +1757,7 @@ size_t sparse_workspace_floats(int n_items, const DecodeShape &sh) {
   const int n = sh.max_n > 0 ? sh.max_n : 1;
   size_t f = align64((size_t)n_items * item_stride(n) + (size_t)n_items * vsum_splits(n) * sh.padded);
   const int cnt = n_items < kMaxItems ? n_items : kMaxItems;
-  if (n > kItemSortMax) f += sort_space(cnt, n).floats;
-  else if (n > kSelectInBlock) f += align64((size_t)cnt * ItemSort::words(n));
+  if (n > kSelectInBlock) f += align64((size_t)cnt * ItemSort::words(n));
   return f;
 }
 
@@ -1847,49 +1833,28 @@ hipError_t launch_decode_sparse(HeadDesc *const *descs, int n_items, const Decod
       if (e != hipSuccess) return e;
     }
     if (n <= kSelectInBlock) {
-      sparse_select_kernel<<<cnt, kSelThreads, 0, s>>>(dsc, v_mass, w, stride, 0, nullptr, nullptr,
-                                                       nullptr, 0);
+      sparse_select_kernel<<<cnt, kSelThreads, 0, s>>>(dsc, v_mass, w, stride, nullptr, 0);
       e = hipGetLastError();
       if (e != hipSuccess) return e;
-    } else if (n <= kItemSortMax) {
+    } else {
       // the item sort: keys, up to kRsPasses passes (each returns at once
       // for items whose key range is shorter), the cut
       uint32_t *rs = reinterpret_cast<uint32_t *>(sort_base);
       const size_t iw = ItemSort::words(n);
-      sparse_select_kernel<<<cnt, kSelThreads, 0, s>>>(dsc, v_mass, w, stride, n, nullptr, nullptr,
-                                                       rs, iw);
+      sparse_select_kernel<<<cnt, kSelThreads, 0, s>>>(dsc, v_mass, w, stride, rs, iw);
       e = hipGetLastError();
       if (e != hipSuccess) return e;
-      const dim3 gp((n + kRsKeys - 1) / kRsKeys, cnt);
+      const dim3 gp(rs_blocks(n), cnt);
+      const int ns = rs_supers(n);
       for (int pass = 0; pass < kRsPasses; ++pass) {
         sparse_rsort_count_kernel<<<gp, kRsThreads, 0, s>>>(pass, rs, iw, n, w, stride);
+        if (ns > 0)
+          sparse_rsort_super_kernel<<<dim3(ns, cnt), kRsThreads, 0, s>>>(pass, rs, iw, n);
         sparse_rsort_pass_kernel<<<gp, kRsThreads, 0, s>>>(pass, rs, iw, n);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
       }
-      sparse_cut_kernel<true><<<cnt, kSelThreads, 0, s>>>(dsc, v_mass, w, stride, n, nullptr,
-                                                          nullptr, rs, iw);
-      e = hipGetLastError();
-      if (e != hipSuccess) return e;
-    } else {
-      // slots of S = n keys per item; the chunk's layout as sized by
-      // sparse_workspace_floats (for the largest chunk)
-      const SortSpace ss = sort_space(cnt, n);
-      uint64_t *k_in = reinterpret_cast<uint64_t *>(sort_base);
-      uint64_t *k_out = reinterpret_cast<uint64_t *>(sort_base + ss.keys_floats);
-      uint32_t *t_in = reinterpret_cast<uint32_t *>(sort_base + 2 * ss.keys_floats);
-      uint32_t *t_out = reinterpret_cast<uint32_t *>(sort_base + 2 * ss.keys_floats + ss.toks_floats);
-      void *temp = sort_base + 2 * ss.keys_floats + 2 * ss.toks_floats;
-      sparse_select_kernel<<<cnt, kSelThreads, 0, s>>>(dsc, v_mass, w, stride, n, k_in, t_in,
-                                                       nullptr, 0);
-      e = hipGetLastError();
-      if (e != hipSuccess) return e;
-      size_t temp_bytes = ss.temp_bytes;
-      e = rocprim::radix_sort_pairs(temp, temp_bytes, k_in, k_out, t_in, t_out, (size_t)cnt * n, 0u,
-                                    32u + (unsigned)item_bits(cnt), s);
-      if (e != hipSuccess) return e;
-      sparse_cut_kernel<false><<<cnt, kSelThreads, 0, s>>>(dsc, v_mass, w, stride, n, k_out,
-                                                           t_out, nullptr, 0);
+      sparse_cut_kernel<<<cnt, kSelThreads, 0, s>>>(dsc, v_mass, w, stride, n, rs, iw);
       e = hipGetLastError();
       if (e != hipSuccess) return e;
     }

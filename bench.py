@@ -591,7 +591,7 @@ def secondary(L, last_error, torch, np, stream, reps=20, which=("C1", "C2", "C3"
                                                            dp(od), row, nh * row, sp)))
         us1 = span(lambda: ok(L.adaptq_mha_compute_all_device(ms[0], dp(qd[0]), dp(od[0]), sp)))
         # Engine defaults (v_mass 0.95, hybrid 512): the sparse-V branch at
-        # 32,768 tokens (selection sorted device-wide)
+        # 32,768 tokens (the per-item radix sort over many blocks)
         md = stack([(nh, 128, 4, 4, cap, 7, 0.95, 512)])
         ok(L.adaptq_mha_append_all_device(md[0], dp(kd), dp(vd), ntok, 0, sp))
         usd = span(lambda: ok(L.adaptq_mha_compute_all_device(md[0], dp(qd[0]), dp(od[0]), sp)))

@@ -139,8 +139,8 @@ def codec_inputs(dim: int, family: str, n: int = 8) -> np.ndarray:
 
 # ------------------------------------------------- sparse-V ties at the cut
 # Rings whose probabilities tie exactly at the mass cut, one per selection
-# path (fused <= 3,072 tokens, in-LDS sort <= 8,192, per-item radix sort <=
-# 65,536, device-wide sort beyond): "zero" decodes a zero query (every
+# path (fused <= 3,072 tokens, in-LDS sort <= 8,192, per-item radix sort
+# above, with superblock sums past 65,536): "zero" decodes a zero query (every
 # logit 0, every probability 1/n); "rep" repeats 97 key vectors (equal codes
 # and scales, so equal probabilities within each group of keys).
 TIE_CASES = [(n, kind) for n in (2048, 5000, 20000, 70000) for kind in ("zero", "rep")]

@@ -81,8 +81,8 @@ def test_plan_empty_rings_give_zeros():
 
 # Sparse-V (v_mass > 0) and hybrid (raw mirror) branches through one plan:
 # heads hold different numbers of tokens, outputs match the oracle per head.
-# Above 8,192 tokens the launch sorts device-wide; heads at or below it in the
-# same launch are selected inside the select kernel.
+# Above 8,192 tokens the launch sorts over many blocks per head; heads at or
+# below it in the same launch are selected inside the select kernel.
 @pytest.mark.parametrize("dim,kb,vb,cap,vm,hyb,sizes", [
     (64, 4, 2, 4096, 0.95, 0, [2048, 1500, 3000, 7]),
     (128, 3, 2, 2048, 0.9, 0, [1025, 1280, 600]),

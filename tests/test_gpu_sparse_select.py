@@ -10,8 +10,9 @@ the fused one-block kernel (rings up to 3,072 tokens at padded 64/128), the
 in-LDS radix sort of the select kernel (up to 8,192 tokens), the per-item
 multi-block radix sort plus cut kernel above that (up to 65,536 tokens: a
 wrapped 32,768-token ring, exact ties across sort blocks, every probability
-equal) and the device-wide sort beyond (a plain and a wrapped ring), at
-v_mass 0.95 / 0.999 / 0.9999 and with peaked queries.
+equal) and, above it, the same sort with superblock sums (a plain and a
+wrapped ring of 70,000 tokens, a wrapped ring of 300,000), at v_mass 0.95 /
+0.999 / 0.9999 and with peaked queries.
 """
 import numpy as np
 import pytest
@@ -125,18 +126,18 @@ def test_item_sort_ties(oracle):
     check_selection(g, o, np.zeros(64, np.float32), "zero query")
 
 
-def test_device_wide_sort_selection(oracle):
-    """A ring above the item sort's limit (70,000 tokens) takes the
-    device-wide sort."""
+def test_superblock_sort_selection(oracle):
+    """A ring of 70,000 tokens: 35 sort blocks, the scatter reading two
+    superblocks' sums."""
     rng = np.random.default_rng(70)
     g, o = fill(64, 2, 2, 70000, 29, 70000, 0.95, oracle, rng)
     q = rng.standard_normal(64).astype(np.float32)
     check_selection(g, o, q, "n=70000")
 
 
-def test_device_wide_sort_wrapped_selection(oracle):
-    """A wrapped ring above the item sort's limit (capacity 66,000, 70,000
-    tokens appended: 4,000 evictions) takes the device-wide sort."""
+def test_superblock_sort_wrapped_selection(oracle):
+    """A wrapped ring above 32 sort blocks (capacity 66,000, 70,000 tokens
+    appended: 4,000 evictions)."""
     rng = np.random.default_rng(66)
     g, o = fill(64, 4, 2, 66000, 31, 70000, 0.95, oracle, rng)
     assert g.info()["head"] == o.info()["head"] == 4000
@@ -160,3 +161,13 @@ def test_not_sparse_is_an_error():
     q = np.ones(64, np.float32)
     assert L.adaptq_sparse_weights(g.h, _lib.fptr(q), _lib.fptr(w)) == -1
     assert "sparse-V" in err()
+
+
+def test_many_superblocks_wrapped_selection(oracle):
+    """A wrapped ring of 300,000 tokens (capacity 300,000, 310,000 appended):
+    147 sort blocks in 5 superblocks."""
+    rng = np.random.default_rng(300)
+    g, o = fill(64, 2, 2, 300000, 37, 310000, 0.95, oracle, rng)
+    assert g.info()["head"] == o.info()["head"] == 10000
+    q = (2.0 * rng.standard_normal(64)).astype(np.float32)
+    check_selection(g, o, q, "cap=300000 n=310000 wrapped")

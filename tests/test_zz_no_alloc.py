@@ -59,7 +59,7 @@ def _both(torch, plan, n_ctx, dim, seed):
     (128, 4, 2, 0.0, [(4, 20000), (2, 3000)]),   # dense, split-K partials in the scratch
     (64, 4, 2, 0.95, [(3, 5000), (2, 1500)]),    # sparse-V, selection workspace in the scratch
     (64, 3, 2, 0.95, [(2, 10000), (1, 9000)]),   # sparse-V with the per-item radix sort
-    (64, 2, 2, 0.95, [(1, 70000), (1, 66000)]),  # sparse-V with the device-wide sort
+    (64, 2, 2, 0.95, [(1, 70000), (1, 66000)]),  # sparse-V, the sort with superblock sums
 ])
 def test_static_matches_allocating(dim, kb, vb, vm, sizes):
     import torch
