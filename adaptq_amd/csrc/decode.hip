@@ -18,7 +18,7 @@
 // tiles with an online softmax; a block writes (max, sum, acc[p]) and the
 // finalize kernel merges splits and applies the inverse FWHT.
 //
-// LUT kernel (padded 64 or 128; 256 with quantised K and V): one lane per
+// LUT kernel (padded 64, 128 and 256): one lane per
 // token.
 //   K: byte lookup table in LDS, LUT[j][b] = the contribution of code byte j
 //      with value b (2 codes at 4 bits, 4 at 2 bits, a 6-bit code pair at 3
@@ -1381,11 +1381,6 @@ hipError_t dispatch_lut(const DecodeShape &sh, dim3 grid, HeadDesc *const *descs
   }
   if constexpr (RAW) {
     AQ_LUT(16, 16)
-  } else if constexpr (P >= 256) {
-    // quantised K and V only (lut_eligible)
-    AQ_LUT(4, 2) AQ_LUT(4, 3) AQ_LUT(4, 4)
-    AQ_LUT(3, 2) AQ_LUT(3, 3) AQ_LUT(3, 4)
-    AQ_LUT(2, 2) AQ_LUT(2, 3) AQ_LUT(2, 4)
   } else {
     AQ_LUT(4, 2) AQ_LUT(4, 3) AQ_LUT(4, 4) AQ_LUT(4, 16)
     AQ_LUT(3, 2) AQ_LUT(3, 3) AQ_LUT(3, 4) AQ_LUT(3, 16)
@@ -1416,12 +1411,11 @@ hipError_t dispatch_generic(const DecodeShape &sh, dim3 grid, HeadDesc *const *d
   return hipErrorInvalidValue;
 }
 
-// The LUT kernel serves padded 64/128 (raw mirrors only when unpadded) and
-// padded 256 with quantised K and V; everything else takes the generic
-// kernel.
+// The LUT kernel serves padded 64, 128 and 256 (raw mirrors only when
+// unpadded); everything else takes the generic kernel.
 bool lut_eligible(const DecodeShape &sh) {
-  const bool q256 = sh.padded == 256 && !sh.raw && sh.k_bits != 16 && sh.v_bits != 16;
-  if (!(q256 || ((sh.padded == 64 || sh.padded == 128) && (!sh.raw || sh.dim == sh.padded))))
+  if (!((sh.padded == 64 || sh.padded == 128 || sh.padded == 256) &&
+        (!sh.raw || sh.dim == sh.padded)))
     return false;
   // the LUT kernel addresses rows with 32-bit byte offsets
   const long long row = sh.raw ? 4LL * sh.padded
@@ -1544,7 +1538,8 @@ hipError_t launch_decode_items(HeadDesc *const *descs, int n_items, const Decode
       e = raw ? dispatch_lut<64, true>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, d_out, s)
               : dispatch_lut<64, false>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, d_out, s);
     else if (sh.padded == 256)
-      e = dispatch_lut<256, false>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, d_out, s);
+      e = raw ? dispatch_lut<256, true>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, d_out, s)
+              : dispatch_lut<256, false>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, d_out, s);
     else
       e = raw ? dispatch_lut<128, true>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, d_out, s)
               : dispatch_lut<128, false>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, d_out, s);

@@ -270,6 +270,13 @@ DECODE_CASES = [
     (256, 3, 3, 512, 512),
     (256, 3, 4, 1000, 1000),
     (200, 4, 2, 600, 777),
+    # padded 256 with fp32 keys or values (the reference's layer-0 K16 policy
+    # at head dim 256) through the LUT kernel
+    (256, 16, 2, 1500, 2000),
+    (256, 16, 4, 300, 200),
+    (256, 4, 16, 700, 700),
+    (256, 16, 16, 256, 300),
+    (200, 16, 3, 400, 400),
 ]
 
 
@@ -292,6 +299,7 @@ def test_decode_dense(oracle, dim, kb, vb, cap, n):
 
 @pytest.mark.parametrize("dim,kb,vb,hyb,n", [
     (64, 4, 2, 512, 512), (128, 4, 4, 64, 40), (96, 3, 2, 128, 100), (64, 16, 2, 16, 10),
+    (256, 4, 2, 512, 500), (256, 3, 3, 64, 64),
 ])
 def test_decode_hybrid(oracle, dim, kb, vb, hyb, n):
     print(f"decode hybrid dim={dim} k{kb}v{vb} hyb={hyb} n={n}", flush=True)
