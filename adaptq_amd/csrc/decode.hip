@@ -679,7 +679,7 @@ __device__ __forceinline__ void transpose_segments(uint32_t *x) {
 template <int P, int KB, int VB, bool RAW, bool FUSE = false>
 __global__ __launch_bounds__(kLutThreads, P <= 128 && (KB == 2 || KB == 4) ? 4 : 2) void decode_lut_kernel(
     HeadDesc *const *item_desc, const float *__restrict__ queries, int chunk, int n_splits,
-    float *__restrict__ partials, float *__restrict__ outs, StepAppend app) {
+    float *__restrict__ partials, float *__restrict__ outs, StepAppend app, int qdim) {
   constexpr bool KQ = KB != 16;
   constexpr bool VQ = VB != 16;
   constexpr int KNB = RAW ? 4 * P : RowBytes<P, KB>::value;
@@ -703,7 +703,9 @@ __global__ __launch_bounds__(kLutThreads, P <= 128 && (KB == 2 || KB == 4) ? 4 :
   // load as scalars (a generic-pointer load is assumed divergent).
   const AQ_AS4 HeadDesc *d =
       (const AQ_AS4 HeadDesc *)((const AQ_AS4 uint64_t *)item_desc)[item];
-  const int dim = d->dim;
+  // every item of a launch has this dim (it is also d->dim): the query's
+  // address does not wait for the descriptor
+  const int dim = qdim;
   static_assert(!FUSE || (KB != 16 && VB != 16 && !RAW && P == 64), "fused step: quantised K and V");
   RingState st0{};  // FUSE: the ring state before the step's append
   int new_slot = -1;
@@ -1282,23 +1284,32 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(HeadDesc *const *ite
                                                             int n_splits,
                                                             const float *__restrict__ partials,
                                                             float *__restrict__ outs, int guard) {
+  // Latency-bound (a few KB per item): every partial the block reads is
+  // requested before any is used, and the descriptor (dim, signs, ring size)
+  // only at the end.  An empty ring is one whose splits are all empty (the
+  // decode kernels write -inf as an empty split's maximum and seed a
+  // non-empty one's at -1e30 or above).
+  constexpr int kPre = 16;  // partial sums a thread requests before the weights are known
   __shared__ float s_acc[kMaxPadded];
   __shared__ float s_f[kMaxSplitWeights];
   __shared__ float s_red[kWaves];
   __shared__ float s_grp[kThreads];
   const int item = blockIdx.x;
-  const HeadDesc *d = item_desc[item];
-  const int dim = d->dim;
-  float *out = outs + (size_t)item * dim;
-  if (d->st.size == 0) {
-    for (int i = threadIdx.x; i < dim; i += blockDim.x) out[i] = 0.0f;
-    return;
-  }
   const size_t stride = (size_t)P + 4;
   const float *part = partials + (size_t)item * n_splits * stride;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int groups = P < kThreads ? kThreads / P : 1;
+  const int gi = threadIdx.x % P, grp = threadIdx.x / P;  // used when groups > 1
+  float pre[kPre];
+  if (groups > 1) {
+#pragma unroll
+    for (int k = 0; k < kPre; ++k) {
+      const int sp = grp + k * groups;
+      pre[k] = sp < n_splits ? part[sp * stride + 4 + gi] : 0.0f;
+    }
+  }
   float m = -INFINITY;
-  for (int s = threadIdx.x; s < n_splits; s += kThreads) m = fmaxf(m, part[s * stride]);
+  for (int sp = threadIdx.x; sp < n_splits; sp += kThreads) m = fmaxf(m, part[sp * stride]);
   m = wave_max(m);
   if (lane == 0) s_red[wave] = m;
   __syncthreads();
@@ -1306,12 +1317,19 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(HeadDesc *const *ite
 #pragma unroll
   for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_red[w]);
   __syncthreads();
+  const HeadDesc *d = item_desc[item];
+  if (M == -INFINITY) {  // an empty ring: zeros (attention.cpp:482-485)
+    const int dim = d->dim;
+    float *out = outs + (size_t)item * dim;
+    for (int i = threadIdx.x; i < dim; i += blockDim.x) out[i] = 0.0f;
+    return;
+  }
   float l = 0.0f;
-  for (int s = threadIdx.x; s < n_splits; s += kThreads) {
-    const float ms = part[s * stride];
+  for (int sp = threadIdx.x; sp < n_splits; sp += kThreads) {
+    const float ms = part[sp * stride];
     const float f = ms == -INFINITY ? 0.0f : expf(ms - M);
-    if (s < kMaxSplitWeights) s_f[s] = f;
-    l += f * part[s * stride + 1];
+    if (sp < kMaxSplitWeights) s_f[sp] = f;
+    l += f * part[sp * stride + 1];
   }
   l = wave_sum(l);
   if (lane == 0) s_red[wave] = l;
@@ -1319,18 +1337,23 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(HeadDesc *const *ite
   float L = 0.0f;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) L += s_red[w];
-  auto weight = [&](int s) -> float {
-    if (s < kMaxSplitWeights) return s_f[s];
-    const float ms = part[s * stride];
+  auto weight = [&](int sp) -> float {
+    if (sp < kMaxSplitWeights) return s_f[sp];
+    const float ms = part[sp * stride];
     return ms == -INFINITY ? 0.0f : expf(ms - M);
   };
-  const int groups = P < kThreads ? kThreads / P : 1;
   if (groups > 1) {
-    // P divides kThreads (P is a power of two below it)
-    const int i = threadIdx.x % P, grp = threadIdx.x / P;
+    // P divides kThreads (P is a power of two below it); the splits of this
+    // thread's group in order: the requested ones, then the rest
     float a = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kPre; ++k) {
+      const int sp = grp + k * groups;
+      if (sp < n_splits) a += weight(sp) * pre[k];
+    }
 #pragma unroll 4
-    for (int s = grp; s < n_splits; s += groups) a += weight(s) * part[s * stride + 4 + i];
+    for (int sp = grp + kPre * groups; sp < n_splits; sp += groups)
+      a += weight(sp) * part[sp * stride + 4 + gi];
     s_grp[threadIdx.x] = a;
     __syncthreads();
     if (threadIdx.x < P) {
@@ -1342,12 +1365,14 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(HeadDesc *const *ite
     for (int i = threadIdx.x; i < P; i += kThreads) {
       float a = 0.0f;
 #pragma unroll 4
-      for (int s = 0; s < n_splits; ++s) a += weight(s) * part[s * stride + 4 + i];
+      for (int sp = 0; sp < n_splits; ++sp) a += weight(sp) * part[sp * stride + 4 + i];
       s_acc[i] = a;
     }
   }
   __syncthreads();
-  finish_item<INVERSE_FWHT>(s_acc, P, dim, L, d->signs, out, guard != 0, d->st.size);
+  const int dim = d->dim;
+  finish_item<INVERSE_FWHT>(s_acc, P, dim, L, d->signs, outs + (size_t)item * dim, guard != 0,
+                            d->st.size);
 }
 
 struct SplitPlan {
@@ -1376,7 +1401,7 @@ hipError_t dispatch_lut(const DecodeShape &sh, dim3 grid, HeadDesc *const *descs
 #define AQ_LUT(KB_, VB_)                                                                         \
   if (sh.k_bits == KB_ && sh.v_bits == VB_) {                                                     \
     decode_lut_kernel<P, KB_, VB_, RAW><<<grid, kLutThreads, 0, s>>>(descs, q, chunk, splits, part, out, \
-                                                                   StepAppend{});                    \
+                                                                   StepAppend{}, sh.dim);            \
     return hipGetLastError();                                                                     \
   }
   if constexpr (RAW) {
@@ -1497,7 +1522,8 @@ hipError_t dispatch_lut_step(const DecodeShape &sh, dim3 grid, HeadDesc *const *
 #define AQ_STEP(KB_, VB_)                                                                        \
   if (sh.k_bits == KB_ && sh.v_bits == VB_) {                                                     \
     decode_lut_kernel<P, KB_, VB_, false, true><<<grid, kLutThreads, 0, s>>>(descs, q, chunk, 1,  \
-                                                                            nullptr, out, app);   \
+                                                                            nullptr, out, app,    \
+                                                                            sh.dim);              \
     return hipGetLastError();                                                                     \
   }
   AQ_STEP(4, 2) AQ_STEP(4, 3) AQ_STEP(4, 4)
