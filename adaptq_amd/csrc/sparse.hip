@@ -91,6 +91,66 @@ __device__ __forceinline__ bool sign_plus(const uint32_t *signs, int i) {
 // normalise, sign+butterflies, * RN(1/RN(sqrt p)), * (sqrt p * ||q||).
 __device__ void rotate_query_exact(float *s_q, const float *q, int dim, int P,
                                    const uint32_t *signs, float inv_sqrt_p, float sqrt_p) {
+  if (P == 64 || P == 128) {
+    // one wave, lane l holding entries l and l + 64, the same operations in
+    // the same order: the squares' sum left to right (every lane runs the
+    // chain over the squares in LDS), the butterflies of span < 64 between
+    // lanes, span 64 inside the lane; no block barriers until the result
+    if (threadIdx.x < 64) {
+      const int lane = threadIdx.x;
+      const bool two = P == 128;
+      float v0 = lane < dim ? q[lane] : 0.0f;
+      float v1 = two && lane + 64 < dim ? q[lane + 64] : 0.0f;
+      s_q[lane] = __fmul_rn(v0, v0);
+      if (two) s_q[lane + 64] = __fmul_rn(v1, v1);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      float sq = 0.0f;
+      {
+        const float4 *q4 = reinterpret_cast<const float4 *>(s_q);
+        const int nb = dim / 16;
+        for (int b = 0; b < nb; ++b) {
+          float4 r[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) r[k] = q4[4 * b + k];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            sq = __fadd_rn(sq, r[k].x);
+            sq = __fadd_rn(sq, r[k].y);
+            sq = __fadd_rn(sq, r[k].z);
+            sq = __fadd_rn(sq, r[k].w);
+          }
+        }
+        for (int i = 16 * nb; i < dim; ++i) sq = __fadd_rn(sq, s_q[i]);
+      }
+      const float qn = sqrtf(__fadd_rn(sq, 1e-12f));
+      const float inv = 1.0f / qn;
+      v0 = __fmul_rn(v0, inv);
+      v1 = __fmul_rn(v1, inv);
+      if (!sign_plus(signs, lane)) v0 = -v0;
+      if (two && !sign_plus(signs, lane + 64)) v1 = -v1;
+#pragma unroll
+      for (int len = 1; len < 64; len <<= 1) {
+        const bool upper = (lane & len) != 0;
+        const float o0 = __shfl_xor(v0, len, 64), o1 = __shfl_xor(v1, len, 64);
+        v0 = upper ? __fsub_rn(o0, v0) : __fadd_rn(v0, o0);
+        v1 = upper ? __fsub_rn(o1, v1) : __fadd_rn(v1, o1);
+      }
+      if (two) {
+        const float lo = v0, hi = v1;
+        v0 = __fadd_rn(lo, hi);
+        v1 = __fsub_rn(lo, hi);
+      }
+      const float m = __fmul_rn(sqrt_p, qn);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();  // every lane has read the squares
+      s_q[lane] = __fmul_rn(__fmul_rn(v0, inv_sqrt_p), m);
+      if (two) s_q[lane + 64] = __fmul_rn(__fmul_rn(v1, inv_sqrt_p), m);
+    }
+    __syncthreads();
+    return;
+  }
   __shared__ float s_qn;
   for (int i = threadIdx.x; i < P; i += blockDim.x) s_q[i] = i < dim ? q[i] : 0.0f;
   __syncthreads();
@@ -139,6 +199,52 @@ __device__ void rotate_query_exact(float *s_q, const float *q, int dim, int P,
   const float m = __fmul_rn(sqrt_p, qn);
   for (int i = threadIdx.x; i < P; i += blockDim.x) s_q[i] = __fmul_rn(__fmul_rn(s_q[i], inv_sqrt_p), m);
   __syncthreads();
+}
+
+// The inverse FWHT of s_acc[0..P) (the block's LDS, complete) with the
+// signs, to out[0..dim): butterflies of span 1 .. P/2 as lo + hi, lo - hi,
+// then x * (1/sqrt(P)) and the sign D_i (fwht.cpp:106-134).  At padded 64
+// and 128 one wave does it with shuffles (the same operations in the same
+// order, lane l holding entries l and l + 64); the other waves return at
+// once, so no block barrier may follow a call.
+__device__ void inverse_fwht_out(float *s_acc, int P, int dim, const uint32_t *signs, float *out) {
+  if (P == 64 || P == 128) {
+    if (threadIdx.x >= 64) return;
+    const int lane = threadIdx.x;
+    const bool two = P == 128;
+    float v0 = s_acc[lane], v1 = two ? s_acc[lane + 64] : 0.0f;
+#pragma unroll
+    for (int len = 1; len < 64; len <<= 1) {
+      const bool upper = (lane & len) != 0;
+      const float o0 = __shfl_xor(v0, len, 64), o1 = __shfl_xor(v1, len, 64);
+      v0 = upper ? o0 - v0 : v0 + o0;
+      v1 = upper ? o1 - v1 : v1 + o1;
+    }
+    if (two) {
+      const float lo = v0, hi = v1;
+      v0 = lo + hi;
+      v1 = lo - hi;
+    }
+    const float scale = 1.0f / sqrtf((float)P);
+    const float w0 = __fmul_rn(v0, scale), w1 = __fmul_rn(v1, scale);
+    if (lane < dim) out[lane] = sign_plus(signs, lane) ? w0 : -w0;
+    if (two && lane + 64 < dim) out[lane + 64] = sign_plus(signs, lane + 64) ? w1 : -w1;
+    return;
+  }
+  for (int len = 1; len < P; len <<= 1) {
+    for (int k = threadIdx.x; k < P / 2; k += blockDim.x) {
+      const int jj = (k / len) * 2 * len + (k % len);
+      const float lo = s_acc[jj], hi = s_acc[jj + len];
+      s_acc[jj] = lo + hi;
+      s_acc[jj + len] = lo - hi;
+    }
+    __syncthreads();
+  }
+  const float scale = 1.0f / sqrtf((float)P);
+  for (int i = threadIdx.x; i < dim; i += blockDim.x) {
+    const float v = __fmul_rn(s_acc[i], scale);
+    out[i] = sign_plus(signs, i) ? v : -v;
+  }
 }
 
 template <int PT, int KB>
@@ -1519,20 +1625,7 @@ __global__ __launch_bounds__(kSelThreads) void sparse_fused_kernel(
     s_acc[j] = a;
   }
   __syncthreads();
-  for (int len = 1; len < PT; len <<= 1) {
-    for (int k = tid; k < PT / 2; k += blockDim.x) {
-      const int jj = (k / len) * 2 * len + (k % len);
-      const float lo = s_acc[jj], hi = s_acc[jj + len];
-      s_acc[jj] = lo + hi;
-      s_acc[jj + len] = lo - hi;
-    }
-    __syncthreads();
-  }
-  const float scale = 1.0f / sqrtf((float)PT);
-  for (int i = tid; i < dim; i += blockDim.x) {
-    const float v = __fmul_rn(s_acc[i], scale);
-    out[i] = sign_plus(d->signs, i) ? v : -v;
-  }
+  inverse_fwht_out(s_acc, PT, dim, d->signs, out);
 }
 
 // Codes per byte-aligned unit of a packed row and the unit's size in bytes:
@@ -1715,20 +1808,7 @@ __global__ __launch_bounds__(kThreads) void sparse_finish_kernel(HeadDesc *const
     }
   }
   __syncthreads();
-  for (int len = 1; len < P; len <<= 1) {
-    for (int k = threadIdx.x; k < P / 2; k += blockDim.x) {
-      const int jj = (k / len) * 2 * len + (k % len);
-      const float lo = s_acc[jj], hi = s_acc[jj + len];
-      s_acc[jj] = lo + hi;
-      s_acc[jj + len] = lo - hi;
-    }
-    __syncthreads();
-  }
-  const float scale = 1.0f / sqrtf((float)P);
-  for (int i = threadIdx.x; i < dim; i += blockDim.x) {
-    const float v = __fmul_rn(s_acc[i], scale);
-    out[i] = sign_plus(d->signs, i) ? v : -v;
-  }
+  inverse_fwht_out(s_acc, P, dim, d->signs, out);
 }
 
 // Per item: the logits, then the exponentials, then the weights (n floats),
