@@ -711,26 +711,40 @@ __device__ __forceinline__ void scan_counts(SelectShared &sh) {
   __syncthreads();
 }
 
-// Stable LSD radix sort, 8 bits a pass, of the n <= 2 kSelThreads keys
-// sh.key[0..n) with payloads sh.idx[0..n) (in: token order; out: sorted, in
-// the same arrays), skipping the digits every key shares (diff: OR ^ AND of
-// the keys).  Position r kSelThreads + t is thread t's in round r; a wave
-// ranks its keys of one digit with 8 ballots (lanes with the same digit
-// below it), leaders record the wave's count of each digit per round, and
-// one exclusive scan in (digit, round, wave) order gives every key its
+// Passes of sort_small<DB> for the differing bits diff: DB-bit digits whose
+// bits are not all shared.
+__device__ __forceinline__ int radix_passes(uint32_t diff, int db) {
+  int np = 0;
+  for (int sft = 0; sft < 32; sft += db) np += ((diff >> sft) & ((1u << db) - 1u)) != 0u;
+  return np;
+}
+
+// Stable LSD radix sort, DB (8 or 9) bits a pass, of the n <= 2 kSelThreads
+// keys sh.key[0..n) with payloads sh.idx[0..n) (in: token order; out:
+// sorted, in the same arrays), skipping the digits every key shares (diff:
+// OR ^ AND of the keys).  Position r kSelThreads + t is thread t's in round
+// r; a wave ranks its keys of one digit with DB ballots (lanes with the same
+// digit below it), leaders record the wave's count of each digit per round,
+// and one exclusive scan in (digit, round, wave) order gives every key its
 // destination.  sh.key / sh.idx from 4,096 on are the second buffer.
-__device__ __forceinline__ void sort8_small(SelectShared &sh, int n, uint32_t diff) {
+template <int DB>
+__device__ __forceinline__ void sort_small(SelectShared &sh, int n, uint32_t diff) {
   constexpr int R = 2;
-  constexpr int NE = 256 * R * (kSelThreads / 64);  // count entries, 8 per thread
-  static_assert(NE == 8 * kSelThreads, "8 count entries per thread");
+  constexpr int ND = 1 << DB;
+  constexpr int NE = ND * R * (kSelThreads / 64);  // count entries, 8 or 16 per thread
+  static_assert(NE == 8 * kSelThreads || NE == 16 * kSelThreads, "8 or 16 count entries per thread");
+  constexpr int EPT = NE / kSelThreads;
+  constexpr uint32_t DM = (uint32_t)ND - 1u;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint64_t below = (1ull << lane) - 1ull;
   uint32_t *kA = sh.key, *kB = sh.key + 4096;
   uint16_t *iA = sh.idx, *iB = sh.idx + 4096;
   uint16_t *cnt = sh.cnt;
-  for (int sft = 0; sft < 32; sft += 8) {
-    if (((diff >> sft) & 255u) == 0) continue;
-    reinterpret_cast<uint4 *>(cnt)[tid] = make_uint4(0u, 0u, 0u, 0u);
+  for (int sft = 0; sft < 32; sft += DB) {
+    if (((diff >> sft) & DM) == 0) continue;
+#pragma unroll
+    for (int j = 0; j < EPT / 8; ++j)
+      reinterpret_cast<uint4 *>(cnt)[(EPT / 8) * tid + j] = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
     uint32_t kk[R], dg[R], rk[R];
     uint16_t ii[R];
@@ -740,10 +754,10 @@ __device__ __forceinline__ void sort8_small(SelectShared &sh, int n, uint32_t di
       const bool valid = pos < n;
       kk[r] = valid ? kA[pos] : 0u;
       ii[r] = valid ? iA[pos] : (uint16_t)0;
-      dg[r] = (kk[r] >> sft) & 255u;
+      dg[r] = (kk[r] >> sft) & DM;
       uint64_t same = __ballot(valid);
 #pragma unroll
-      for (int b = 0; b < 8; ++b) {
+      for (int b = 0; b < DB; ++b) {
         const uint64_t m = __ballot((dg[r] >> b) & 1u);
         same &= ((dg[r] >> b) & 1u) ? m : ~m;
       }
@@ -752,7 +766,9 @@ __device__ __forceinline__ void sort8_small(SelectShared &sh, int n, uint32_t di
     }
     __syncthreads();
     // exclusive scan of the counts in (digit, round, wave) order
-    {
+    if constexpr (EPT == 16) {
+      scan_counts(sh);  // ends with a barrier
+    } else {
       uint4 *c4 = reinterpret_cast<uint4 *>(cnt) + tid;
       const uint4 a = *c4;
       uint32_t w[4] = {a.x, a.y, a.z, a.w};
@@ -775,8 +791,8 @@ __device__ __forceinline__ void sort8_small(SelectShared &sh, int n, uint32_t di
       for (int k = 0; k < wave; ++k) base += sh.wsum[k];
       const uint32_t b2 = base * 0x10001u;  // every prefix is below 2^16: no carry between halves
       *c4 = make_uint4(w[0] + b2, w[1] + b2, w[2] + b2, w[3] + b2);
+      __syncthreads();
     }
-    __syncthreads();
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if (r * kSelThreads + tid < n) {
@@ -808,8 +824,11 @@ __device__ __forceinline__ void sort8_small(SelectShared &sh, int n, uint32_t di
 //   2. e = expf(l - max) into LDS (expf_ref: the reference's libm expf, bit
 //      for bit); thread 0 adds them left to right
 //      (attention.cpp:422-426); p = e * (1/sum)
-//   3. stable LSD radix sort of the 32-bit keys, 4 bits a pass, skipping
-//      digits every key shares: order p descending, ties older first
+//   3. stable LSD radix sort of the 32-bit keys less the smallest one,
+//      skipping digits every key shares: order p descending, ties older
+//      first.  Up to 2 kSelThreads tokens: sort_small in LDS, 8 or 9 bits a
+//      pass (whichever needs fewer passes); above: 4 bits a pass, in
+//      registers
 //   4. quad sums ((p0+p1)+p2)+p3 of the sorted order in parallel; thread 0
 //      runs the mass loop over them, then the single tokens
 //      (attention.cpp:454-472)
@@ -848,14 +867,22 @@ __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, fl
   for (int e = 0; e < E; ++e) ev[e] = ef[p0 + e];
   __syncthreads();
 
+  // Keys are sorted less the smallest one, key_hi(inv): every e is at most
+  // 1 (or NaN), so every p = e inv is at most inv (or NaN, whose key is the
+  // largest), and the subtraction keeps the order.  The digits then cover
+  // only the key range.
+  const uint32_t kmin = key_hi(inv);
   uint32_t k[E], ix[E];
   uint32_t kor = 0, kand = 0xFFFFFFFFu;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    k[e] = p0 + e < n ? key_hi(__fmul_rn(ev[e], inv)) : 0xFFFFFFFFu;
+    const bool valid = p0 + e < n;
+    k[e] = valid ? key_hi(__fmul_rn(ev[e], inv)) - kmin : 0u;
     ix[e] = (uint32_t)(p0 + e);
-    kor |= k[e];
-    kand &= k[e];
+    if (valid) {
+      kor |= k[e];
+      kand &= k[e];
+    }
   }
   // digits every key shares do not move anything: skip their passes
   for (int off = 32; off > 0; off >>= 1) {
@@ -875,6 +902,7 @@ __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, fl
       a &= reinterpret_cast<uint32_t *>(sh.red)[w];
     }
     diff = o ^ a;
+    kor = o;
   }
   __syncthreads();
 
@@ -885,8 +913,16 @@ __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, fl
       sh.idx[p0 + e] = (uint16_t)ix[e];
     }
     __syncthreads();
-    sort8_small(sh, n, diff);
+    // 9-bit digits when they need fewer passes than 8-bit ones
+    if (radix_passes(diff, 9) < radix_passes(diff, 8)) sort_small<9>(sh, n, diff);
+    else sort_small<8>(sh, n, diff);
   } else {
+  // positions from n on sort after every token: the OR of the keys is at
+  // least each of them, shares their common digits, and stable order puts
+  // the later positions last among equal keys
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+    if (p0 + e >= n) k[e] = kor;
   for (int sft = 0; sft < 32; sft += 4) {
     if (((diff >> sft) & 15u) == 0) continue;
     // counts of each digit among this thread's tokens (8-bit fields) and the
@@ -934,21 +970,21 @@ __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, fl
 
   const int n_quads = n / 4;
   for (int q = tid; q < n_quads; q += blockDim.x)
-    sh.stage[q] = __fadd_rn(__fadd_rn(__fadd_rn(hi_p(sh.key[4 * q]), hi_p(sh.key[4 * q + 1])),
-                                      hi_p(sh.key[4 * q + 2])),
-                            hi_p(sh.key[4 * q + 3]));
+    sh.stage[q] = __fadd_rn(__fadd_rn(__fadd_rn(hi_p(sh.key[4 * q] + kmin), hi_p(sh.key[4 * q + 1] + kmin)),
+                                      hi_p(sh.key[4 * q + 2] + kmin)),
+                            hi_p(sh.key[4 * q + 3] + kmin));
   __syncthreads();
   // the mass loop, on one lane
   if (tid == 0) {
     float mass = 0.0f;
     int ii = 4 * mass_scan(sh.stage, n_quads, v_mass, &mass);
-    for (; ii < n && mass < v_mass; ++ii) mass = __fadd_rn(mass, hi_p(sh.key[ii]));
+    for (; ii < n && mass < v_mass; ++ii) mass = __fadd_rn(mass, hi_p(sh.key[ii] + kmin));
     sh.cut = ii;
   }
   __syncthreads();
   if (tid == 0) {
     const int ii = sh.cut;
-    sh.last = ii > 0 ? ((uint64_t)sh.key[ii - 1] << 32) | sh.idx[ii - 1] : 0;
+    sh.last = ii > 0 ? ((uint64_t)(sh.key[ii - 1] + kmin) << 32) | sh.idx[ii - 1] : 0;
   }
   __syncthreads();
   // The selection is the first cut keys of the sorted order, i.e. every key
