@@ -89,18 +89,33 @@ __device__ __forceinline__ bool sign_plus(const uint32_t *signs, int i) {
 
 // Query rotation with the reference's exact float steps: sequential ||q||^2,
 // normalise, sign+butterflies, * RN(1/RN(sqrt p)), * (sqrt p * ||q||).
+// The query entries lane l of wave 0 holds in rotate_query_exact's one-wave
+// path (P = 64 or 128): l and l + 64.  Loaded apart from the rotation so a
+// caller can issue them before other loads.
+__device__ __forceinline__ float2 query_lanes(const float *q, int dim, int P) {
+  const int lane = threadIdx.x;
+  float2 v = make_float2(0.0f, 0.0f);
+  if (lane < 64) {
+    if (lane < dim) v.x = q[lane];
+    if (P == 128 && lane + 64 < dim) v.y = q[lane + 64];
+  }
+  return v;
+}
+
 __device__ void rotate_query_exact(float *s_q, const float *q, int dim, int P,
-                                   const uint32_t *signs, float inv_sqrt_p, float sqrt_p) {
+                                   const uint32_t *signs, float inv_sqrt_p, float sqrt_p,
+                                   const float2 *preloaded = nullptr) {
   if (P == 64 || P == 128) {
     // one wave, lane l holding entries l and l + 64, the same operations in
     // the same order: the squares' sum left to right (every lane runs the
     // chain over the squares in LDS), the butterflies of span < 64 between
     // lanes, span 64 inside the lane; no block barriers until the result
+    const float2 qv = preloaded ? *preloaded : query_lanes(q, dim, P);
     if (threadIdx.x < 64) {
       const int lane = threadIdx.x;
       const bool two = P == 128;
-      float v0 = lane < dim ? q[lane] : 0.0f;
-      float v1 = two && lane + 64 < dim ? q[lane + 64] : 0.0f;
+      float v0 = qv.x;
+      float v1 = qv.y;
       s_q[lane] = __fmul_rn(v0, v0);
       if (two) s_q[lane + 64] = __fmul_rn(v1, v1);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -253,19 +268,69 @@ struct KRow {
 };
 
 // The row's words in reference byte order (PT = 64/128): 3-bit rows are
-// stored so; 2/4-bit rows are XOR-permuted by x = slot & mask.
+// stored so; 2/4-bit rows are XOR-permuted by x = slot & mask.  Two steps,
+// so the loads can be issued well before the words are used: kload_raw
+// reads the words in word order (x >> 2 undone), kperm_raw then undoes the
+// byte order inside each word (x & 3).
 template <int PT, int KB>
-__device__ __forceinline__ void kload_row(const uint8_t *row, int x, uint32_t *w) {
-  const uint32_t *r32 = reinterpret_cast<const uint32_t *>(row);
+__device__ __forceinline__ void kload_raw(const uint8_t *row, int x, uint32_t *w) {
+  constexpr int W = KRow<PT, KB>::words;
   if constexpr (KB == 3) {
+    // 24 or 48 bytes a row: 8-byte loads
+    const uint2 *r = reinterpret_cast<const uint2 *>(row);
 #pragma unroll
-    for (int i = 0; i < KRow<PT, KB>::words; ++i) w[i] = r32[i];
+    for (int i = 0; i < W / 2; ++i) {
+      const uint2 v = r[i];
+      w[2 * i] = v.x;
+      w[2 * i + 1] = v.y;
+    }
   } else {
+    // 16 to 64 bytes a row: 16-byte loads in stored order, then word i of
+    // the reference order is stored word i ^ (x >> 2), by one conditional
+    // swap per bit of x >> 2 (below XS)
+    constexpr int XS = (kperm_mask(PT, KB) + 1) / 4;
+    static_assert(W % 4 == 0 && XS <= W, "whole 16-byte groups");
+    const uint4 *r = reinterpret_cast<const uint4 *>(row);
+#pragma unroll
+    for (int i = 0; i < W / 4; ++i) {
+      const uint4 v = r[i];
+      w[4 * i] = v.x;
+      w[4 * i + 1] = v.y;
+      w[4 * i + 2] = v.z;
+      w[4 * i + 3] = v.w;
+    }
+    // (the swaps are byte permutes: written as selects, the compiler turns
+    // the stages back into one run-time index and a compare chain per word)
     const uint32_t xw = (uint32_t)x >> 2;
+    constexpr int NB = XS >= 8 ? 3 : XS >= 4 ? 2 : XS >= 2 ? 1 : 0;  // log2(XS)
+    static_assert((1 << NB) == XS || XS == 0, "XS is a power of two");
+#pragma unroll
+    for (int sb = 0; sb < NB; ++sb) {
+      const int b = 1 << sb;
+      // all bytes from the first operand (the partner word) or the second
+      const uint32_t sel = (xw & (uint32_t)b) ? 0x07060504u : 0x03020100u;
+#pragma unroll
+      for (int i = 0; i < W; ++i) {
+        if (i & b) continue;
+        const uint32_t lo = w[i], hi = w[i | b];
+        w[i] = __builtin_amdgcn_perm(hi, lo, sel);
+        w[i | b] = __builtin_amdgcn_perm(lo, hi, sel);
+      }
+    }
+  }
+}
+template <int PT, int KB>
+__device__ __forceinline__ void kperm_raw(int x, uint32_t *w) {
+  if constexpr (KB != 3) {
     const uint32_t sel = 0x03020100u ^ (((uint32_t)x & 3u) * 0x01010101u);
 #pragma unroll
-    for (int i = 0; i < KRow<PT, KB>::words; ++i) w[i] = __builtin_amdgcn_perm(0u, r32[i ^ xw], sel);
+    for (int i = 0; i < KRow<PT, KB>::words; ++i) w[i] = __builtin_amdgcn_perm(0u, w[i], sel);
   }
+}
+template <int PT, int KB>
+__device__ __forceinline__ void kload_row(const uint8_t *row, int x, uint32_t *w) {
+  kload_raw<PT, KB>(row, x, w);
+  kperm_raw<PT, KB>(x, w);
 }
 
 // dot(s_q, CB[codes]) of a row given as words in reference order, with the
@@ -635,6 +700,23 @@ __device__ int mass_scan(const float *q, int m, float v_mass, float *mass) {
   return taken;
 }
 
+// Sum of the totals of the waves before `wave` (NW of them in LDS, 16-byte
+// aligned): NW / 4 broadcast 16-byte reads rather than a chain of dependent
+// ones.
+template <int NW>
+__device__ __forceinline__ uint32_t waves_before(const uint32_t *wsum, int wave) {
+  static_assert(NW % 4 == 0, "whole 16-byte groups");
+  const uint4 *w4 = reinterpret_cast<const uint4 *>(wsum);
+  uint32_t b = 0u;
+#pragma unroll
+  for (int q = 0; q < NW / 4; ++q) {
+    const uint4 v = w4[q];
+    b += (4 * q < wave ? v.x : 0u) + (4 * q + 1 < wave ? v.y : 0u) +
+         (4 * q + 2 < wave ? v.z : 0u) + (4 * q + 3 < wave ? v.w : 0u);
+  }
+  return b;
+}
+
 // Shared memory of the select kernel.  The small path (n <= kLdsSort) keeps
 // 32-bit keys, 16-bit token indices and 16 x kSelThreads 16-bit radix counts;
 // the large path keeps its sort keys in the workspace.
@@ -656,7 +738,7 @@ struct SelectShared {
   };
   __align__(16) float stage[kStage];
   float red[kSelThreads];
-  uint32_t wsum[kSelThreads / 64];
+  __align__(16) uint32_t wsum[kSelThreads / 64];
   float bcast[2];
   int cut;
   uint64_t last;
@@ -703,8 +785,7 @@ __device__ __forceinline__ void scan_counts(SelectShared &sh) {
   }
   if (lane == 63) sh.wsum[wave] = incl;
   __syncthreads();
-  uint32_t base = incl - run;
-  for (int k = 0; k < wave; ++k) base += sh.wsum[k];
+  const uint32_t base = incl - run + waves_before<kSelThreads / 64>(sh.wsum, wave);
   const uint32_t b2 = base * 0x10001u;
   c4[0] = make_uint4(w[0] + b2, w[1] + b2, w[2] + b2, w[3] + b2);
   c4[1] = make_uint4(w[4] + b2, w[5] + b2, w[6] + b2, w[7] + b2);
@@ -750,6 +831,11 @@ __device__ __forceinline__ void sort_small(SelectShared &sh, int n, uint32_t dif
     uint16_t ii[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
+      kk[r] = 0u;
+      ii[r] = 0;
+      dg[r] = 0u;
+      rk[r] = 0u;
+      if (r * kSelThreads >= n) continue;  // no key in this round (uniform)
       const int pos = r * kSelThreads + tid;
       const bool valid = pos < n;
       kk[r] = valid ? kA[pos] : 0u;
@@ -787,8 +873,7 @@ __device__ __forceinline__ void sort_small(SelectShared &sh, int n, uint32_t dif
       }
       if (lane == 63) sh.wsum[wave] = incl;
       __syncthreads();
-      uint32_t base = incl - run;
-      for (int k = 0; k < wave; ++k) base += sh.wsum[k];
+      const uint32_t base = incl - run + waves_before<kSelThreads / 64>(sh.wsum, wave);
       const uint32_t b2 = base * 0x10001u;  // every prefix is below 2^16: no carry between halves
       *c4 = make_uint4(w[0] + b2, w[1] + b2, w[2] + b2, w[3] + b2);
       __syncthreads();
@@ -840,13 +925,12 @@ template <int E>
 __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, float *lg, int n, int s0,
                              SelectShared &sh, const float *lin = nullptr,
                              float *wout = nullptr) {
+  static_assert(E == 1 || E == 2 || E == 4 || E == 8, "tokens per thread");
   const int tid = threadIdx.x, p0 = tid * E;
   const int cap = d->cap, P = d->padded;
-  float ev[E], l_own[E];
+  float ev[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) ev[e] = p0 + e < n ? (lin ? lin[e] : lg[p0 + e]) : 0.0f;
-#pragma unroll
-  for (int e = 0; e < E; ++e) l_own[e] = ev[e];
   if (!wout) wout = lg;
   float mx = -1e30f;
 #pragma unroll
@@ -854,8 +938,15 @@ __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, fl
     if (p0 + e < n && ev[e] > mx) mx = ev[e];
   mx = block_max(mx, sh);
 
-  // (the exponentials wait in LDS, not in registers, while thread 0 adds)
-  float *ef = reinterpret_cast<float *>(sh.key);
+  // the exponentials' left-to-right sum (attention.cpp:422-426), one lane's
+  // chain (block_seq_sum is slower at these lengths: 4 heads x 2,048 tokens
+  // 8.9 -> 13.6 us).  The exponentials wait in LDS, not in registers,
+  // meanwhile.  Up to 4
+  // tokens a thread they stay there for the weights (step 5), above the keys
+  // the sort uses: sort_small's buffers sh.key[0, n) and [4096, 4096 + n)
+  // with n <= 2048, the 4-bit sort's sh.key[0, 4096).  At 8 a thread the
+  // weights recompute them from the logits in lg.
+  float *ef = reinterpret_cast<float *>(sh.key) + (E <= 2 ? 2048 : E == 4 ? 4096 : 0);
 #pragma unroll
   for (int e = 0; e < E; ++e)
     if (p0 + e < n) ef[p0 + e] = expf_ref(ev[e] - mx);
@@ -974,7 +1065,7 @@ __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, fl
                                       hi_p(sh.key[4 * q + 2] + kmin)),
                             hi_p(sh.key[4 * q + 3] + kmin));
   __syncthreads();
-  // the mass loop, on one lane
+  // the mass loop, on one lane (attention.cpp:454-472)
   if (tid == 0) {
     float mass = 0.0f;
     int ii = 4 * mass_scan(sh.stage, n_quads, v_mass, &mass);
@@ -988,9 +1079,10 @@ __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, fl
   }
   __syncthreads();
   // The selection is the first cut keys of the sorted order, i.e. every key
-  // up to the last one taken (keys are distinct).  Each thread recomputes its
-  // own tokens' p (the logits are still in lg; expf and the product give the
-  // same bits as before) and writes their weights in token order.
+  // up to the last one taken (keys are distinct).  Each thread forms its own
+  // tokens' p again (e from LDS, or at 8 tokens a thread from the logits
+  // still in lg: the same bits as before) and writes their weights in token
+  // order.
   const int cut = sh.cut;
   const uint64_t last = sh.last;
   const float isp = 1.0f / sqrtf((float)P);
@@ -1004,7 +1096,10 @@ __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, fl
   for (int e = 0; e < E; ++e) {
     const int t = p0 + e;
     if (t < n) {
-      const float p = __fmul_rn(expf_ref(l_own[e] - mx), inv);
+      // with 8 tokens a thread there are no logits in registers (lin is
+      // null: only sparse_select_kernel runs this width)
+      const float ee = E <= 4 ? ef[t] : expf_ref(lg[t] - mx);
+      const float p = __fmul_rn(ee, inv);
       const float w = cut > 0 && make_key(p, t) <= last ? __fmul_rn(__fmul_rn(p, vs[e]), isp) : 0.0f;
       wout[t] = w;
       if (wout != lg) lg[t] = w;  // the workspace keeps every launch's weights
@@ -1181,7 +1276,7 @@ __global__ __launch_bounds__(kRsThreads) void sparse_rsort_pass_kernel(int pass,
   constexpr int R = kRsRounds, NW = kRsWaves;
   __shared__ __align__(16) uint16_t s_wc[NW][kRsDigits];  // per-wave digit counts
   __shared__ uint32_t s_off[kRsDigits];
-  __shared__ uint32_t s_wsum[NW];
+  __shared__ __align__(16) uint32_t s_wsum[NW];
   RsPass rp;
   int np;
   uint32_t kmin;
@@ -1245,8 +1340,7 @@ __global__ __launch_bounds__(kRsThreads) void sparse_rsort_pass_kernel(int pass,
     uint4 *z4 = reinterpret_cast<uint4 *>(&s_wc[0][0]);
     for (int i = tid; i < NW * kRsDigits / 8; i += kRsThreads) z4[i] = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
-    uint32_t base = incl - mine;
-    for (int k = 0; k < wave; ++k) base += s_wsum[k];
+    const uint32_t base = incl - mine + waves_before<NW>(s_wsum, wave);
     s_off[2 * tid] = base + pre[0];
     s_off[2 * tid + 1] = base + tot[0] + pre[1];
   }
@@ -1561,6 +1655,7 @@ __device__ __forceinline__ int vcode_shift(int c) {
   else return 21 - 3 * c;
 }
 
+
 template <int PT, int KB, int VB, bool LOGITS_IN>
 __global__ __launch_bounds__(kSelThreads) void sparse_fused_kernel(
     HeadDesc *const *item_desc, const float *__restrict__ queries, float v_mass, float inv_sqrt_p,
@@ -1590,17 +1685,31 @@ __global__ __launch_bounds__(kSelThreads) void sparse_fused_kernel(
   float lreg[4];  // the thread's logits when computed here
   if constexpr (!LOGITS_IN) {
     // logits of the tokens select_small gives this thread (E per thread),
-    // handed over in registers
-    rotate_query_exact(s_q, queries + (size_t)item * dim, dim, PT, d->signs, inv_sqrt_p, sqrt_p);
-    const float attn_s = 1.0f / (sqrtf((float)dim) * (float)PT);
-    for (int e = 0; e < E; ++e) {
+    // handed over in registers; the query, then their K rows and scales
+    // are requested before the query rotation, which hides the rows'
+    // latency
+    constexpr int KW = KRow<PT, KB>::words;
+    const float2 qv = query_lanes(queries + (size_t)item * dim, dim, PT);
+    uint32_t kw[4][KW];
+    float ks[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
       const int t = tid * E + e;
-      if (t < n) {
+      if (e < E && t < n) {
         const int slot = ring_slot(s0, t, cap);
-        const float ks = d->k_scale[slot];  // issued with the row, not after the dot
-        const uint8_t *row = d->k_codes + (size_t)slot * d->k_pb;
-        const float dot = kdot_row<PT, KB>(row, slot & kperm_mask(PT, KB), s_q, PT, s_cbk);
-        lreg[e] = __fmul_rn(__fmul_rn(dot, attn_s), ks);
+        ks[e] = d->k_scale[slot];
+        kload_raw<PT, KB>(d->k_codes + (size_t)slot * d->k_pb, slot & kperm_mask(PT, KB), kw[e]);
+      }
+    }
+    rotate_query_exact(s_q, nullptr, dim, PT, d->signs, inv_sqrt_p, sqrt_p, &qv);
+    const float attn_s = 1.0f / (sqrtf((float)dim) * (float)PT);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int t = tid * E + e;
+      if (e < E && t < n) {
+        kperm_raw<PT, KB>(ring_slot(s0, t, cap) & kperm_mask(PT, KB), kw[e]);
+        const float dot = kdot_words<PT, KB>(kw[e], s_q, s_cbk);
+        lreg[e] = __fmul_rn(__fmul_rn(dot, attn_s), ks[e]);
       }
     }
   }
