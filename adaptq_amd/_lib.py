@@ -10,7 +10,9 @@ import ctypes as C
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libadaptq.so")
+# ADAPTQ_AMD_LIB names another build of the same ABI (bench.py --clock-stamps
+# sets it to the timing library, libadaptq_clk.so)
+LIB_PATH = os.environ.get("ADAPTQ_AMD_LIB") or os.path.join(_HERE, "libadaptq.so")
 
 _f = C.POINTER(C.c_float)
 _u8 = C.POINTER(C.c_uint8)

@@ -4,7 +4,10 @@
   adaptq_amd/adaptq_py*.so         pybind11 module (MHAContext), links the above
 
 Run ``python -m adaptq_amd.build`` or call :func:`build`.  Every call
-recompiles.
+recompiles.  ``python -m adaptq_amd.build --clock-stamps`` builds only
+adaptq_amd/libadaptq_clk.so, the same library with decode.hip compiled with
+AQ_CLOCK_STAMPS (per-block shader-clock stamps of the LUT decode kernel, read
+by ``bench.py --clock-stamps``); the product never loads it.
 """
 from __future__ import annotations
 
@@ -19,6 +22,7 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libadaptq.so")
+CLK_LIB = os.path.join(PKG, "libadaptq_clk.so")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"
@@ -63,6 +67,24 @@ def build_lib(jobs: int = 8) -> str:
     return LIB
 
 
+def build_clock_lib() -> str:
+    """libadaptq_clk.so: decode.hip with AQ_CLOCK_STAMPS, the other objects
+    from the last build_lib()."""
+    os.makedirs(BUILD, exist_ok=True)
+    obj = os.path.join(BUILD, "decode_clk.hip.o")
+    _run([HIPCC, *HIP_FLAGS, "-DAQ_CLOCK_STAMPS", "-x", "hip", "-c",
+          os.path.join(CSRC, "decode.hip"), "-o", obj])
+    objs = [obj] + [os.path.join(BUILD, s + ".o") for s in SOURCES if s != "decode.hip"]
+    missing = [o for o in objs if not os.path.exists(o)]
+    if missing:
+        raise RuntimeError(f"build the library first (missing {missing})")
+    tmp = CLK_LIB + ".tmp"
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp,
+          f"-Wl,-rpath,{ROCM}/lib", "-Wl,-soname,libadaptq.so"])
+    os.replace(tmp, CLK_LIB)
+    return CLK_LIB
+
+
 def build_pybind() -> str:
     import pybind11
 
@@ -84,5 +106,8 @@ def build(jobs: int = 8) -> None:
 
 
 if __name__ == "__main__":
-    build()
-    print("built", LIB)
+    if "--clock-stamps" in sys.argv[1:]:
+        print("built", build_clock_lib())
+    else:
+        build()
+        print("built", LIB)

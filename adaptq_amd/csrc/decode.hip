@@ -653,6 +653,42 @@ __device__ __forceinline__ void transpose_segments(uint32_t *x) {
   }
 }
 
+// Clock stamps, compiled only into the timing library (AQ_CLOCK_STAMPS,
+// `python -m adaptq_amd.build --clock-stamps`): thread 0 of every block of
+// decode_lut_kernel records s_memtime (shader clock cycles) and
+// s_memrealtime (the constant 100 MHz clock) at its start and end, into slot
+// [launch][block] of g_clk; the launch index is set beforehand by
+// adaptq_clock_stamp_set.  The clock a launch ran at is the ratio of the two
+// deltas summed over its blocks.
+#ifdef AQ_CLOCK_STAMPS
+constexpr int kClkLaunches = 32, kClkBlocks = 16384;
+__device__ unsigned long long g_clk[kClkLaunches * kClkBlocks * 4];
+__device__ int g_clk_launch;
+__global__ void clk_set_kernel(int i) { g_clk_launch = i; }
+#define AQ_CLK_BEGIN()                                     \
+  unsigned long long clk_c0 = 0, clk_r0 = 0;               \
+  int clk_l = 0;                                           \
+  if (!FUSE && threadIdx.x == 0) {                         \
+    clk_c0 = __builtin_amdgcn_s_memtime();                 \
+    clk_r0 = __builtin_amdgcn_s_memrealtime();             \
+    clk_l = g_clk_launch;                                  \
+  }
+#define AQ_CLK_END()                                                                             \
+  if (!FUSE && threadIdx.x == 0) {                                                               \
+    const unsigned long long c1 = __builtin_amdgcn_s_memtime();                                 \
+    const unsigned long long r1 = __builtin_amdgcn_s_memrealtime();                             \
+    const size_t b = ((size_t)(clk_l & (kClkLaunches - 1)) * kClkBlocks +                       \
+                      ((blockIdx.y * gridDim.x + blockIdx.x) & (kClkBlocks - 1))) * 4;          \
+    g_clk[b] = clk_c0;                                                                           \
+    g_clk[b + 1] = clk_r0;                                                                       \
+    g_clk[b + 2] = c1;                                                                           \
+    g_clk[b + 3] = r1;                                                                           \
+  }
+#else
+#define AQ_CLK_BEGIN()
+#define AQ_CLK_END()
+#endif
+
 // With n_splits == 1 the block owns its item and writes the final output
 // (outs) directly; otherwise it writes a partial for finalize_kernel.
 //
@@ -723,6 +759,7 @@ __global__ __launch_bounds__(kLutThreads, P <= 128 && (KB == 2 || KB == 4) ? 4 :
   const int grow = lane / G, gcol = lane % G;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t *signs = (const uint32_t *)d->signs;
+  AQ_CLK_BEGIN();
   if (t_begin >= t_end) {
     if (n_splits == 1) {
       for (int i = threadIdx.x; i < dim; i += blockDim.x) outs[(size_t)item * dim + i] = 0.0f;
@@ -1080,6 +1117,7 @@ __global__ __launch_bounds__(kLutThreads, P <= 128 && (KB == 2 || KB == 4) ? 4 :
       if (threadIdx.x == 0) item_desc[item]->st = ring_after(st0, 1, d->cap, d->hyb);
     }
     finish_item<VQ && !RAW>(s_q, P, dim, L, signs, outs + (size_t)item * dim, RAW, n);
+    AQ_CLK_END();
     return;
   }
   for (int i = threadIdx.x; i < P; i += blockDim.x) {
@@ -1093,6 +1131,7 @@ __global__ __launch_bounds__(kLutThreads, P <= 128 && (KB == 2 || KB == 4) ? 4 :
     part[0] = KQ ? M * 0.69314718055994530942f : M;
     part[1] = L;
   }
+  AQ_CLK_END();
 }
 
 // Code c of a packed row (generic unpack; restates quantizer.cpp:161-209).
@@ -1585,3 +1624,19 @@ hipError_t launch_decode_items(HeadDesc *const *descs, int n_items, const Decode
 }
 
 }  // namespace aq
+
+#ifdef AQ_CLOCK_STAMPS
+// The timing library's reader of the clock stamps (no counterpart in the
+// reference; declared nowhere else): set the launch index the next decode
+// launches record under, and copy the stamps out (n = kClkLaunches x
+// kClkBlocks x 4 words).
+extern "C" int adaptq_clock_stamp_set(int launch, void *stream) {
+  aq::clk_set_kernel<<<1, 1, 0, (hipStream_t)stream>>>(launch);
+  return (int)hipGetLastError();
+}
+extern "C" int adaptq_clock_stamp_read(unsigned long long *host, size_t n) {
+  const size_t cap = (size_t)aq::kClkLaunches * aq::kClkBlocks * 4;
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(aq::g_clk), (n < cap ? n : cap) * 8, 0,
+                                  hipMemcpyDeviceToHost);
+}
+#endif

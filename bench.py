@@ -629,6 +629,53 @@ def profiled_traffic(name="decode_lut_k4v2_d128_cfg5.md"):
         return None
 
 
+def clock_stamps(L, last_error, torch, np, plan, qp, op, stream, sptr, warmup, steps):
+    """Per decode launch: HIP-event ms and the shader clock, sum over blocks of
+    s_memtime deltas / sum of s_memrealtime deltas (100 MHz), from the timing
+    library's stamps (decode.hip, AQ_CLOCK_STAMPS)."""
+    import ctypes as C
+    n_launch, n_block = 32, 16384
+    tot = warmup + steps
+    if tot > n_launch:
+        sys.exit(f"bench: --clock-stamps records at most {n_launch} launches")
+    L.adaptq_clock_stamp_set.argtypes = [C.c_int, C.c_void_p]
+    L.adaptq_clock_stamp_set.restype = C.c_int
+    L.adaptq_clock_stamp_read.argtypes = [C.c_void_p, C.c_size_t]
+    L.adaptq_clock_stamp_read.restype = C.c_int
+    rate_hz = 100e6  # s_memrealtime
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(tot)]
+    torch.cuda.synchronize()
+    for i in range(tot):
+        assert L.adaptq_clock_stamp_set(i, sptr) == 0
+        a, b = evs[i]
+        a.record(stream)
+        assert L.adaptq_plan_compute_device(plan, qp, op, sptr) == 0, last_error()
+        b.record(stream)
+    torch.cuda.synchronize()
+    buf = np.zeros(n_launch * n_block * 4, np.uint64)
+    assert L.adaptq_clock_stamp_read(buf.ctypes.data, buf.size) == 0
+    buf = buf.reshape(n_launch, n_block, 4).astype(np.float64)
+    rows = []
+    for i in range(tot):
+        c0, r0, c1, r1 = buf[i, :, 0], buf[i, :, 1], buf[i, :, 2], buf[i, :, 3]
+        dc, dr = c1 - c0, r1 - r0
+        row = {"launch": i, "timed": i >= warmup,
+               "event_ms": round(evs[i][0].elapsed_time(evs[i][1]), 4),
+               "clock_ghz": round(float(dc.sum() / dr.sum() * rate_hz / 1e9), 4),
+               "span_ms": round(float((r1.max() - r0.min()) / rate_hz * 1e3), 4),
+               "block_us_median": round(float(np.median(dr)) / rate_hz * 1e6, 2)}
+        rows.append(row)
+        print(json.dumps(row), flush=True)
+    t = [r for r in rows if r["timed"]]
+    print(json.dumps({"clock_stamps": {
+        "timed_launches": len(t),
+        "event_ms_mean": float(np.mean([r["event_ms"] for r in t])),
+        "clock_ghz_mean": float(np.mean([r["clock_ghz"] for r in t])),
+        "clock_ghz_min": float(np.min([r["clock_ghz"] for r in t])),
+        "clock_ghz_max": float(np.max([r["clock_ghz"] for r in t]))}}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -643,6 +690,11 @@ def main():
     ap.add_argument("--only", default="",
                     help="comma-separated BASELINE configs 1-4 (e.g. C1,C3): run only those "
                          "secondary timings and print them (profiling runs)")
+    ap.add_argument("--clock-stamps", action="store_true",
+                    help="with the timing library (python -m adaptq_amd.build --clock-stamps): "
+                         "warmup + steps decode launches (at most 32), each one's HIP-event "
+                         "time and the shader clock from its blocks' s_memtime / s_memrealtime "
+                         "stamps; prints one JSON line per launch and a summary")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy 5 times (scales rocprof "
                          "FETCH_SIZE/WRITE_SIZE readings to bytes)")
@@ -666,6 +718,11 @@ def main():
         return
 
     sys.path.insert(0, ROOT)
+    if args.clock_stamps:
+        clk_lib = os.path.join(ROOT, "adaptq_amd", "libadaptq_clk.so")
+        if not os.path.exists(clk_lib):
+            sys.exit("bench: --clock-stamps needs python -m adaptq_amd.build --clock-stamps")
+        os.environ["ADAPTQ_AMD_LIB"] = clk_lib
     from adaptq_amd import _lib
     L = _lib.lib
     import ctypes as C
@@ -738,6 +795,13 @@ def main():
     q = torch.randn(H, dim, generator=g, device=dev)
     out = torch.empty(H, dim, device=dev)
     qp, op = C.c_void_p(q.data_ptr()), C.c_void_p(out.data_ptr())
+    if args.clock_stamps:
+        clock_stamps(L, _lib.last_error, torch, np, plan, qp, op, stream, sptr,
+                     args.warmup, args.steps)
+        L.adaptq_plan_destroy(plan)
+        for m in mhas:
+            L.adaptq_mha_destroy(m)
+        return
     for _ in range(args.warmup):
         assert L.adaptq_plan_compute_device(plan, qp, op, sptr) == 0, _lib.last_error()
     torch.cuda.synchronize()
