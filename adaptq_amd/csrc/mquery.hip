@@ -33,13 +33,17 @@
 // subtile at k-step r; the logits (one token per lane) reach that layout
 // through LDS.
 //
-// Block: 4 waves = 64 queries of one head over one token split; a wave owns
-// 16 queries.  Per 64-token tile the block stages into LDS, shared by its
-// waves: K dequantised to f32 rows [token][P + 4] (the 16-byte pad puts the
-// rows that 8 lanes read at once in 8 different bank groups), V dequantised
-// to f32 in [token][dim / 64][dim % 16][4] (lane (token, c) reads 4 output
-// tiles' values with one 16-byte load), the scales.  K rows stored in XOR
-// byte order (device.hpp kperm_mask) are restored while staging.
+// Block: kMqWaves (8) waves and kMqQueries (16) queries of one head over one
+// token split.  Every wave handles all 16 queries; the waves split the
+// tokens: wave w takes the 64-token tiles starting at t_begin + 64 w, then
+// every 64 kMqWaves tokens.  Lane l owns token l of its wave's tile: the K
+// row, dequantised through the codebook in LDS into registers (the next
+// tile's row requested a tile ahead; rows stored in XOR byte order,
+// device.hpp kperm_mask, are read back in reference order by load_k_row),
+// and the V slices the MFMA's B operand takes from global memory.  A wave's
+// logits reach the MFMA layout through its own LDS region (transposed, row
+// stride 17); at the end the waves' (m, l, acc) records meet in LDS and are
+// merged per query.
 #include <algorithm>
 
 #include "launch.hpp"
