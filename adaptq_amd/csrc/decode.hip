@@ -809,9 +809,10 @@ __global__ __launch_bounds__(kLutThreads, P <= 128 && (KB == 2 || KB == 4) ? 4 :
     if constexpr (VQ) vsc = v_scale[tt];
   }
 
-  load_query<P>(s_q, queries + (size_t)item * dim, dim, KQ, signs);
   // FUSE: waves 1 and 2 encode the step's key and value rows (LDS scratch of
   // the codec, its 4-bit bucket table per wave, the stored rows' copies)
+  // while wave 0 rotates the query; load_query's closing barrier publishes
+  // both
   constexpr bool kQ4 = FUSE && (KB == 4 || VB == 4);
   __shared__ Q4Entry s_app_q4[kQ4 ? 2 : 1][kQ4 ? kQ4Entries : 1];
   __shared__ __align__(16) float s_app_sq[FUSE ? 2 : 1][FUSE ? P : 1];
@@ -833,6 +834,7 @@ __global__ __launch_bounds__(kLutThreads, P <= 128 && (KB == 2 || KB == 4) ? 4 :
                                 s_app_code[side], s_app_row[side], &s_app_scale[side]);
     }
   }
+  load_query<P>(s_q, queries + (size_t)item * dim, dim, KQ, signs);
   // fixed-point scale of the K table (2/4-bit keys): f and 1/f
   __shared__ float s_fix[2];
   if constexpr (KPERM || NIB) {
