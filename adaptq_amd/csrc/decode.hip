@@ -28,8 +28,11 @@
 //   V: per-lane accumulators acc[p] in VGPRs, fed from a codebook-only table
 //      (byte -> 4 floats at 2 bits, byte -> 2 floats at 4 bits, 6-bit pair ->
 //      2 floats at 3 bits); reduced across lanes once per block.
+// Wide kernel (padded 512 and 1024, quantised K and V): a wave per token, the
+// row's dimensions over the lanes, a fixed-point K table per (code,
+// dimension).
 // Generic kernel (any padded up to 1024): one block-wide reduction per token
-// group; used for shapes the LUT kernel does not cover.
+// group; used for shapes the other kernels do not cover.
 #include <algorithm>
 
 #include "encode_one.hpp"
@@ -1314,6 +1317,234 @@ __global__ __launch_bounds__(kThreads) void decode_generic_kernel(
   }
 }
 
+// Wide kernel (padded 512 and 1024, quantised K and V): one wave per token at
+// a time, the row's dimensions spread over the lanes.  Lane l owns dimensions
+// [C l, C l + C), C = P / 64, so a row's codes arrive in one coalesced load
+// per wave (C KB / 8 bytes per lane).
+//   K: fixed-point table in LDS, entry (code c, dimension i) = trunc(f qr_i
+//      CB_K[c]) with f as in build_klut_fixed (so every partial sum of a
+//      row's entries stays below 2^29 in magnitude); a lane adds its C
+//      entries in int32 and the wave adds the lanes' sums by DPP, exactly.
+//      Plane c holds lane group g's C entries at words g (C + 1) .. (C + 1)
+//      g + C - 1: with the odd stride C + 1 the 64 lanes' reads of their k-th
+//      entry fall in 64 distinct banks whatever their codes.
+//   V: per-lane accumulators of the lane's C dimensions, codebook in LDS.
+// Each wave runs an online softmax (base 2) over its tokens, GT at a time;
+// the block merges its waves and writes (max, sum, acc[P]) for the finalize
+// kernel.  The LUT kernel's one lane per token needs a row's codes (and a
+// V accumulator per dimension segment) in one lane's registers, which at
+// these sizes do not fit.
+template <int NB>
+__device__ __forceinline__ void load_lane_bytes(const uint8_t *p, uint32_t (&w)[(NB + 3) / 4]) {
+  const AQ_AS1 uint8_t *g = (const AQ_AS1 uint8_t *)p;
+  if constexpr (NB == 2) {
+    w[0] = *reinterpret_cast<const AQ_AS1 uint16_t *>(g);
+  } else if constexpr (NB == 3) {
+    w[0] = (uint32_t)g[0] | ((uint32_t)g[1] << 8) | ((uint32_t)g[2] << 16);
+  } else if constexpr (NB == 4) {
+    w[0] = *reinterpret_cast<const AQ_AS1 uint32_t *>(g);
+  } else if constexpr (NB == 6) {
+    const AQ_AS1 uint16_t *h = reinterpret_cast<const AQ_AS1 uint16_t *>(g);
+    w[0] = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+    w[1] = h[2];
+  } else {
+    static_assert(NB == 8, "2, 3, 4, 6 or 8 bytes a lane");
+    const u32x2 v = *reinterpret_cast<const AQ_AS1 u32x2 *>(g);
+    w[0] = v.x;
+    w[1] = v.y;
+  }
+}
+
+// Code k of a lane's bytes (the row's bytes from the lane's first, as loaded
+// by load_lane_bytes): MSB-first in each byte at 2 and 4 bits, big-endian
+// 24-bit groups of 8 codes at 3 bits (quantizer.cpp:156-209).
+template <int B>
+__device__ __forceinline__ uint32_t lane_code(const uint32_t *w, int k) {
+  if constexpr (B == 4) {
+    return (byte_of(w, k >> 1) >> ((k & 1) ? 0 : 4)) & 15u;
+  } else if constexpr (B == 2) {
+    return (byte_of(w, k >> 2) >> (6 - 2 * (k & 3))) & 3u;
+  } else {
+    const int g = 3 * (k >> 3);
+    const uint32_t w24 = (byte_of(w, g) << 16) | (byte_of(w, g + 1) << 8) | byte_of(w, g + 2);
+    return (w24 >> (21 - 3 * (k & 7))) & 7u;
+  }
+}
+
+__device__ __forceinline__ int wave_isum(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, true);   // quad_perm [1,0,3,2]
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, true);   // quad_perm [2,3,0,1]
+  v += __builtin_amdgcn_update_dpp(0, v, 0x124, 0xf, 0xf, true);  // row_ror:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, true);  // row_ror:8
+  return (__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
+         (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
+}
+
+constexpr int kWideTokens = 4;  // tokens a wave takes per step
+
+template <int P, int KB, int VB>
+__global__ __launch_bounds__(kThreads) void decode_wide_kernel(HeadDesc *const *item_desc,
+                                                               const float *__restrict__ queries,
+                                                               int chunk, int n_splits,
+                                                               float *__restrict__ partials) {
+  static_assert(P == 512 || P == 1024, "padded 512 or 1024");
+  static_assert(KB >= 2 && KB <= 4 && VB >= 2 && VB <= 4, "quantised K and V");
+  constexpr int C = P / 64;             // dimensions a lane
+  constexpr int KBY = C * KB / 8, VBY = C * VB / 8;
+  constexpr int KRB = P * KB / 8, VRB = P * VB / 8;
+  constexpr int NC = 1 << KB;
+  constexpr int LS = C + 1;             // words of a lane group in a code plane
+  constexpr int PS = 64 * LS;           // words of a code plane
+  constexpr int GT = kWideTokens;
+  static_assert(NC * PS >= kWaves * P, "the waves' accumulators fit in the table's space");
+  __shared__ int32_t s_k[NC * PS];      // K table; after the tokens, the waves' acc[P]
+  __shared__ float s_q[P];
+  __shared__ float s_cbv[16];
+  __shared__ float s_ml[kWaves][2];
+  __shared__ float s_fix[2];
+  const int item = blockIdx.y, split = blockIdx.x;
+  const HeadDesc *d = item_desc[item];
+  const int dim = d->dim, n = d->st.size;
+  const int t_begin = split * chunk, t_end = min(n, t_begin + chunk);
+  float *part = partials + ((size_t)item * n_splits + split) * (P + 4);
+  if (t_begin >= t_end) {
+    for (int i = threadIdx.x; i < P; i += blockDim.x) part[4 + i] = 0.0f;
+    if (threadIdx.x == 0) {
+      part[0] = -INFINITY;
+      part[1] = 0.0f;
+    }
+    return;
+  }
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (threadIdx.x < (1 << VB)) s_cbv[threadIdx.x] = cbv<VB>(threadIdx.x);
+  load_query<P>(s_q, queries + (size_t)item * dim, dim, true, d->signs);  // ends with a barrier
+  if (wave == 0) {
+    float a = 0.0f;
+    for (int i = lane; i < P; i += 64) a += fabsf(s_q[i]);
+    a = wave_sum(a) * fabsf(cbv<KB>(0));  // the outermost centre has the largest magnitude
+    if (lane == 0) {
+      // the largest power of two f with f * max|CB| * sum|qr| <= 2^29
+      const float f = a > 0.0f ? ldexpf(1.0f, min(ilogbf(536870912.0f / a), 100)) : 1.0f;
+      s_fix[0] = f;
+      s_fix[1] = 1.0f / f;
+    }
+  }
+  __syncthreads();
+  {
+    const float f = s_fix[0];
+    // P is a multiple of the block size, so the code plane c is uniform per pass
+    for (int e = threadIdx.x; e < NC * P; e += kThreads) {
+      const int c = e / P, i = e - c * P;
+      s_k[c * PS + (i / C) * LS + i % C] = (int32_t)((s_q[i] * f) * cbv<KB>(c));
+    }
+  }
+  __syncthreads();
+
+  constexpr float kLog2e = 1.44269504088896340736f;
+  const float attn = kLog2e / (sqrtf((float)dim) * (float)P) * s_fix[1];
+  const float isp = 1.0f / sqrtf((float)P);
+  const uint8_t *krow = d->k_codes + lane * KBY;
+  const uint8_t *vrow = d->v_codes + lane * VBY;
+  const AQ_AS1 float *k_scale = (const AQ_AS1 float *)d->k_scale;
+  const AQ_AS1 float *v_scale = (const AQ_AS1 float *)d->v_scale;
+  const int32_t *tk = s_k + lane * LS;
+  float acc[C];
+#pragma unroll
+  for (int k = 0; k < C; ++k) acc[k] = 0.0f;
+  float m_run = kMaxSeed2, l_run = 0.0f;
+  // the next step's rows are requested before this step's are used
+  uint32_t kw[GT][(KBY + 3) / 4], vw[GT][(VBY + 3) / 4];
+  float ks[GT], vs[GT];
+  auto fetch = [&](int t0, uint32_t (&kx)[GT][(KBY + 3) / 4], uint32_t (&vx)[GT][(VBY + 3) / 4],
+                   float (&ksx)[GT], float (&vsx)[GT]) {
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      const size_t t = (size_t)min(t0 + g, t_end - 1);
+      load_lane_bytes<KBY>(krow + t * KRB, kx[g]);
+      load_lane_bytes<VBY>(vrow + t * VRB, vx[g]);
+      ksx[g] = k_scale[t];
+      vsx[g] = v_scale[t];
+    }
+  };
+  if (t_begin + wave * GT < t_end) fetch(t_begin + wave * GT, kw, vw, ks, vs);
+  for (int t0 = t_begin + wave * GT; t0 < t_end; t0 += kWaves * GT) {
+    uint32_t nkw[GT][(KBY + 3) / 4], nvw[GT][(VBY + 3) / 4];
+    float nks[GT], nvs[GT];
+    const int tn = t0 + kWaves * GT;
+    if (tn < t_end) fetch(tn, nkw, nvw, nks, nvs);
+    float lg[GT];
+    float gmax = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      int sum = 0;
+#pragma unroll
+      for (int k = 0; k < C; ++k) sum += tk[lane_code<KB>(kw[g], k) * PS + k];
+      sum = wave_isum(sum);
+      lg[g] = t0 + g < t_end ? (float)sum * attn * ks[g] : -INFINITY;
+      gmax = fmaxf(gmax, lg[g]);
+    }
+    if (gmax > m_run) {
+      const float alpha = __builtin_amdgcn_exp2f(m_run - gmax);
+#pragma unroll
+      for (int k = 0; k < C; ++k) acc[k] *= alpha;
+      l_run *= alpha;
+      m_run = gmax;
+    }
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      if (t0 + g >= t_end) break;
+      const float e = __builtin_amdgcn_exp2f(lg[g] - m_run);
+      l_run += e;
+      const float w = e * vs[g] * isp;
+#pragma unroll
+      for (int k = 0; k < C; ++k) acc[k] = fmaf(s_cbv[lane_code<VB>(vw[g], k)], w, acc[k]);
+    }
+    if (tn < t_end) {
+#pragma unroll
+      for (int g = 0; g < GT; ++g) {
+#pragma unroll
+        for (int i = 0; i < (KBY + 3) / 4; ++i) kw[g][i] = nkw[g][i];
+#pragma unroll
+        for (int i = 0; i < (VBY + 3) / 4; ++i) vw[g][i] = nvw[g][i];
+        ks[g] = nks[g];
+        vs[g] = nvs[g];
+      }
+    }
+  }
+
+  // ---- block merge: waves -> one (m, l, acc) ----
+  __syncthreads();  // every wave is done with the K table
+  float *s_acc = reinterpret_cast<float *>(s_k);  // [kWaves][P]
+#pragma unroll
+  for (int k = 0; k < C; ++k) s_acc[wave * P + lane * C + k] = acc[k];
+  if (lane == 0) {
+    s_ml[wave][0] = m_run;
+    s_ml[wave][1] = l_run;
+  }
+  __syncthreads();
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_ml[w][0]);
+  float fw[kWaves], L = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    fw[w] = s_ml[w][0] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s_ml[w][0] - M);
+    L += fw[w] * s_ml[w][1];
+  }
+  for (int i = threadIdx.x; i < P; i += kThreads) {
+    float a = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) a += fw[w] * s_acc[w * P + i];
+    part[4 + i] = a;
+  }
+  if (threadIdx.x == 0) {
+    // the finalize kernel merges splits in natural units
+    part[0] = M * 0.69314718055994530942f;
+    part[1] = L;
+  }
+}
+
 // Merge the splits of each item, normalise, undo the rotation.  The split
 // maxima, weights and sums are spread over the block (split s on thread
 // s mod kThreads); each dimension's weighted sum over the splits is shared by
@@ -1477,8 +1708,30 @@ hipError_t dispatch_generic(const DecodeShape &sh, dim3 grid, HeadDesc *const *d
   return hipErrorInvalidValue;
 }
 
+template <int P>
+hipError_t dispatch_wide(const DecodeShape &sh, dim3 grid, HeadDesc *const *descs, const float *q,
+                         int chunk, int splits, float *part, hipStream_t s) {
+#define AQ_WIDE(KB_, VB_)                                                                        \
+  if (sh.k_bits == KB_ && sh.v_bits == VB_) {                                                    \
+    decode_wide_kernel<P, KB_, VB_><<<grid, kThreads, 0, s>>>(descs, q, chunk, splits, part);     \
+    return hipGetLastError();                                                                    \
+  }
+  AQ_WIDE(4, 2) AQ_WIDE(4, 3) AQ_WIDE(4, 4)
+  AQ_WIDE(3, 2) AQ_WIDE(3, 3) AQ_WIDE(3, 4)
+  AQ_WIDE(2, 2) AQ_WIDE(2, 3) AQ_WIDE(2, 4)
+#undef AQ_WIDE
+  return hipErrorInvalidValue;
+}
+
+// The wide kernel serves padded 512 and 1024 with quantised K and V.
+bool wide_eligible(const DecodeShape &sh) {
+  return !sh.raw && (sh.padded == 512 || sh.padded == 1024) && sh.k_bits >= 2 && sh.k_bits <= 4 &&
+         sh.v_bits >= 2 && sh.v_bits <= 4;
+}
+
 // The LUT kernel serves padded 64, 128 and 256 (raw mirrors only when
-// unpadded); everything else takes the generic kernel.
+// unpadded), the wide kernel padded 512 and 1024 with quantised K and V;
+// everything else takes the generic kernel.
 bool lut_eligible(const DecodeShape &sh) {
   if (!((sh.padded == 64 || sh.padded == 128 || sh.padded == 256) &&
         (!sh.raw || sh.dim == sh.padded)))
@@ -1507,6 +1760,10 @@ SplitPlan decode_plan(int n_items, const DecodeShape &sh) {
   // 8,192 tokens 35 -> 25 us, 8 heads x 32,768 tokens 28 -> 25 us against a
   // target of 1,024 blocks; none of the sampled shapes slower).
   if (lut) return plan_splits(n_items, max_n, kLutWaves * kTile, 256);
+  // wide kernel: each block builds a table of 2^KB x P entries, so a block
+  // takes at least 512 tokens; 4 blocks a CU at padded 512 (a 4-bit table
+  // takes 36 KB of LDS), 2 at padded 1024 (68 KB)
+  if (wide_eligible(sh)) return plan_splits(n_items, max_n, 512, sh.padded == 512 ? 1024 : 512);
   return plan_splits(n_items, max_n, 256, 1024);
 }
 
@@ -1611,6 +1868,9 @@ hipError_t launch_decode_items(HeadDesc *const *descs, int n_items, const Decode
       e = raw ? dispatch_lut<128, true>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, d_out, s)
               : dispatch_lut<128, false>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, d_out, s);
     if (e != hipSuccess || sp.splits == 1) return e;  // one split: the kernel finished the items
+  } else if (wide_eligible(sh)) {
+    e = sh.padded == 512 ? dispatch_wide<512>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, s)
+                         : dispatch_wide<1024>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, s);
   } else {
     e = raw ? dispatch_generic<true>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, s)
             : dispatch_generic<false>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, s);

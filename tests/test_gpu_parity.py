@@ -277,6 +277,17 @@ DECODE_CASES = [
     (256, 4, 16, 700, 700),
     (256, 16, 16, 256, 300),
     (200, 16, 3, 400, 400),
+    # padded 512 and 1024 through the wide kernel (quantised K and V): a
+    # wrapped ring over several splits, unpadded dims, every K width, a ring
+    # shorter than one step of the block's waves
+    (512, 4, 2, 3000, 4100),
+    (300, 3, 3, 700, 700),
+    (512, 2, 4, 1500, 1500),
+    (1024, 4, 4, 2000, 2600),
+    (1000, 2, 3, 600, 600),
+    (600, 3, 2, 300, 13),
+    # and fp32 keys there still take the generic kernel
+    (512, 16, 2, 300, 300),
 ]
 
 
