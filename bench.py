@@ -74,13 +74,15 @@ class _CpuRef:
     reference build, the CPU restatement (oracle/) stands in, looped from
     Python, and the figures are marked kind "port"."""
 
-    def __init__(self):
+    def __init__(self, path=None):
         import numpy as np
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         # test infrastructure: the baseline only
         from bind import Oracle, Ref, REF_SO, fptr
         self.np, self.fptr = np, fptr
-        if os.path.exists(REF_SO):
+        if path is not None:
+            self.L, self.kind = Ref(path).lib, "reference"
+        elif os.path.exists(REF_SO):
             self.L, self.kind = Ref().lib, "reference"
         else:
             self.L, self.kind = Oracle().lib, "port"
@@ -136,6 +138,13 @@ def _timed_threads(work, n_threads, seconds):
     return sum(done) / (max(t_end) - t0)
 
 
+# The reference built with its CMake flags (the baseline's value) and with
+# setup.py's, as the pip package builds it on an AVX2 host (oracle/Makefile).
+REF_CMAKE_FLAGS = "-std=c++17 -O3 -ffp-contract=off (CMakeLists.txt:17)"
+REF_AVX2_SO = os.path.join(ROOT, "oracle", "_ref", "libadaptq_ref_avx2.so")
+REF_AVX2_FLAGS = "-std=c++17 -O3 -fopenmp -march=x86-64-v3 (setup.py:25, :38 with x86-64-v3 for native)"
+
+
 def cpu_baseline(cfg, seconds=12.0, seed=0):
     """The reference's CPU path on this host, on a bounded sample of the bench
     workload: heads of the bench shape (d128 K4/V2, 8,192 tokens, v_mass 0,
@@ -143,8 +152,10 @@ def cpu_baseline(cfg, seconds=12.0, seed=0):
     again; decode: compute() again and again over a full ring.  Each is timed
     on one thread (the reference's execution model: the Engine walks heads
     serially) and on one thread per usable CPU (independent heads; the
-    reference's C ABI allows concurrent calls on different handles).
-    `seconds` is split over the four timings."""
+    reference's C ABI allows concurrent calls on different handles), with the
+    reference built by its CMake flags; the pip package's flavour (setup.py's
+    flags) is timed beside it on all threads when that build is present.
+    `seconds` is split over the six timings."""
     np = __import__("numpy")
     ref = _CpuRef()
     cpus = host_cpus()
@@ -167,7 +178,7 @@ def cpu_baseline(cfg, seconds=12.0, seed=0):
         ref.compute(heads[i], q[i], outs[i], reps)
         return float(reps * n)
 
-    quarter = seconds / 4
+    quarter = seconds / 6
     app1 = _timed_threads(append_work, 1, quarter)
     appT = _timed_threads(append_work, T, quarter)  # also leaves every ring full
     dec1 = _timed_threads(decode_work, 1, quarter)
@@ -175,8 +186,21 @@ def cpu_baseline(cfg, seconds=12.0, seed=0):
     for h in heads:
         ref.destroy(h)
     db, ab = decode_bytes_per_token(dim, kb, vb), append_bytes_per_token(dim, dim, kb, vb)
+    avx2 = None
+    if ref.kind == "reference" and os.path.exists(REF_AVX2_SO):
+        ref = _CpuRef(REF_AVX2_SO)
+        heads = [ref.create(dim, kb, vb, n, 1000 + h) for h in range(T)]
+        appA = _timed_threads(append_work, T, quarter)
+        decA = _timed_threads(decode_work, T, quarter)
+        for h in heads:
+            ref.destroy(h)
+        avx2 = {"build": REF_AVX2_FLAGS, "threads": T,
+                "decode": {"token_heads_per_s": decA, "gb_per_s": decA * db / 1e9},
+                "append": {"token_heads_per_s": appA, "gb_per_s": appA * ab / 1e9}}
     return {
         "value": decT, "unit": "token*heads/s", "cores": T, "threads": T, "kind": ref.kind,
+        "build": REF_CMAKE_FLAGS if ref.kind == "reference" else "oracle/ restatement",
+        "setup_py_flavour": avx2,
         "sample": f"{T} heads (one per thread) x {n} tokens, d{dim} K{kb}/V{vb}, v_mass=0, "
                   f"hybrid=0; append = reset + {n} rows, decode = compute() over the full "
                   f"ring, each repeated ~{quarter:.1f}s on 1 thread and ~{quarter:.1f}s on "
@@ -846,6 +870,10 @@ def main():
     if cpu is not None:
         cpu["decode"]["gpu_over_cpu"] = value / cpu["decode"]["token_heads_per_s"]
         cpu["append"]["gpu_over_cpu"] = append_rate / cpu["append"]["token_heads_per_s"]
+        if cpu.get("setup_py_flavour"):
+            fl = cpu["setup_py_flavour"]
+            fl["decode"]["gpu_over_cpu"] = value / fl["decode"]["token_heads_per_s"]
+            fl["append"]["gpu_over_cpu"] = append_rate / fl["append"]["token_heads_per_s"]
         if not args.no_cpu_configs:
             cpu["configs"] = cpu_configs(cpu["threads"])
 
