@@ -1321,10 +1321,15 @@ __global__ __launch_bounds__(kThreads) void decode_generic_kernel(
 // a time, the row's dimensions spread over the lanes.  Lane l owns dimensions
 // [C l, C l + C), C = P / 64, so a row's codes arrive in one coalesced load
 // per wave (C KB / 8 bytes per lane).
-//   K: fixed-point table in LDS, entry (code c, dimension i) = trunc(f qr_i
-//      CB_K[c]) with f as in build_klut_fixed (so every partial sum of a
-//      row's entries stays below 2^29 in magnitude); a lane adds its C
+//   K: fixed-point table in LDS, entry (code c, dimension i) = f qr_i
+//      CB_K[c] rounded to the nearest integer, f the largest power of two
+//      with f max|CB| sum_i |qr_i| <= 2^30 (so every partial sum of a row's
+//      entries stays below 2^30 + P / 2 in magnitude); a lane adds its C
 //      entries in int32 and the wave adds the lanes' sums by DPP, exactly.
+//      The one-lane-per-token LUT kernel's byte entries cover two or four
+//      codes each; here a row adds P entries, so rounding (rather than
+//      truncating) and the larger scale keep the sum's error near the fp32
+//      dot product's.
 //      Plane c holds lane group g's C entries at words g (C + 1) .. (C + 1)
 //      g + C - 1: with the odd stride C + 1 the 64 lanes' reads of their k-th
 //      entry fall in 64 distinct banks whatever their codes.
@@ -1424,8 +1429,8 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(HeadDesc *const *
     for (int i = lane; i < P; i += 64) a += fabsf(s_q[i]);
     a = wave_sum(a) * fabsf(cbv<KB>(0));  // the outermost centre has the largest magnitude
     if (lane == 0) {
-      // the largest power of two f with f * max|CB| * sum|qr| <= 2^29
-      const float f = a > 0.0f ? ldexpf(1.0f, min(ilogbf(536870912.0f / a), 100)) : 1.0f;
+      // the largest power of two f with f * max|CB| * sum|qr| <= 2^30
+      const float f = a > 0.0f ? ldexpf(1.0f, min(ilogbf(1073741824.0f / a), 100)) : 1.0f;
       s_fix[0] = f;
       s_fix[1] = 1.0f / f;
     }
@@ -1436,7 +1441,7 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(HeadDesc *const *
     // P is a multiple of the block size, so the code plane c is uniform per pass
     for (int e = threadIdx.x; e < NC * P; e += kThreads) {
       const int c = e / P, i = e - c * P;
-      s_k[c * PS + (i / C) * LS + i % C] = (int32_t)((s_q[i] * f) * cbv<KB>(c));
+      s_k[c * PS + (i / C) * LS + i % C] = (int32_t)rintf((s_q[i] * f) * cbv<KB>(c));
     }
   }
   __syncthreads();

@@ -102,6 +102,24 @@ def config4_queries():
     return _normal(rng, (64, 8, 128))
 
 
+# Padded 512 and 1024 (the library's wide decode kernel): N(0,1) rings, the
+# second wrapped (1,300 tokens into 1,024 slots).
+WIDE = {
+    "wide512": dict(n_heads=4, dim=512, k_bits=4, v_bits=2, cap=2048, base_seed=51, n=2048),
+    "wide1000": dict(n_heads=2, dim=1000, k_bits=3, v_bits=4, cap=1024, base_seed=52, n=1300),
+}
+
+
+def wide_inputs(name: str):
+    """(K[n,h,dim], V[n,h,dim], q[h,dim]) of a WIDE case."""
+    c = WIDE[name]
+    rng = np.random.default_rng([5, c["dim"]])
+    K = _normal(rng, (c["n"], c["n_heads"], c["dim"]))
+    V = _normal(rng, (c["n"], c["n_heads"], c["dim"]))
+    q = _normal(rng, (c["n_heads"], c["dim"]))
+    return K, V, q
+
+
 # ---------------------------------------------------------- codec families
 FAMILIES = ["normal", "student_t", "outliers", "zeros", "huge", "tiny", "nan", "inf",
             "negzero", "mixed"]

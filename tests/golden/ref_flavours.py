@@ -32,6 +32,8 @@ and writes tests/golden/ref_flavours.json:
            dequantised ring (K^ = scale D H CB[codes] / p, fp32 keys as
            stored), configs 1-4 with v_mass = 0 and hybrid 0: how far the
            reference's own fp32 results sit from the exact value
+  The WIDE cases of inputs.py (padded 512 and 1024) add to rings, outputs,
+  floor and exact with v_mass 0 and hybrid 0.
 
     make -C oracle ref flavours && python tests/golden/ref_flavours.py
 """
@@ -109,6 +111,17 @@ def heads_of(cfg_name, r, vm, hyb):
                 for t in range(c["bulk"] + 1):  # the bulk, then step 0's token
                     hd.append(K[t, h], V[t, h], t)
                 out.append((f"l{layer}h{h}", hd, Q[0, h], (kb, vb, I.mha_seed(base, h))))
+    elif cfg_name in I.WIDE:
+        c = I.WIDE[cfg_name]
+        K, V, q = I.wide_inputs(cfg_name)
+        base = c["base_seed"]
+        hs = [r.head(c["dim"], c["k_bits"], c["v_bits"], c["cap"], I.mha_seed(base, h), vm, hyb)
+              for h in range(c["n_heads"])]
+        for t in range(c["n"]):
+            for h, hd in enumerate(hs):
+                hd.append(K[t, h], V[t, h], t)
+        out = [(f"h{h}", hd, q[h], (c["k_bits"], c["v_bits"], I.mha_seed(base, h)))
+               for h, hd in enumerate(hs)]
     else:
         c = I.CONFIG4
         Q = I.config4_queries()
@@ -147,9 +160,9 @@ def ring_diff(a, b):
 def configs(refs):
     cb = {b: Oracle().codebook(b).astype(np.float64) for b in (2, 3, 4)}
     rings, outs, floor, ex = {}, {}, {}, {}
-    for cfg in ("config1", "config2", "config3", "config4"):
+    for cfg in ("config1", "config2", "config3", "config4") + tuple(I.WIDE):
         print(cfg, flush=True)
-        for vm, hyb in MODES:
+        for vm, hyb in (MODES if cfg.startswith("config") else MODES[:1]):
             tag = f"{cfg}_vm{int(vm * 100)}_h{hyb}"
             per = {f: heads_of(cfg, r, vm, hyb) for f, r in refs.items() if f != "scalar" or vm == 0.0}
             base = per["base"]

@@ -4,7 +4,8 @@ An fp32 decode of a packed ring approximates the float64 softmax attention
 over the dequantised ring (tests/golden/exact64.py).  The reference's AVX2
 path and its scalar path (attention.cpp:606-659) each sit some distance from
 that exact value; tests/golden/ref_flavours.json records those distances for
-configs 1-4 (v_mass 0, hybrid 0), measured on the reference build by
+configs 1-4 and two rings at padded 512 and 1024 (v_mass 0, hybrid 0),
+measured on the reference build by
 tests/golden/ref_flavours.py.  Here the library decodes the same rings and
 its distance to the exact value, norm-wise (max|y - x| / max|x|) and
 elementwise (max |y - x| / |x| over entries with |x| >= 1e-3 max|x|), worst
@@ -70,6 +71,16 @@ def cfg_heads(name):
                 for h in range(c["n_heads"]):
                     m.append(h, K[t, h], V[t, h], t)
             yield m, [(h, Q[0, h], I.mha_seed(base, h), kb, vb) for h in range(c["n_heads"])]
+    elif name in I.WIDE:
+        c = I.WIDE[name]
+        K, V, q = I.wide_inputs(name)
+        base = c["base_seed"]
+        m = Mha(c["n_heads"], c["dim"], c["k_bits"], c["v_bits"], c["cap"], base, 0.0, 0)
+        for t in range(c["n"]):
+            for h in range(c["n_heads"]):
+                m.append(h, K[t, h], V[t, h], t)
+        yield m, [(h, q[h], I.mha_seed(base, h), c["k_bits"], c["v_bits"])
+                  for h in range(c["n_heads"])]
     else:
         c = I.CONFIG4
         Q = I.config4_queries()
@@ -83,7 +94,7 @@ def cfg_heads(name):
                   for qi in range(8) for h in range(c["n_heads"])]
 
 
-@pytest.mark.parametrize("name", ["config1", "config2", "config3", "config4"])
+@pytest.mark.parametrize("name", ["config1", "config2", "config3", "config4", "wide512", "wide1000"])
 def test_distance_to_exact_within_reference_spread(oracle, name):
     print(f"{name}: GPU and reference against exact attention", flush=True)
     cb = {b: oracle.codebook(b).astype(np.float64) for b in (2, 3, 4)}
