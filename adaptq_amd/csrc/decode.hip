@@ -1405,6 +1405,7 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(HeadDesc *const *
   __shared__ int32_t s_k[NC * PS];      // K table; after the tokens, the waves' acc[P]
   __shared__ float s_q[P];
   __shared__ float s_cbv[16];
+  __shared__ float2 s_cbv2[16];  // 2-bit V: nibble -> its two codes' centres
   __shared__ float s_ml[kWaves][2];
   __shared__ float s_fix[2];
   const int item = blockIdx.y, split = blockIdx.x;
@@ -1423,6 +1424,8 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(HeadDesc *const *
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (threadIdx.x < (1 << VB)) s_cbv[threadIdx.x] = cbv<VB>(threadIdx.x);
+  if (VB == 2 && threadIdx.x < 16)
+    s_cbv2[threadIdx.x] = make_float2(cbv<2>(threadIdx.x >> 2), cbv<2>(threadIdx.x & 3));
   load_query<P>(s_q, queries + (size_t)item * dim, dim, true, d->signs);  // ends with a barrier
   if (wave == 0) {
     float a = 0.0f;
@@ -1458,35 +1461,35 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(HeadDesc *const *
 #pragma unroll
   for (int k = 0; k < C; ++k) acc[k] = 0.0f;
   float m_run = kMaxSeed2, l_run = 0.0f;
-  // the next step's rows are requested before this step's are used
-  uint32_t kw[GT][(KBY + 3) / 4], vw[GT][(VBY + 3) / 4];
-  float ks[GT], vs[GT];
-  auto fetch = [&](int t0, uint32_t (&kx)[GT][(KBY + 3) / 4], uint32_t (&vx)[GT][(VBY + 3) / 4],
-                   float (&ksx)[GT], float (&vsx)[GT]) {
+  // A step takes GT tokens; the next step's rows are requested before this
+  // step's are used, into the other of two register sets (the loop runs two
+  // steps an iteration, so no set is copied).
+  struct Rows {
+    uint32_t k[GT][(KBY + 3) / 4], v[GT][(VBY + 3) / 4];
+    float ks[GT], vs[GT];
+  };
+  auto fetch = [&](int t0, Rows &r) {
 #pragma unroll
     for (int g = 0; g < GT; ++g) {
       const size_t t = (size_t)min(t0 + g, t_end - 1);
-      load_lane_bytes<KBY>(krow + t * KRB, kx[g]);
-      load_lane_bytes<VBY>(vrow + t * VRB, vx[g]);
-      ksx[g] = k_scale[t];
-      vsx[g] = v_scale[t];
+      load_lane_bytes<KBY>(krow + t * KRB, r.k[g]);
+      load_lane_bytes<VBY>(vrow + t * VRB, r.v[g]);
+      r.ks[g] = k_scale[t];
+      r.vs[g] = v_scale[t];
     }
   };
-  if (t_begin + wave * GT < t_end) fetch(t_begin + wave * GT, kw, vw, ks, vs);
-  for (int t0 = t_begin + wave * GT; t0 < t_end; t0 += kWaves * GT) {
-    uint32_t nkw[GT][(KBY + 3) / 4], nvw[GT][(VBY + 3) / 4];
-    float nks[GT], nvs[GT];
-    const int tn = t0 + kWaves * GT;
-    if (tn < t_end) fetch(tn, nkw, nvw, nks, nvs);
+  constexpr int kStep = kWaves * GT;
+  auto step = [&](int t0, const Rows &r, Rows &next) {
+    if (t0 + kStep < t_end) fetch(t0 + kStep, next);
     float lg[GT];
     float gmax = -INFINITY;
 #pragma unroll
     for (int g = 0; g < GT; ++g) {
       int sum = 0;
 #pragma unroll
-      for (int k = 0; k < C; ++k) sum += tk[lane_code<KB>(kw[g], k) * PS + k];
+      for (int k = 0; k < C; ++k) sum += tk[lane_code<KB>(r.k[g], k) * PS + k];
       sum = wave_isum(sum);
-      lg[g] = t0 + g < t_end ? (float)sum * attn * ks[g] : -INFINITY;
+      lg[g] = t0 + g < t_end ? (float)sum * attn * r.ks[g] : -INFINITY;
       gmax = fmaxf(gmax, lg[g]);
     }
     if (gmax > m_run) {
@@ -1501,21 +1504,28 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(HeadDesc *const *
       if (t0 + g >= t_end) break;
       const float e = __builtin_amdgcn_exp2f(lg[g] - m_run);
       l_run += e;
-      const float w = e * vs[g] * isp;
+      const float w = e * r.vs[g] * isp;
+      if constexpr (VB == 2) {
+        // two codes a read: the nibble's pair of centres (s_cbv2)
 #pragma unroll
-      for (int k = 0; k < C; ++k) acc[k] = fmaf(s_cbv[lane_code<VB>(vw[g], k)], w, acc[k]);
-    }
-    if (tn < t_end) {
+        for (int k = 0; k < C; k += 2) {
+          const float2 cv = s_cbv2[(byte_of(r.v[g], k >> 2) >> (4 - 2 * (k & 3))) & 15u];
+          acc[k] = fmaf(cv.x, w, acc[k]);
+          acc[k + 1] = fmaf(cv.y, w, acc[k + 1]);
+        }
+      } else {
 #pragma unroll
-      for (int g = 0; g < GT; ++g) {
-#pragma unroll
-        for (int i = 0; i < (KBY + 3) / 4; ++i) kw[g][i] = nkw[g][i];
-#pragma unroll
-        for (int i = 0; i < (VBY + 3) / 4; ++i) vw[g][i] = nvw[g][i];
-        ks[g] = nks[g];
-        vs[g] = nvs[g];
+        for (int k = 0; k < C; ++k) acc[k] = fmaf(s_cbv[lane_code<VB>(r.v[g], k)], w, acc[k]);
       }
     }
+  };
+  Rows ra, rb;
+  int t0 = t_begin + wave * GT;
+  if (t0 < t_end) fetch(t0, ra);
+  for (; t0 < t_end; t0 += 2 * kStep) {
+    step(t0, ra, rb);
+    if (t0 + kStep >= t_end) break;
+    step(t0 + kStep, rb, ra);
   }
 
   // ---- block merge: waves -> one (m, l, acc) ----
