@@ -1560,6 +1560,162 @@ __global__ __launch_bounds__(kThreads) void decode_wide_kernel(HeadDesc *const *
   }
 }
 
+// Row-dot kernel (padded 512 and 1024 with fp32 keys: K16 rings and the
+// hybrid branch's mirror).  A block takes kThreads tokens of one item.
+//   1. logits: one thread per token, the reference's sequential unfused dot
+//      product over the dim entries (attention.cpp:212-219, :497-502),
+//      times 1/sqrt(dim); the query is in LDS (read broadcast), the row
+//      streams in 16-byte loads;
+//   2. the block's maximum (seeded at -1e30 like the reference) and
+//      e = expf(l - max) into LDS;
+//   3. the V sum with the dimensions over the lanes, as the wide kernel's:
+//      wave w takes tokens w, w + 4, ..., lane l dimensions [C l, C l + C),
+//      C = P / 64, one coalesced load per wave and token (fp32 rows, or
+//      codes and their scale);
+//   4. (max, sum, acc[P]) for the finalize kernel.
+// The generic kernel ran the same per-token dot with 8 threads of 256 at a
+// time.
+template <int P, int VB, bool RAW>
+__global__ __launch_bounds__(kThreads) void decode_rowdot_kernel(HeadDesc *const *item_desc,
+                                                                 const float *__restrict__ queries,
+                                                                 int chunk, int n_splits,
+                                                                 float *__restrict__ partials) {
+  static_assert(P == 512 || P == 1024, "padded 512 or 1024");
+  static_assert(!RAW || VB == 16, "the mirror holds fp32 values");
+  constexpr bool VQ = VB != 16;
+  constexpr int C = P / 64;
+  constexpr int VBY = VQ ? C * VB / 8 : 0;
+  constexpr int VRB = VQ ? P * VB / 8 : 0;
+  __shared__ float s_q[P];
+  __shared__ float s_e[kThreads];
+  __shared__ float s_red[kWaves];
+  __shared__ float s_cbv[16];
+  __shared__ float s_acc[kWaves][P];
+  const int item = blockIdx.y, split = blockIdx.x;
+  const HeadDesc *d = item_desc[item];
+  const ItemView iv = item_view<RAW>(d);
+  const int dim = d->dim, n = iv.n;
+  const int t_begin = split * chunk, t_end = min(n, t_begin + chunk);
+  float *part = partials + ((size_t)item * n_splits + split) * (P + 4);
+  if (t_begin >= t_end) {
+    for (int i = threadIdx.x; i < P; i += blockDim.x) part[4 + i] = 0.0f;
+    if (threadIdx.x == 0) {
+      part[0] = -INFINITY;
+      part[1] = 0.0f;
+    }
+    return;
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if constexpr (VQ) {
+    if (threadIdx.x < (1 << VB)) s_cbv[threadIdx.x] = cbv<VB>(threadIdx.x);
+  }
+  const float *q = queries + (size_t)item * dim;
+  for (int i = threadIdx.x; i < P; i += kThreads) s_q[i] = i < dim ? q[i] : 0.0f;
+  __syncthreads();
+
+  // 1. this thread's token's logit
+  const int kstride = RAW ? dim : P;  // floats per key row
+  const float attn_s = 1.0f / sqrtf((float)dim);
+  const int t = t_begin + threadIdx.x;
+  float lg = -INFINITY;
+  if (t < t_end) {
+    const float *row = reinterpret_cast<const float *>(iv.k_rows) + (size_t)t * kstride;
+    float dsum = 0.0f;
+    int i = 0;
+    if ((kstride & 3) == 0) {
+      // 16-byte loads, 8 in flight ahead of their products
+      for (; i + 32 <= dim; i += 32) {
+        float4 r[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) r[k] = reinterpret_cast<const float4 *>(row + i)[k];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          dsum = __fadd_rn(dsum, __fmul_rn(s_q[i + 4 * k], r[k].x));
+          dsum = __fadd_rn(dsum, __fmul_rn(s_q[i + 4 * k + 1], r[k].y));
+          dsum = __fadd_rn(dsum, __fmul_rn(s_q[i + 4 * k + 2], r[k].z));
+          dsum = __fadd_rn(dsum, __fmul_rn(s_q[i + 4 * k + 3], r[k].w));
+        }
+      }
+    }
+    for (; i < dim; ++i) dsum = __fadd_rn(dsum, __fmul_rn(s_q[i], row[i]));
+    lg = __fmul_rn(dsum, attn_s);
+  }
+
+  // 2. the block maximum (the reference's compare from -1e30) and the weights
+  float m = t < t_end && lg > kMaxSeed ? lg : kMaxSeed;
+  m = wave_max(m);
+  if (lane == 0) s_red[wave] = m;
+  __syncthreads();
+  float M = s_red[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_red[w]);
+  const float e = t < t_end ? expf(lg - M) : 0.0f;
+  s_e[threadIdx.x] = e;
+  __syncthreads();
+  float l = wave_sum(e);
+  if (lane == 0) s_red[wave] = l;
+
+  // 3. the V sum, dimensions over the lanes
+  float acc[C];
+#pragma unroll
+  for (int k = 0; k < C; ++k) acc[k] = 0.0f;
+  const float isp = VQ ? 1.0f / sqrtf((float)P) : 1.0f;
+  for (int tt = t_begin + wave; tt < t_end; tt += kWaves) {
+    const float et = s_e[tt - t_begin];
+    if constexpr (VQ) {
+      uint32_t vw[(VBY + 3) / 4];
+      load_lane_bytes<VBY>(iv.v_rows + (size_t)tt * VRB + lane * VBY, vw);
+      const float w = et * iv.v_scale[tt] * isp;
+#pragma unroll
+      for (int k = 0; k < C; ++k) acc[k] = fmaf(s_cbv[lane_code<VB>(vw, k)], w, acc[k]);
+    } else {
+      const int vstride = RAW ? dim : P;
+      const float *vr = reinterpret_cast<const float *>(iv.v_rows) + (size_t)tt * vstride;
+      if (!RAW || (dim & 3) == 0) {
+        // C = 8 or 16 floats a lane: whole 16-byte loads within the row
+#pragma unroll
+        for (int k = 0; k < C; k += 4) {
+          const int i0 = lane * C + k;
+          float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          if (i0 + 4 <= (RAW ? dim : P)) v = *reinterpret_cast<const float4 *>(vr + i0);
+          else {
+            if (i0 < dim) v.x = vr[i0];
+            if (i0 + 1 < dim) v.y = vr[i0 + 1];
+            if (i0 + 2 < dim) v.z = vr[i0 + 2];
+          }
+          acc[k] = fmaf(v.x, et, acc[k]);
+          acc[k + 1] = fmaf(v.y, et, acc[k + 1]);
+          acc[k + 2] = fmaf(v.z, et, acc[k + 2]);
+          acc[k + 3] = fmaf(v.w, et, acc[k + 3]);
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+          const int i = lane * C + k;
+          acc[k] = fmaf(i < dim ? vr[i] : 0.0f, et, acc[k]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < C; ++k) s_acc[wave][lane * C + k] = acc[k];
+  __syncthreads();
+  // 4. the block's partial (natural units)
+  for (int i = threadIdx.x; i < P; i += kThreads) {
+    float a = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) a += s_acc[w][i];
+    part[4 + i] = a;
+  }
+  if (threadIdx.x == 0) {
+    float L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) L += s_red[w];
+    part[0] = M;
+    part[1] = L;
+  }
+}
+
 // Merge the splits of each item, normalise, undo the rotation.  The split
 // maxima, weights and sums are spread over the block (split s on thread
 // s mod kThreads); each dimension's weighted sum over the splits is shared by
@@ -1738,6 +1894,31 @@ hipError_t dispatch_wide(const DecodeShape &sh, dim3 grid, HeadDesc *const *desc
   return hipErrorInvalidValue;
 }
 
+template <int P>
+hipError_t dispatch_rowdot(const DecodeShape &sh, dim3 grid, HeadDesc *const *descs,
+                           const float *q, int chunk, int splits, float *part, hipStream_t s) {
+  if (chunk > kThreads) return hipErrorInvalidValue;  // one token a thread
+  if (sh.raw) {
+    decode_rowdot_kernel<P, 16, true><<<grid, kThreads, 0, s>>>(descs, q, chunk, splits, part);
+    return hipGetLastError();
+  }
+#define AQ_ROWDOT(VB_)                                                                              \
+  if (sh.v_bits == VB_) {                                                                           \
+    decode_rowdot_kernel<P, VB_, false><<<grid, kThreads, 0, s>>>(descs, q, chunk, splits, part);    \
+    return hipGetLastError();                                                                       \
+  }
+  AQ_ROWDOT(2) AQ_ROWDOT(3) AQ_ROWDOT(4) AQ_ROWDOT(16)
+#undef AQ_ROWDOT
+  return hipErrorInvalidValue;
+}
+
+// The row-dot kernel serves padded 512 and 1024 with fp32 keys: K16 rings
+// and the hybrid branch's mirror (a block takes kThreads tokens).
+bool rowdot_eligible(const DecodeShape &sh) {
+  return (sh.padded == 512 || sh.padded == 1024) && (sh.raw || sh.k_bits == 16) &&
+         (sh.raw || sh.v_bits == 2 || sh.v_bits == 3 || sh.v_bits == 4 || sh.v_bits == 16);
+}
+
 // The wide kernel serves padded 512 and 1024 with quantised K and V.
 bool wide_eligible(const DecodeShape &sh) {
   return !sh.raw && (sh.padded == 512 || sh.padded == 1024) && sh.k_bits >= 2 && sh.k_bits <= 4 &&
@@ -1779,6 +1960,14 @@ SplitPlan decode_plan(int n_items, const DecodeShape &sh) {
   // takes at least 512 tokens; 4 blocks a CU at padded 512 (a 4-bit table
   // takes 36 KB of LDS), 2 at padded 1024 (68 KB)
   if (wide_eligible(sh)) return plan_splits(n_items, max_n, 512, sh.padded == 512 ? 1024 : 512);
+  // row-dot kernel: one token a thread, so chunks of exactly kThreads tokens
+  if (rowdot_eligible(sh)) {
+    SplitPlan sp;
+    sp.chunk = kThreads;
+    sp.splits = (max_n + kThreads - 1) / kThreads;
+    if (sp.splits < 1) sp.splits = 1;
+    return sp;
+  }
   return plan_splits(n_items, max_n, 256, 1024);
 }
 
@@ -1886,6 +2075,9 @@ hipError_t launch_decode_items(HeadDesc *const *descs, int n_items, const Decode
   } else if (wide_eligible(sh)) {
     e = sh.padded == 512 ? dispatch_wide<512>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, s)
                          : dispatch_wide<1024>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, s);
+  } else if (rowdot_eligible(sh)) {
+    e = sh.padded == 512 ? dispatch_rowdot<512>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, s)
+                         : dispatch_rowdot<1024>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, s);
   } else {
     e = raw ? dispatch_generic<true>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, s)
             : dispatch_generic<false>(sh, grid, descs, d_q, sp.chunk, sp.splits, d_ws, s);

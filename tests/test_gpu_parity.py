@@ -286,8 +286,14 @@ DECODE_CASES = [
     (1024, 4, 4, 2000, 2600),
     (1000, 2, 3, 600, 600),
     (600, 3, 2, 300, 13),
-    # and fp32 keys there still take the generic kernel
+    # fp32 keys there take the row-dot kernel (one token a thread): every V
+    # width, a wrapped ring, a ring of exactly one block's tokens, a dim that
+    # is not a multiple of 4
     (512, 16, 2, 300, 300),
+    (1024, 16, 16, 600, 700),
+    (700, 16, 4, 900, 1000),
+    (512, 16, 3, 256, 256),
+    (602, 16, 16, 300, 257),
 ]
 
 
@@ -311,6 +317,8 @@ def test_decode_dense(oracle, dim, kb, vb, cap, n):
 @pytest.mark.parametrize("dim,kb,vb,hyb,n", [
     (64, 4, 2, 512, 512), (128, 4, 4, 64, 40), (96, 3, 2, 128, 100), (64, 16, 2, 16, 10),
     (256, 4, 2, 512, 500), (256, 3, 3, 64, 64),
+    # the mirror at padded 512 and 1024: the row-dot kernel
+    (512, 4, 2, 512, 400), (602, 3, 4, 300, 257), (1024, 2, 2, 64, 40),
 ])
 def test_decode_hybrid(oracle, dim, kb, vb, hyb, n):
     print(f"decode hybrid dim={dim} k{kb}v{vb} hyb={hyb} n={n}", flush=True)
