@@ -167,9 +167,10 @@ __device__ __forceinline__ T *wave_uniform(T *p) {
 // then applied to the codes: a code is a nondecreasing function of the value,
 // so the code of the clamped value is the code clamped to
 // [code(nclip), code(clip)] (passed as cl, ch).
+// s_q4: the 4-bit cell table (quantize_g4).
 template <int P, int B, bool CLAMP, bool BD = false>
 __device__ __forceinline__ void pack_codes(const float (&buf)[P], uint32_t (&w)[Row<P, B>::words],
-                                           const Q4Entry *s_q4, float nclip, float clip,
+                                           const Q4Cell *s_q4, float nclip, float clip,
                                            float q0 = 0.0f, float q1 = 0.0f, float q2 = 0.0f,
                                            uint32_t cl = 0u, uint32_t ch = 0u) {
   static_assert(!BD || B == 2, "b-domain codes for 2 bits");
@@ -182,7 +183,7 @@ __device__ __forceinline__ void pack_codes(const float (&buf)[P], uint32_t (&w)[
     } else {
       // the reference's two-sided clamp is the median for finite values
       const float v = CLAMP ? __builtin_amdgcn_fmed3f(buf[i], nclip, clip) : buf[i];
-      q = B == 4 ? quantize_ss4(v, s_q4) : B == 3 ? quantize_ss3(v) : quantize_ss2(v);
+      q = B == 4 ? quantize_g4(v, s_q4) : B == 3 ? quantize_ss3(v) : quantize_ss2(v);
     }
     // Bit position of code i inside the little-endian word stream.
     int byte, shift;
@@ -226,7 +227,7 @@ __device__ __forceinline__ void pack_codes(const float (&buf)[P], uint32_t (&w)[
 // three-wave register budget would spill).
 template <int P, int B, bool BD = false, bool U = false>
 __device__ __forceinline__ void encode_vec(float (&buf)[P], const HeadDesc *d, int side, int slot,
-                                           float inv_sqrt_p, float sqrt_p, const Q4Entry *s_q4,
+                                           float inv_sqrt_p, float sqrt_p, const Q4Cell *s_q4,
                                            float q0 = 0.0f, float q1 = 0.0f, float q2 = 0.0f) {
   uint8_t *codes = side == 0 ? d->k_codes : d->v_codes;
   float *scales = side == 0 ? d->k_scale : d->v_scale;
@@ -357,7 +358,7 @@ template <int P, int B, bool UNIFORM, bool BD = false>
 __device__ __forceinline__ void encode_row(const HeadDesc *d, const RingState st, int c, int t,
                                            int side, const float *__restrict__ src, int n_tok,
                                            int dim, float inv_sqrt_p, float sqrt_p,
-                                           const Q4Entry *s_q4, float q0 = 0.0f, float q1 = 0.0f,
+                                           const Q4Cell *s_q4, float q0 = 0.0f, float q1 = 0.0f,
                                            float q2 = 0.0f) {
   const int cap = d->cap;
   const float *x = src + ((size_t)c * n_tok + t) * dim;
@@ -406,9 +407,14 @@ __device__ __forceinline__ void encode_row(const HeadDesc *d, const RingState st
 
 // Three waves per SIMD instead of two at the compiler's own 192-200 VGPRs:
 // measured on config 5's bulk append, K side 1,101 -> 1,030 us, V side 996 ->
-// 988 us.  Within the 168-VGPR budget the 4-bit codec keeps one dword in
-// scratch (with its ring pointers in scalar registers) and the 2-bit codec
-// needs 155 VGPRs.
+// 988 us.  Within the 168-VGPR budget the 4-bit codec fits without scratch
+// (with its ring pointers in scalar registers) and the 2-bit codec needs 158
+// VGPRs.
+//
+// 4-bit codes come from the quarter-unit cell table (quantize_g4: an fma, a
+// clamp, a conversion and one 8-byte LDS read per value, instead of the
+// sign-split key and a bucket table over the exponent and mantissa bits):
+// measured on config 5's bulk append, K side 1,003 -> 993 us.
 //
 // 2-bit codes come from the values before the two scalings (bd: the
 // thresholds for this launch's inv_sqrt_p and sqrt_p, quant.hpp): two
@@ -420,10 +426,11 @@ __global__ __launch_bounds__(128, 3) void append_kernel(HeadDesc *const *descs, 
                                                      int n_tok, int dim, float inv_sqrt_p,
                                                      float sqrt_p, int commit, BdThr bd) {
   constexpr bool BD = B == 2;
-  // 4-bit codes: the bucket table of quantize_ss4, built before any lane leaves
-  __shared__ Q4Entry s_q4[B == 4 ? kQ4Entries : 1];
+  // 4-bit codes: the cell table of quantize_g4, in LDS before any lane leaves
+  __shared__ Q4Cell s_q4[B == 4 ? kQ4Cells : 1];
   if constexpr (B == 4) {
-    for (int i = threadIdx.x; i < kQ4Entries; i += blockDim.x) s_q4[i] = q4s_entry(i);
+    static constexpr Q4Table kTab = q4_table();
+    if (threadIdx.x < kQ4Cells) s_q4[threadIdx.x] = kTab.c[threadIdx.x];
     __syncthreads();
   }
   int c, t;
@@ -463,9 +470,10 @@ __global__ __launch_bounds__(128) void append_kv_kernel(HeadDesc *const *descs, 
                                                         const float *__restrict__ keys,
                                                         const float *__restrict__ vals,
                                                         int dim, float inv_sqrt_p, float sqrt_p) {
-  __shared__ Q4Entry s_q4[(KB == 4 || VB == 4) ? kQ4Entries : 1];
+  __shared__ Q4Cell s_q4[(KB == 4 || VB == 4) ? kQ4Cells : 1];
   if constexpr (KB == 4 || VB == 4) {
-    for (int i = threadIdx.x; i < kQ4Entries; i += blockDim.x) s_q4[i] = q4s_entry(i);
+    static constexpr Q4Table kTab = q4_table();
+    if (threadIdx.x < kQ4Cells) s_q4[threadIdx.x] = kTab.c[threadIdx.x];
     __syncthreads();
   }
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
@@ -494,13 +502,14 @@ __global__ __launch_bounds__(128) void append_one_kernel(HeadDesc *const *descs,
                                                          const float *__restrict__ vals, int dim,
                                                          int n_tok, float inv_sqrt_p,
                                                          float sqrt_p) {
-  __shared__ Q4Entry s_q4[(KB == 4 || VB == 4) ? kQ4Entries : 1];
+  __shared__ Q4Cell s_q4[(KB == 4 || VB == 4) ? kQ4Cells : 1];
   __shared__ __align__(16) float s_sq[2][P];
   __shared__ uint8_t s_code[2][P];
   const int c = blockIdx.x, t = blockIdx.y;
   const int lane = threadIdx.x & 63, side = threadIdx.x >> 6;
   if constexpr (KB == 4 || VB == 4) {
-    for (int i = threadIdx.x; i < kQ4Entries; i += blockDim.x) s_q4[i] = q4s_entry(i);
+    static constexpr Q4Table kTab = q4_table();
+    if (threadIdx.x < kQ4Cells) s_q4[threadIdx.x] = kTab.c[threadIdx.x];
   }
   HeadDesc *d = descs[c];
   const RingState st = d->st;
@@ -520,9 +529,10 @@ __global__ __launch_bounds__(128) void append_kernel_wide(HeadDesc *const *descs
                                                           int side, const float *__restrict__ src,
                                                           int n_tok, int dim, int P,
                                                           float inv_sqrt_p, float sqrt_p) {
-  __shared__ Q4Entry s_q4[B == 4 ? kQ4Entries : 1];
+  __shared__ Q4Cell s_q4[B == 4 ? kQ4Cells : 1];
   if constexpr (B == 4) {
-    for (int i = threadIdx.x; i < kQ4Entries; i += blockDim.x) s_q4[i] = q4_entry(i);
+    static constexpr Q4Table kTab = q4_table();
+    if (threadIdx.x < kQ4Cells) s_q4[threadIdx.x] = kTab.c[threadIdx.x];
     __syncthreads();
   }
   const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -586,7 +596,7 @@ __global__ __launch_bounds__(128) void append_kernel_wide(HeadDesc *const *descs
       float v = buf[i];
       if (v > clip) v = clip;
       if (v < -clip) v = -clip;
-      const uint32_t q = B == 4 ? quantize4_tab(v, s_q4) : quantize<B>(v);
+      const uint32_t q = B == 4 ? (v != v ? 7u : quantize_g4(v, s_q4)) : quantize<B>(v);
       if constexpr (B == 4) {
         row[i / 2] |= (uint8_t)(q << ((i % 2) ? 0 : 4));
       } else if constexpr (B == 2) {

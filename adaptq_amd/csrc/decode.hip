@@ -813,11 +813,11 @@ __global__ __launch_bounds__(kLutThreads, P <= 128 && (KB == 2 || KB == 4) ? 4 :
   }
 
   // FUSE: waves 1 and 2 encode the step's key and value rows (LDS scratch of
-  // the codec, its 4-bit bucket table per wave, the stored rows' copies)
+  // the codec, its 4-bit cell table per wave, the stored rows' copies)
   // while wave 0 rotates the query; load_query's closing barrier publishes
   // both
   constexpr bool kQ4 = FUSE && (KB == 4 || VB == 4);
-  __shared__ Q4Entry s_app_q4[kQ4 ? 2 : 1][kQ4 ? kQ4Entries : 1];
+  __shared__ Q4Cell s_app_q4[kQ4 ? 2 : 1][kQ4 ? kQ4Cells : 1];
   __shared__ __align__(16) float s_app_sq[FUSE ? 2 : 1][FUSE ? P : 1];
   __shared__ uint8_t s_app_code[FUSE ? 2 : 1][FUSE ? P : 1];
   __shared__ uint32_t s_app_row[FUSE ? 2 : 1][FUSE ? (KW > VW ? KW : VW) : 1];
@@ -826,7 +826,8 @@ __global__ __launch_bounds__(kLutThreads, P <= 128 && (KB == 2 || KB == 4) ? 4 :
     if (wave == 1 || wave == 2) {
       const int side = wave - 1;
       if constexpr (kQ4) {
-        for (int i = lane; i < kQ4Entries; i += 64) s_app_q4[side][i] = q4s_entry(i);
+        static constexpr Q4Table kTab = q4_table();
+        if (lane < kQ4Cells) s_app_q4[side][lane] = kTab.c[lane];
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");

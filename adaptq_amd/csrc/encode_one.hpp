@@ -29,14 +29,14 @@ __device__ __forceinline__ uint32_t nan_word(int k) {
 // Token t (of n_tok appended at once, ring state st before them) of head d,
 // side 0 (key, KB bits) or 1 (value, VB bits), from the dim floats at x.
 // s_sq (P floats) and s_code (P bytes): this wave's LDS scratch; s_q4: the
-// sign-split 4-bit bucket table (q4s_entry) when KB or VB is 4.  lds_row /
+// 4-bit cell table (q4_table) when KB or VB is 4.  lds_row /
 // lds_scale, when not null, receive a copy of the stored row (in its stored
 // word order) and scale, for quantised rows.
 template <int P, int KB, int VB>
 __device__ __forceinline__ void encode_one_row(HeadDesc *d, const RingState st, int n_tok, int t,
                                                const float *__restrict__ x, int dim, int side,
                                                int lane, float inv_sqrt_p, float sqrt_p,
-                                               const Q4Entry *s_q4, float *s_sq, uint8_t *s_code,
+                                               const Q4Cell *s_q4, float *s_sq, uint8_t *s_code,
                                                uint32_t *lds_row, float *lds_scale) {
   constexpr int E = P / 64;
   const int cap = d->cap;
@@ -124,7 +124,7 @@ __device__ __forceinline__ void encode_one_row(HeadDesc *d, const RingState st, 
   }
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    const uint32_t q = B == 4 ? quantize_ss4(v[e], s_q4) : B == 3 ? quantize_ss3(v[e]) : quantize_ss2(v[e]);
+    const uint32_t q = B == 4 ? quantize_g4(v[e], s_q4) : B == 3 ? quantize_ss3(v[e]) : quantize_ss2(v[e]);
     s_code[lane + 64 * e] = (uint8_t)q;
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

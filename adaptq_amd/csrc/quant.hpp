@@ -2,32 +2,27 @@
 //
 // quantize<B>: the reference's branchless binary search (codebook.cpp:119-144):
 // the count of thresholds t with v >= t, NaN -> the lower centre code.
-// quantize4_tab: the same function for 4-bit codes from one table lookup.
-// The thresholds are symmetric (thr(14-k) = -thr(k) exactly) and the centre
-// one is 0, so for v >= 0 (including -0.0, as v >= 0 holds for it) the index
-// is 8 + #{positive t : |v| >= t} and for v < 0 it is 7 - #{positive t : |v| > t}.
-// Both conditions are one unsigned compare on key = bits(|v|) + [v >= 0]
-// against bits(t) (positive floats order like their bit patterns).  The table
-// has one entry per bucket of bits(|v|) >> 18 (exponent and 5 mantissa bits)
-// over [2^-4, 4], where each bucket holds at most one positive threshold:
-// n = thresholds below the bucket, t = the one inside it (or none).  Values
-// below 2^-4 or from 4 up use the end buckets, which hold no threshold.
-// Equality with quantize<4> over every float is checked on the host
-// (tests/cpp/quant_exhaustive.cpp).
-// quantize_ss2/3/4: the sign-split forms of the append kernels (below).
+// quantize_g4: the same function for 4-bit codes from one lookup in a grid
+// of quarter-unit cells: cell g = floor(4 v) covers [g/4, (g+1)/4).  The 15
+// thresholds are at least 0.2527 apart, so a cell holds at most one of them:
+// the code is n + [v >= t], n = thresholds below the cell, t = the one inside
+// it (NaN for none, so the compare fails).  Cells below -10 and from 9 up hold
+// none and are clamped to those end cells.  The compare v >= t on v itself
+// decides as the binary search does, -0.0 included (cell 0, whose threshold
+// is 0).  Equality with quantize<4> over every finite float is checked on the
+// host (tests/cpp/quant_exhaustive.cpp).
+// quantize_ss2/3: the sign-split forms of the append kernels (below).
 // quantize_bd2: 2-bit codes of a value before its scalings by 1/sqrt(p) and
 // sqrt(p), against thresholds moved through both roundings (below).
 #pragma once
+
+#include <math.h>
 
 #include "codebook.hpp"
 
 namespace aq {
 
-AQ_HD inline uint32_t f32_bits(float f) {
-  uint32_t u;
-  __builtin_memcpy(&u, &f, 4);
-  return u;
-}
+AQ_HD constexpr uint32_t f32_bits(float f) { return __builtin_bit_cast(uint32_t, f); }
 
 template <int B>
 AQ_HD inline uint32_t quantize(float v) {
@@ -54,36 +49,53 @@ AQ_HD inline uint32_t quantize(float v) {
   }
 }
 
-struct Q4Entry {
-  uint32_t t;  // bits of the positive threshold inside the bucket, or ~0
-  uint32_t n;  // positive thresholds below the bucket
+struct Q4Cell {
+  float t;     // the threshold inside the cell, or NaN
+  uint32_t n;  // thresholds below the cell
 };
 
-constexpr int kQ4Lo = 3936;  // bits(2^-4) >> 18
-constexpr int kQ4Hi = 4128;  // bits(4.0f) >> 18
-constexpr int kQ4Entries = kQ4Hi - kQ4Lo + 1;
+constexpr int kQ4CellLo = -10;  // cell of [-2.5, -2.25) and everything below
+constexpr int kQ4CellHi = 9;    // cell of [2.25, 2.5) and everything above
+constexpr int kQ4Cells = kQ4CellHi - kQ4CellLo + 1;
 
-AQ_HD inline Q4Entry q4_entry(int i) {
-  const uint32_t lo = (uint32_t)(kQ4Lo + i) << 18, hi = lo + (1u << 18);
-  Q4Entry e{~0u, 0u};
-  for (int k = 8; k < 15; ++k) {
-    const uint32_t t = f32_bits(thr<4>(k));
-    if (t < lo) ++e.n;
-    else if (t < hi && i < kQ4Entries - 1) e.t = t;
+AQ_HD constexpr Q4Cell q4_cell(int i) {
+  const int g = kQ4CellLo + i;
+  Q4Cell c{__builtin_nanf(""), 0u};
+  for (int k = 0; k < 15; ++k) {
+    const float t = thr<4>(k);
+    if (4.0f * t < (float)g) ++c.n;
+    else if (4.0f * t < (float)(g + 1)) c.t = t;
   }
-  return e;
+  return c;
 }
 
-AQ_HD inline uint32_t quantize4_tab(float v, const Q4Entry *tab) {
-  const uint32_t ab = f32_bits(v) & 0x7FFFFFFFu;
-  const bool nonneg = !(v < 0.0f);
-  const uint32_t key = ab + (nonneg ? 1u : 0u);
-  uint32_t b = ab >> 18;
-  b = b < (uint32_t)kQ4Lo ? (uint32_t)kQ4Lo : b > (uint32_t)kQ4Hi ? (uint32_t)kQ4Hi : b;
-  const Q4Entry e = tab[b - kQ4Lo];
-  const uint32_t m = e.n + (key > e.t ? 1u : 0u);
-  const uint32_t idx = nonneg ? 8u + m : 7u - m;
-  return v != v ? 7u : idx;
+// every cell, evaluated by the compiler (kernels copy it into LDS)
+struct Q4Table {
+  Q4Cell c[kQ4Cells];
+};
+AQ_HD constexpr Q4Table q4_table() {
+  Q4Table t{};
+  for (int i = 0; i < kQ4Cells; ++i) t.c[i] = q4_cell(i);
+  return t;
+}
+
+// Table index of v's cell, for non-NaN v: floor(4 v) - kQ4CellLo clamped to
+// the table, computed as the truncation of the clamped fma(v, 4, 10), which
+// is nonnegative.  The fma rounds (by at most 1e-6 in w, 2.4e-7 in v), so a
+// v just below a cell's upper edge can land in the next cell; that changes no
+// code: 0, the lower edge of its own cell, is the only threshold within
+// 0.0026 of a cell edge, so a value moved across an edge is on the same side
+// of every threshold of both cells.  (Checked with quantize_g4 on every
+// float.)
+AQ_HD inline int q4_cell_index(float v) {
+  const float w = fminf(fmaxf(fmaf(v, 4.0f, (float)-kQ4CellLo), 0.0f), (float)(kQ4Cells - 1));
+  return (int)w;
+}
+
+// non-NaN v (a NaN vector is given its code as a whole by the caller)
+AQ_HD inline uint32_t quantize_g4(float v, const Q4Cell *tab) {
+  const Q4Cell c = tab[q4_cell_index(v)];
+  return c.n + (v >= c.t ? 1u : 0u);
 }
 
 // Sign-split quantisers of the append kernel, for finite v (a NaN vector is
@@ -95,11 +107,8 @@ AQ_HD inline uint32_t quantize4_tab(float v, const Q4Entry *tab) {
 //   code = u ^ (s & (2^B - 1))
 // For v >= 0, key > bits(t) is v >= t; for v < 0 it is |v| > t, and the
 // negative side's count 2^(B-1) - 1 - m equals (2^(B-1) + m) ^ (2^B - 1).
-// -0.0 belongs to the positive side (-0.0 >= 0 holds): the 2- and 3-bit forms
-// add +0.0 first (which turns -0.0 into +0.0 and changes nothing else); the
-// 4-bit form reads the bucket table with n raised by 8 (q4s_entry), whose
-// lowest bucket holds a threshold at key 0 over a base count of 7, so key 0
-// (only -0.0 has it) gives 7 ^ 15 = 8 and every other key in it gives 8.
+// -0.0 belongs to the positive side (-0.0 >= 0 holds): both forms add +0.0
+// first (which turns -0.0 into +0.0 and changes nothing else).
 // Equality with quantize<B> over every finite float is checked on the host
 // (tests/cpp/quant_exhaustive.cpp).
 struct SignSplit {
@@ -113,22 +122,6 @@ AQ_HD inline SignSplit sign_split(float c) {
   r.ab = bits & 0x7FFFFFFFu;
   r.key = r.ab + 1u + r.s;
   return r;
-}
-
-AQ_HD inline Q4Entry q4s_entry(int i) {
-  Q4Entry e = q4_entry(i);
-  if (i == 0) return Q4Entry{0u, 7u};  // holds no threshold (checked below)
-  e.n += 8u;
-  return e;
-}
-
-AQ_HD inline uint32_t quantize_ss4(float v, const Q4Entry *tab8) {
-  const SignSplit x = sign_split(v);
-  uint32_t b = x.ab >> 18;
-  b = b < (uint32_t)kQ4Lo ? (uint32_t)kQ4Lo : b > (uint32_t)kQ4Hi ? (uint32_t)kQ4Hi : b;
-  const Q4Entry e = tab8[b - kQ4Lo];
-  const uint32_t u = e.n + (x.key > e.t ? 1u : 0u);
-  return u ^ (x.s & 15u);
 }
 
 AQ_HD inline uint32_t quantize_ss3(float v) {

@@ -1,5 +1,6 @@
-// Every float bit pattern: quantize4_tab and the sign-split quantisers
-// quantize_ss2/3/4 (adaptq_amd/csrc/quant.hpp, the append kernel's) against
+// Every float bit pattern: the 4-bit cell quantiser quantize_g4 (with the NaN
+// code put in front, as the wide append kernel does) and the sign-split
+// quantisers quantize_ss2/3 (adaptq_amd/csrc/quant.hpp, the append kernels') against
 // quantize<B> (the reference's binary search restated) and, on a stride,
 // against the oracle's quantize_fast; then quantize_bd2 against quantize<2>
 // of the twice-rounded scaled value for every padded size up to 128.  The sign-split forms are defined for
@@ -18,13 +19,11 @@
 extern "C" int orc_quantize_fast(float v, int bits);
 
 int main() {
-  aq::Q4Entry tab[aq::kQ4Entries], tab8[aq::kQ4Entries];
-  for (int i = 0; i < aq::kQ4Entries; ++i) {
-    tab[i] = aq::q4_entry(i);
-    tab8[i] = aq::q4s_entry(i);
-  }
-  if (tab[0].n != 0 || tab[0].t != ~0u) {
-    std::printf("lowest bucket holds a threshold\n");
+  constexpr aq::Q4Table tab = aq::q4_table();
+  // the end cells, which take every value beyond them, hold no threshold
+  if (tab.c[0].n != 0 || tab.c[0].t == tab.c[0].t || tab.c[aq::kQ4Cells - 1].n != 15 ||
+      tab.c[aq::kQ4Cells - 1].t == tab.c[aq::kQ4Cells - 1].t) {
+    std::printf("end cells hold a threshold\n");
     return 1;
   }
   std::atomic<unsigned long long> bad{0};
@@ -37,17 +36,16 @@ int main() {
         const uint32_t u = (uint32_t)x;
         float v;
         std::memcpy(&v, &u, 4);
-        const uint32_t a = aq::quantize4_tab(v, tab), b = aq::quantize<4>(v);
+        const uint32_t a = v != v ? 7u : aq::quantize_g4(v, tab.c), b = aq::quantize<4>(v);
         bool wrong = a != b;
         if ((u & 0xFFF) == 0x5A5) wrong = wrong || (int)b != orc_quantize_fast(v, 4);
         if (v == v) {
-          wrong = wrong || aq::quantize_ss4(v, tab8) != b;
           wrong = wrong || aq::quantize_ss3(v) != aq::quantize<3>(v);
           wrong = wrong || aq::quantize_ss2(v) != aq::quantize<2>(v);
         }
         if (wrong && bad.fetch_add(1) < 10)
-          std::printf("mismatch bits=%08x v=%g tab=%u search=%u ss4=%u ss3=%u/%u ss2=%u/%u\n", u, v,
-                      a, b, aq::quantize_ss4(v, tab8), aq::quantize_ss3(v), aq::quantize<3>(v),
+          std::printf("mismatch bits=%08x v=%g g4=%u search=%u ss3=%u/%u ss2=%u/%u\n", u, v,
+                      a, b, aq::quantize_ss3(v), aq::quantize<3>(v),
                       aq::quantize_ss2(v), aq::quantize<2>(v));
       }
     });

@@ -1,7 +1,8 @@
-"""The append kernel's quantisers (quantize4_tab and the sign-split
-quantize_ss2/3/4 in adaptq_amd/csrc/quant.hpp) equal the reference's binary
-search (quantize<B>) on every float bit pattern (every finite one for the
-sign-split forms), and the oracle's quantize_fast on a stride of them; the
+"""The append kernels' quantisers (the 4-bit cell lookup quantize_g4 and the
+sign-split quantize_ss2/3 in adaptq_amd/csrc/quant.hpp) equal the reference's
+binary search (quantize<B>) on every float bit pattern (every finite one for
+the sign-split forms; NaN takes its code before the cell lookup, as the wide
+append kernel does), and the oracle's quantize_fast on a stride of them; the
 2-bit quantiser of the values before the scalings (quantize_bd2) equals
 quantize<2> of the twice-rounded scaled value on every finite float for every
 padded size up to 128: the header is compiled for the host by
