@@ -3,11 +3,17 @@
   adaptq_amd/libadaptq.so          C ABI + gfx950 kernels (hipcc)
   adaptq_amd/adaptq_py*.so         pybind11 module (MHAContext), links the above
 
-Run ``python -m adaptq_amd.build`` or call :func:`build`.  Every call
-recompiles.  ``python -m adaptq_amd.build --clock-stamps`` builds only
-adaptq_amd/libadaptq_clk.so, the same library with decode.hip compiled with
-AQ_CLOCK_STAMPS (per-block shader-clock stamps of the LUT decode kernel, read
-by ``bench.py --clock-stamps``); the product never loads it.
+  adaptq_amd/libadaptq_clk.so      timing library: the same library with decode.hip
+                                   compiled with AQ_CLOCK_STAMPS (per-block
+                                   shader-clock stamps of the LUT decode kernel,
+                                   read by ``bench.py --clock-stamps``)
+  adaptq_amd/libadaptq_probe.so    timing library: the bulk append's memory
+                                   traffic without its codec (probe_rows.hip,
+                                   read by ``bench.py --append-floor``)
+
+Run ``python -m adaptq_amd.build`` or call :func:`build` (all four).  Every
+call recompiles.  ``--clock-stamps`` or ``--probes`` builds only that timing
+library.  The product never loads the timing libraries.
 """
 from __future__ import annotations
 
@@ -23,6 +29,7 @@ CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libadaptq.so")
 CLK_LIB = os.path.join(PKG, "libadaptq_clk.so")
+PROBE_LIB = os.path.join(PKG, "libadaptq_probe.so")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"
@@ -85,6 +92,19 @@ def build_clock_lib() -> str:
     return CLK_LIB
 
 
+def build_probe_lib() -> str:
+    """libadaptq_probe.so: the bulk append's memory traffic without its codec
+    (probe_rows.hip; bench.py --append-floor)."""
+    os.makedirs(BUILD, exist_ok=True)
+    obj = os.path.join(BUILD, "probe_rows.hip.o")
+    _run([HIPCC, *HIP_FLAGS, "-x", "hip", "-c", os.path.join(CSRC, "probe_rows.hip"), "-o", obj])
+    tmp = PROBE_LIB + ".tmp"
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", obj, "-o", tmp,
+          f"-Wl,-rpath,{ROCM}/lib", "-Wl,-soname,libadaptq_probe.so"])
+    os.replace(tmp, PROBE_LIB)
+    return PROBE_LIB
+
+
 def build_pybind() -> str:
     import pybind11
 
@@ -101,13 +121,18 @@ def build_pybind() -> str:
 
 
 def build(jobs: int = 8) -> None:
+    """The library, its Python module and the two timing libraries."""
     build_lib(jobs)
     build_pybind()
+    build_clock_lib()
+    build_probe_lib()
 
 
 if __name__ == "__main__":
     if "--clock-stamps" in sys.argv[1:]:
         print("built", build_clock_lib())
+    elif "--probes" in sys.argv[1:]:
+        print("built", build_probe_lib())
     else:
         build()
         print("built", LIB)

@@ -700,6 +700,47 @@ def clock_stamps(L, last_error, torch, np, plan, qp, op, stream, sptr, warmup, s
         "clock_ghz_max": float(np.max([r["clock_ghz"] for r in t]))}}), flush=True)
 
 
+def append_floor(torch, n_rows=1024 * 8192, reps=10):
+    """The bulk append's traffic without its codec (libadaptq_probe.so): one
+    config-5 chunk's input (1,024 heads x 8,192 rows of 128 floats) read and
+    64 or 32 bytes a row written, in the append kernel's own load and store
+    pattern and linearly; HIP events over `reps` launches on one stream."""
+    import ctypes as C
+    path = os.path.join(ROOT, "adaptq_amd", "libadaptq_probe.so")
+    if not os.path.exists(path):
+        sys.exit("bench: --append-floor needs python -m adaptq_amd.build --probes")
+    lib = C.CDLL(path)
+    lib.adaptq_probe_rows.argtypes = [C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_longlong,
+                                      C.c_void_p]
+    lib.adaptq_probe_rows.restype = C.c_int
+    src = torch.full((n_rows * 128,), 0.5, device="cuda:0")
+    dst = torch.empty(n_rows * 64, dtype=torch.uint8, device="cuda:0")
+    stream = torch.cuda.current_stream()
+    sptr = C.c_void_p(stream.cuda_stream)
+    res = {}
+    for nb in (64, 32):
+        for mode, name in ((0, "append_pattern"), (1, "linear"), (2, "linear_read_only")):
+            def call():
+                rc = lib.adaptq_probe_rows(mode, nb, C.c_void_p(src.data_ptr()),
+                                           C.c_void_p(dst.data_ptr()), n_rows, sptr)
+                if rc != 0:
+                    sys.exit(f"bench: adaptq_probe_rows({mode}, {nb}) returned {rc}")
+            call()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for _ in range(reps):
+                call()
+            b.record(stream)
+            torch.cuda.synchronize()
+            us = a.elapsed_time(b) * 1e3 / reps
+            nbytes = n_rows * 512 + (0 if mode == 2 else n_rows * nb)
+            res[f"nb{nb}_{name}"] = {"us": round(us, 1), "bytes": nbytes,
+                                     "gb_per_s": round(nbytes / us / 1e3, 1),
+                                     "frac_hbm": round(nbytes / us / 1e3 / 8000.0, 4)}
+    print(json.dumps({"append_floor": res, "rows": n_rows, "launches_each": reps}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -719,6 +760,10 @@ def main():
                          "warmup + steps decode launches (at most 32), each one's HIP-event "
                          "time and the shader clock from its blocks' s_memtime / s_memrealtime "
                          "stamps; prints one JSON line per launch and a summary")
+    ap.add_argument("--append-floor", action="store_true",
+                    help="with the probe library (python -m adaptq_amd.build --probes): the "
+                         "bulk append's memory traffic for one config-5 chunk without its "
+                         "codec, in its own access pattern and linearly")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy 5 times (scales rocprof "
                          "FETCH_SIZE/WRITE_SIZE readings to bytes)")
@@ -731,6 +776,10 @@ def main():
 
     import numpy as np
     import torch  # loads torch's HIP runtime first; libadaptq binds to the same one
+
+    if args.append_floor:
+        append_floor(torch)
+        return
 
     if args.copy_calibration:
         x = torch.ones(1 << 28, device="cuda:0")  # 1 GiB of fp32
