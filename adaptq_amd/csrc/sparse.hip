@@ -792,115 +792,89 @@ __device__ __forceinline__ void scan_counts(SelectShared &sh) {
   __syncthreads();
 }
 
-// Passes of sort_small<DB> for the differing bits diff: DB-bit digits whose
-// bits are not all shared.
-__device__ __forceinline__ int radix_passes(uint32_t diff, int db) {
-  int np = 0;
-  for (int sft = 0; sft < 32; sft += db) np += ((diff >> sft) & ((1u << db) - 1u)) != 0u;
-  return np;
-}
-
-// Stable LSD radix sort, DB (8 or 9) bits a pass, of the n <= 2 kSelThreads
-// keys sh.key[0..n) with payloads sh.idx[0..n) (in: token order; out:
-// sorted, in the same arrays), skipping the digits every key shares (diff:
-// OR ^ AND of the keys).  Position r kSelThreads + t is thread t's in round
-// r; a wave ranks its keys of one digit with DB ballots (lanes with the same
-// digit below it), leaders record the wave's count of each digit per round,
-// and one exclusive scan in (digit, round, wave) order gives every key its
-// destination.  sh.key / sh.idx from 4,096 on are the second buffer.
-template <int DB>
-__device__ __forceinline__ void sort_small(SelectShared &sh, int n, uint32_t diff) {
-  constexpr int R = 2;
-  constexpr int ND = 1 << DB;
-  constexpr int NE = ND * R * (kSelThreads / 64);  // count entries, 8 or 16 per thread
-  static_assert(NE == 8 * kSelThreads || NE == 16 * kSelThreads, "8 or 16 count entries per thread");
-  constexpr int EPT = NE / kSelThreads;
-  constexpr uint32_t DM = (uint32_t)ND - 1u;
+// Stable sort of up to 2 kSelThreads 32-bit keys by comparison: the pairs
+// (key, position) are distinct, so sorting them gives the stable order.
+// (An LSD radix sort in LDS with 8- or 9-bit digits, ranked by wave ballots,
+// took 11.6-12.8 us of config 1 and 3's decodes; this one 9.1-9.4 us.)  Thread t holds positions E t .. E t + E - 1 (E = 1 or 2) as
+// 64-bit values key << 32 | position; its slots without a token (positions
+// from n on, and the second slot when E = 1) hold key 0xFFFFFFFF with a
+// position of 2,048 or more, distinct and after every token.  Each wave sorts its 128
+// values in registers (a bitonic network, partners by lane shuffles); four
+// rounds of pairwise merges in LDS (sh.cnt as two 2,048-value buffers) then
+// give one run: a value's place in the merged run is its place in its own
+// run plus the count of smaller values in the other, found by binary search.
+// Leaves the order in sh.key[0, n) and sh.idx[0, n); touches no other key.
+template <int E>
+__device__ __forceinline__ void sort_small_merge(SelectShared &sh, int n, const uint32_t (&k)[E]) {
+  static_assert(E == 1 || E == 2, "one or two keys a thread");
+  constexpr int NV = 2 * kSelThreads;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint64_t below = (1ull << lane) - 1ull;
-  uint32_t *kA = sh.key, *kB = sh.key + 4096;
-  uint16_t *iA = sh.idx, *iB = sh.idx + 4096;
-  uint16_t *cnt = sh.cnt;
-  for (int sft = 0; sft < 32; sft += DB) {
-    if (((diff >> sft) & DM) == 0) continue;
+  uint64_t a[2];
 #pragma unroll
-    for (int j = 0; j < EPT / 8; ++j)
-      reinterpret_cast<uint4 *>(cnt)[(EPT / 8) * tid + j] = make_uint4(0u, 0u, 0u, 0u);
-    __syncthreads();
-    uint32_t kk[R], dg[R], rk[R];
-    uint16_t ii[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      kk[r] = 0u;
-      ii[r] = 0;
-      dg[r] = 0u;
-      rk[r] = 0u;
-      if (r * kSelThreads >= n) continue;  // no key in this round (uniform)
-      const int pos = r * kSelThreads + tid;
-      const bool valid = pos < n;
-      kk[r] = valid ? kA[pos] : 0u;
-      ii[r] = valid ? iA[pos] : (uint16_t)0;
-      dg[r] = (kk[r] >> sft) & DM;
-      uint64_t same = __ballot(valid);
-#pragma unroll
-      for (int b = 0; b < DB; ++b) {
-        const uint64_t m = __ballot((dg[r] >> b) & 1u);
-        same &= ((dg[r] >> b) & 1u) ? m : ~m;
-      }
-      rk[r] = (uint32_t)__popcll(same & below);
-      if (valid && rk[r] == 0u) cnt[(dg[r] * R + r) * 16 + wave] = (uint16_t)__popcll(same);
-    }
-    __syncthreads();
-    // exclusive scan of the counts in (digit, round, wave) order
-    if constexpr (EPT == 16) {
-      scan_counts(sh);  // ends with a barrier
-    } else {
-      uint4 *c4 = reinterpret_cast<uint4 *>(cnt) + tid;
-      const uint4 a = *c4;
-      uint32_t w[4] = {a.x, a.y, a.z, a.w};
-      uint32_t run = 0u;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t lo = w[i] & 0xFFFFu, hi = w[i] >> 16;
-        w[i] = run | ((run + lo) << 16);
-        run += lo + hi;
-      }
-      uint32_t incl = run;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t y = __shfl_up(incl, off, 64);
-        if (lane >= off) incl += y;
-      }
-      if (lane == 63) sh.wsum[wave] = incl;
-      __syncthreads();
-      const uint32_t base = incl - run + waves_before<kSelThreads / 64>(sh.wsum, wave);
-      const uint32_t b2 = base * 0x10001u;  // every prefix is below 2^16: no carry between halves
-      *c4 = make_uint4(w[0] + b2, w[1] + b2, w[2] + b2, w[3] + b2);
-      __syncthreads();
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      if (r * kSelThreads + tid < n) {
-        const uint32_t dst = (uint32_t)cnt[(dg[r] * R + r) * 16 + wave] + rk[r];
-        kB[dst] = kk[r];
-        iB[dst] = ii[r];
-      }
-    }
-    __syncthreads();
-    uint32_t *tk = kA;
-    kA = kB;
-    kB = tk;
-    uint16_t *ti = iA;
-    iA = iB;
-    iB = ti;
+  for (int e = 0; e < 2; ++e) {
+    const int pos = tid * E + e;
+    a[e] = (e < E && pos < n) ? ((uint64_t)k[e < E ? e : 0] << 32) | (uint32_t)pos
+                              : (0xFFFFFFFFull << 32) | (uint32_t)(NV + 2 * tid + e);
   }
-  if (kA != sh.key) {
-    for (int i = tid; i < n; i += kSelThreads) {
-      sh.key[i] = kA[i];
-      sh.idx[i] = iA[i];
+  auto shfl64 = [](uint64_t x, int m) -> uint64_t {
+    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)x, m, 64);
+    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(x >> 32), m, 64);
+    return ((uint64_t)hi << 32) | lo;
+  };
+  // bitonic sort of the wave's 128 values: value i = 2 lane + e
+#pragma unroll
+  for (int kk = 2; kk <= 128; kk <<= 1) {
+    const bool asc = ((2 * lane) & kk) == 0;
+#pragma unroll
+    for (int j = kk >> 1; j > 1; j >>= 1) {
+      const int m = j >> 1;
+      const bool lower = (lane & m) == 0;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const uint64_t b = shfl64(a[e], m);
+        const uint64_t lo = a[e] < b ? a[e] : b, hi = a[e] < b ? b : a[e];
+        a[e] = lower == asc ? lo : hi;
+      }
+    }
+    const uint64_t lo = a[0] < a[1] ? a[0] : a[1], hi = a[0] < a[1] ? a[1] : a[0];
+    a[0] = asc ? lo : hi;
+    a[1] = asc ? hi : lo;
+  }
+  uint64_t *X = reinterpret_cast<uint64_t *>(sh.cnt), *Y = X + NV;
+  X[128 * wave + 2 * lane] = a[0];
+  X[128 * wave + 2 * lane + 1] = a[1];
+  __syncthreads();
+#pragma unroll
+  for (int L = 128; L < NV; L <<= 1) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int p = 2 * tid + e;
+      const uint64_t x = X[p];
+      const int r = p / L;
+      const uint64_t *other = X + (size_t)(r ^ 1) * L;
+      int c = 0;  // values of the other run below x
+#pragma unroll
+      for (int step = L; step >= 1; step >>= 1) {
+        const int q = c + step;
+        if (q <= L && other[q - 1] < x) c = q;
+      }
+      Y[(r & ~1) * L + (p - r * L) + c] = x;
     }
     __syncthreads();
+    uint64_t *t = X;
+    X = Y;
+    Y = t;
   }
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int p = 2 * tid + e;
+    if (p < n) {
+      const uint64_t x = X[p];
+      sh.key[p] = (uint32_t)(x >> 32);
+      sh.idx[p] = (uint16_t)(x & 0xFFFFu);
+    }
+  }
+  __syncthreads();
 }
 
 // Selection for n <= kLdsSort tokens.  Thread t owns tokens E t .. E t + E - 1
@@ -909,11 +883,11 @@ __device__ __forceinline__ void sort_small(SelectShared &sh, int n, uint32_t dif
 //   2. e = expf(l - max) into LDS (expf_ref: the reference's libm expf, bit
 //      for bit); thread 0 adds them left to right
 //      (attention.cpp:422-426); p = e * (1/sum)
-//   3. stable LSD radix sort of the 32-bit keys less the smallest one,
-//      skipping digits every key shares: order p descending, ties older
-//      first.  Up to 2 kSelThreads tokens: sort_small in LDS, 8 or 9 bits a
-//      pass (whichever needs fewer passes); above: 4 bits a pass, in
-//      registers
+//   3. stable sort of the 32-bit keys less the smallest one: order p
+//      descending, ties older first.  Up to 2 kSelThreads tokens:
+//      sort_small_merge (bitonic within waves, merges in LDS); above: an LSD
+//      radix sort, 4 bits a pass, in registers, skipping digits every key
+//      shares
 //   4. quad sums ((p0+p1)+p2)+p3 of the sorted order in parallel; thread 0
 //      runs the mass loop over them, then the single tokens
 //      (attention.cpp:454-472)
@@ -943,9 +917,9 @@ __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, fl
   // 8.9 -> 13.6 us).  The exponentials wait in LDS, not in registers,
   // meanwhile.  Up to 4
   // tokens a thread they stay there for the weights (step 5), above the keys
-  // the sort uses: sort_small's buffers sh.key[0, n) and [4096, 4096 + n)
-  // with n <= 2048, the 4-bit sort's sh.key[0, 4096).  At 8 a thread the
-  // weights recompute them from the logits in lg.
+  // the sort writes: sort_small_merge's sh.key[0, n) with n <= 2048 (its
+  // buffers are sh.cnt), the 4-bit sort's sh.key[0, 4096).  At 8 a thread
+  // the weights recompute them from the logits in lg.
   float *ef = reinterpret_cast<float *>(sh.key) + (E <= 2 ? 2048 : E == 4 ? 4096 : 0);
 #pragma unroll
   for (int e = 0; e < E; ++e)
@@ -975,18 +949,18 @@ __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, fl
       kand &= k[e];
     }
   }
-  // digits every key shares do not move anything: skip their passes
-  for (int off = 32; off > 0; off >>= 1) {
-    kor |= __shfl_xor(kor, off);
-    kand &= __shfl_xor(kand, off);
-  }
-  if ((tid & 63) == 0) {
-    sh.wsum[tid >> 6] = kor;
-    reinterpret_cast<uint32_t *>(sh.red)[tid >> 6] = kand;
-  }
-  __syncthreads();
   uint32_t diff = 0;
-  {
+  if constexpr (E > 2) {
+    // digits every key shares do not move anything: skip their passes
+    for (int off = 32; off > 0; off >>= 1) {
+      kor |= __shfl_xor(kor, off);
+      kand &= __shfl_xor(kand, off);
+    }
+    if ((tid & 63) == 0) {
+      sh.wsum[tid >> 6] = kor;
+      reinterpret_cast<uint32_t *>(sh.red)[tid >> 6] = kand;
+    }
+    __syncthreads();
     uint32_t o = 0, a = 0xFFFFFFFFu;
     for (int w = 0; w < (int)(blockDim.x >> 6); ++w) {
       o |= sh.wsum[w];
@@ -994,19 +968,11 @@ __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, fl
     }
     diff = o ^ a;
     kor = o;
+    __syncthreads();
   }
-  __syncthreads();
 
   if constexpr (E <= 2) {
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      sh.key[p0 + e] = k[e];
-      sh.idx[p0 + e] = (uint16_t)ix[e];
-    }
-    __syncthreads();
-    // 9-bit digits when they need fewer passes than 8-bit ones
-    if (radix_passes(diff, 9) < radix_passes(diff, 8)) sort_small<9>(sh, n, diff);
-    else sort_small<8>(sh, n, diff);
+    sort_small_merge<E>(sh, n, k);
   } else {
   // positions from n on sort after every token: the OR of the keys is at
   // least each of them, shares their common digits, and stable order puts
