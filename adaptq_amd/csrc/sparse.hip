@@ -798,8 +798,9 @@ __device__ __forceinline__ void scan_counts(SelectShared &sh) {
 // took 11.6-12.8 us of config 1 and 3's decodes; this one 9.1-9.4 us.)  Thread t holds positions E t .. E t + E - 1 (E = 1 or 2) as
 // 64-bit values key << 32 | position; its slots without a token (positions
 // from n on, and the second slot when E = 1) hold key 0xFFFFFFFF with a
-// position of 2,048 or more, distinct and after every token.  Each wave sorts its 128
-// values in registers (a bitonic network, partners by lane shuffles); four
+// position of 2,048 or more, distinct and after every token.  Each wave sorts
+// its 128 values in registers (a bitonic network, partners by DPP moves up to
+// lane ^ 8 and lane shuffles beyond); four
 // rounds of pairwise merges in LDS (sh.cnt as two 2,048-value buffers) then
 // give one run: a value's place in the merged run is its place in its own
 // run plus the count of smaller values in the other, found by binary search.
@@ -816,10 +817,22 @@ __device__ __forceinline__ void sort_small_merge(SelectShared &sh, int n, const 
     a[e] = (e < E && pos < n) ? ((uint64_t)k[e < E ? e : 0] << 32) | (uint32_t)pos
                               : (0xFFFFFFFFull << 32) | (uint32_t)(NV + 2 * tid + e);
   }
-  auto shfl64 = [](uint64_t x, int m) -> uint64_t {
-    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)x, m, 64);
-    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(x >> 32), m, 64);
-    return ((uint64_t)hi << 32) | lo;
+  // the value of lane ^ m: DPP within a row of 16 lanes (quad permutes for
+  // 1 and 2, row shifts by 4 either way, a row rotation by 8), lane shuffles
+  // for 16 and 32
+  auto xch = [&](uint32_t x, int m) -> uint32_t {
+    if (m == 1) return __builtin_amdgcn_update_dpp(0u, x, 0xB1, 0xF, 0xF, false);
+    if (m == 2) return __builtin_amdgcn_update_dpp(0u, x, 0x4E, 0xF, 0xF, false);
+    if (m == 4) {
+      const uint32_t up = __builtin_amdgcn_update_dpp(0u, x, 0x104, 0xF, 0xF, false);  // lane + 4
+      const uint32_t dn = __builtin_amdgcn_update_dpp(0u, x, 0x114, 0xF, 0xF, false);  // lane - 4
+      return (lane & 4) ? dn : up;
+    }
+    if (m == 8) return __builtin_amdgcn_update_dpp(0u, x, 0x128, 0xF, 0xF, false);
+    return (uint32_t)__shfl_xor((int)x, m, 64);
+  };
+  auto shfl64 = [&](uint64_t x, int m) -> uint64_t {
+    return ((uint64_t)xch((uint32_t)(x >> 32), m) << 32) | xch((uint32_t)x, m);
   };
   // bitonic sort of the wave's 128 values: value i = 2 lane + e
 #pragma unroll
