@@ -382,6 +382,44 @@ __device__ __forceinline__ float kdot_row(const uint8_t *row, int x, const float
     return kdot_words<PT, KB>(w, s_q, cbk);
   } else {
     float s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if constexpr (KB >= 2 && KB <= 4) {
+      // unpermuted rows (padded 256 and up) in 16-byte loads: CB bytes hold CC
+      // codes, a multiple of 8, so code jj still goes to s[jj % 8] in order
+      constexpr int CB = KB == 3 ? 48 : 16;
+      constexpr int CC = CB * 8 / KB;
+      if (x == 0 && P % CC == 0) {
+        const uint4 *r4 = reinterpret_cast<const uint4 *>(row);
+        for (int c = 0; c < P / CC; ++c) {
+          uint32_t w[CB / 4];
+#pragma unroll
+          for (int u = 0; u < CB / 16; ++u) {
+            const uint4 v = r4[c * (CB / 16) + u];
+            w[4 * u] = v.x;
+            w[4 * u + 1] = v.y;
+            w[4 * u + 2] = v.z;
+            w[4 * u + 3] = v.w;
+          }
+          auto byte = [&](int b) -> uint32_t { return (w[b >> 2] >> ((b & 3) * 8)) & 0xFFu; };
+#pragma unroll
+          for (int j = 0; j < CC; ++j) {
+            uint32_t code;
+            if constexpr (KB == 4) {
+              const uint32_t bb = byte(j >> 1);
+              code = (j & 1) ? (bb & 15u) : (bb >> 4);
+            } else if constexpr (KB == 2) {
+              code = (byte(j >> 2) >> (6 - 2 * (j & 3))) & 3u;
+            } else {
+              const int g = j >> 3;
+              const uint32_t w24 = (byte(3 * g) << 16) | (byte(3 * g + 1) << 8) | byte(3 * g + 2);
+              code = (w24 >> (21 - 3 * (j & 7))) & 7u;
+            }
+            s[j & 7] = fmaf(cbk[code], s_q[c * CC + j], s[j & 7]);
+          }
+        }
+        const float t0 = s[0] + s[4], t1 = s[1] + s[5], t2 = s[2] + s[6], t3 = s[3] + s[7];
+        return (t0 + t1) + (t2 + t3);
+      }
+    }
     for (int j = 0; j < P; j += 8)
 #pragma unroll
       for (int L = 0; L < 8; ++L)

@@ -86,6 +86,10 @@ def test_config1_selection(oracle):
     (64, 4, 4, 9000, 0.95, 1.0),      # item sort, 5 blocks a pass
     (128, 4, 2, 12000, 0.9999, 3.0),  # item sort, peaked
     (64, 2, 2, 65536, 0.95, 1.0),     # item sort at its size limit
+    (32, 4, 2, 600, 0.95, 1.0),       # padded 32: K rows in XOR order, codes read a byte at a time
+    (200, 4, 3, 700, 0.95, 3.0),      # padded 256: 16-byte row loads in the logits kernel
+    (512, 3, 4, 1200, 0.95, 1.0),     # padded 512, 3-bit K: 48-byte chunks
+    (1000, 2, 2, 900, 0.99, 1.0),     # padded 1024, 2-bit K
 ])
 def test_selection_paths(oracle, dim, kb, vb, n_tok, v_mass, peak):
     rng = np.random.default_rng(1000 + n_tok)
