@@ -1945,6 +1945,11 @@ SplitPlan decode_plan(int n_items, const DecodeShape &sh) {
   // Short rings at padded 64: one block per item streams up to four tiles per
   // wave, cheaper than a finalize launch (measured: 4 heads x 1,100 tokens
   // 13.8 -> 11.2 us; at padded 128 the extra tiles cost more than it saves)
+  // fp32 mirrors at padded 64 carry 512 bytes a token: chunks down to one
+  // tile, about one block a CU, merged by the finalize launch (measured:
+  // config 2's hybrid step, 24 calls of 14 heads x 512 tokens, 268 -> 252 us
+  // with 128-token chunks, 241-248 us with 64; one block per head before)
+  if (lut && sh.raw && sh.padded == 64) return plan_splits(n_items, max_n, kTile, 256);
   if (lut && sh.padded == 64 && max_n <= 4 * kLutWaves * kTile) {
     SplitPlan sp;
     sp.splits = 1;
