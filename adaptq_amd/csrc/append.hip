@@ -313,6 +313,11 @@ __device__ __forceinline__ void encode_row(const HeadDesc *d, const RingState st
   const bool write_ring = cap > 0 && t >= n_tok - cap;
   const int slot = cap > 0 ? (int)(((long long)st.head + t) % cap) : 0;
   const bool write_mirror = t < mirror_count(st, n_tok, cap, d->hyb);
+  if constexpr (UNIFORM) {
+    // a wave whose tokens the same call evicts and the mirror does not take
+    // reads nothing (the lanes of a wave all return or none do)
+    if (!__any(write_ring || write_mirror)) return;
+  }
 
   float buf[P];
   // a wave whose 64 rows are all in the batch loads them by row segments

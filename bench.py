@@ -619,15 +619,16 @@ def secondary(L, last_error, torch, np, stream, reps=20, which=("C1", "C2", "C3"
         md = stack([(nh, 128, 4, 4, cap, 7, 0.95, 512)])
         ok(L.adaptq_mha_append_all_device(md[0], dp(kd), dp(vd), ntok, 0, sp))
         usd = span(lambda: ok(L.adaptq_mha_compute_all_device(md[0], dp(qd[0]), dp(od[0]), sp)))
+        # the 7,232 tokens per head that the same call evicts are neither
+        # coded nor stored, and a wave of 64 of them is not read either (the
+        # first 7,232 = 113 x 64 rows of each head): bytes = the rows read +
+        # the survivors' codes and scales written
+        rows_read = ntok - ((ntok - cap) // 64) * 64
         res["C4"] = {
-            # the 7,232 tokens per head that the same call evicts are read but
-            # never coded or stored (a row that is overwritten within the
-            # call is not encoded): bytes = every row read + the survivors'
-            # codes and scales written
             "append_40000": dict(
-                rate(app_us, nh * (ntok * 8 * 128 + cap * (append_bytes_per_token(128, 128, 4, 4)
-                                                           - 8 * 128))),
-                rows_read_per_head=ntok, rows_encoded_per_head=cap,
+                rate(app_us, nh * (rows_read * 8 * 128 + cap * (append_bytes_per_token(128, 128, 4, 4)
+                                                                - 8 * 128))),
+                rows_read_per_head=rows_read, rows_encoded_per_head=cap,
                 rows_evicted_in_call_not_encoded_per_head=ntok - cap),
             "queries_64_one_launch": dict(rate(us, nq * per_query), per_query_bytes=per_query),
             "query_1": rate(us1, per_query),
