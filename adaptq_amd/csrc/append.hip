@@ -412,6 +412,37 @@ __global__ __launch_bounds__(128, 3) void append_kernel(HeadDesc *const *descs, 
                                 bd.q2[0], bd.q2[1], bd.q2[2]);
 }
 
+// Both sides of a head-per-block append in one launch: blockIdx.z 0 codes
+// the K rows (KB bits), 1 the V rows, each block as append_kernel's UNIFORM
+// blocks do (one head, 128 tokens).  No block advances the ring states (a V
+// block could run before a K block of the same head has read them):
+// commit_kernel follows.  One launch instead of two lets the second side's
+// blocks fill the CUs while the first side's last blocks drain.
+template <int P, int KB, int VB>
+__global__ __launch_bounds__(128, 3) void append_pair_kernel(HeadDesc *const *descs,
+                                                          const float *__restrict__ keys,
+                                                          const float *__restrict__ vals,
+                                                          int n_tok, int dim, float inv_sqrt_p,
+                                                          float sqrt_p, BdThr bd) {
+  __shared__ Q4Cell s_q4[(KB == 4 || VB == 4) ? kQ4Cells : 1];
+  if constexpr (KB == 4 || VB == 4) {
+    static constexpr Q4Table kTab = q4_table();
+    if (threadIdx.x < kQ4Cells) s_q4[threadIdx.x] = kTab.c[threadIdx.x];
+    __syncthreads();
+  }
+  const int c = blockIdx.y;
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  const HeadDesc *d = descs[c];
+  const RingState st = d->st;
+  if (t >= n_tok) return;
+  if (blockIdx.z == 0)
+    encode_row<P, KB, true, KB == 2>(d, st, c, t, 0, keys, n_tok, dim, inv_sqrt_p, sqrt_p, s_q4,
+                                     bd.q2[0], bd.q2[1], bd.q2[2]);
+  else
+    encode_row<P, VB, true, VB == 2>(d, st, c, t, 1, vals, n_tok, dim, inv_sqrt_p, sqrt_p, s_q4,
+                                     bd.q2[0], bd.q2[1], bd.q2[2]);
+}
+
 // Both sides of one token per head in one launch (n_tok == 1, lanes over
 // heads): each lane encodes its head's K row, then its V row, and advances the
 // head's ring state, which no other lane reads.  Halves the launches of a
@@ -637,6 +668,14 @@ hipError_t launch_side(HeadDesc *const *descs, int n_ctx, int side, int bits, co
 
 }  // namespace
 
+// Blocks per side up to which a head-per-block append runs both sides in one
+// launch (append_pair_kernel): a few rounds of blocks per CU, whose last round
+// leaves CUs idle in a launch of one side (measured: config 4's 40,000-token
+// append, 2,504 blocks a side, 96 -> 78 us).  Above, one launch per side (a
+// config-5 chunk, 65,536 blocks a side: 30.0 ms for 16 chunks against 31.3
+// paired, whose 4-bit/2-bit codec pair keeps 20 bytes in scratch).
+constexpr long long kPairMaxBlocks = 8192;
+
 // Token-heads up to which an append takes a wave per vector (above, a lane
 // per vector keeps the launch to a few waves' worth of work per CU).
 constexpr int kOneWaveMaxVectors = 16384;
@@ -681,6 +720,32 @@ hipError_t launch_append(HeadDesc *const *descs, int n_ctx, int dim, int padded,
 #undef AQ_KV_V
 #undef AQ_KV
     return hipErrorInvalidValue;
+  }
+  if ((padded == 64 || padded == 128) && head_per_block(n_ctx, n_tok) &&
+      !commit_in_kernel(n_ctx, n_tok) && k_bits >= 2 && k_bits <= 4 && v_bits >= 2 &&
+      v_bits <= 4 && (long long)n_ctx * ((n_tok + 127) / 128) <= kPairMaxBlocks) {
+    // both sides in one launch, then the ring states
+    const float sp = sqrtf((float)padded), isp = 1.0f / sp;
+    const dim3 grid((unsigned)((n_tok + 127) / 128), (unsigned)n_ctx, 2u);
+    static const BdThr bd64 = bd_thresholds(1.0f / sqrtf(64.0f), sqrtf(64.0f));
+    static const BdThr bd128 = bd_thresholds(1.0f / sqrtf(128.0f), sqrtf(128.0f));
+    const BdThr bd = padded == 64 ? bd64 : bd128;
+    bool launched = false;
+#define AQ_PAIR(P_, KB_, VB_)                                                                    \
+  if (!launched && padded == P_ && k_bits == KB_ && v_bits == VB_) {                             \
+    append_pair_kernel<P_, KB_, VB_><<<grid, 128, 0, s>>>(descs, keys, vals, n_tok, dim, isp, sp, \
+                                                          bd);                                    \
+    launched = true;                                                                              \
+  }
+#define AQ_PAIR_V(P_, KB_) AQ_PAIR(P_, KB_, 2) AQ_PAIR(P_, KB_, 3) AQ_PAIR(P_, KB_, 4)
+    AQ_PAIR_V(64, 2) AQ_PAIR_V(64, 3) AQ_PAIR_V(64, 4)
+    AQ_PAIR_V(128, 2) AQ_PAIR_V(128, 3) AQ_PAIR_V(128, 4)
+#undef AQ_PAIR_V
+#undef AQ_PAIR
+    if (!launched) return hipErrorInvalidValue;
+    if (const hipError_t e1 = hipGetLastError(); e1 != hipSuccess) return e1;
+    commit_kernel<<<(n_ctx + 255) / 256, 256, 0, s>>>(descs, n_ctx, n_tok);
+    return hipGetLastError();
   }
   hipError_t e = hipSuccess;
   const bool fold = padded <= 128 && commit_in_kernel(n_ctx, n_tok);
