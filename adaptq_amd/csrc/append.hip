@@ -677,15 +677,25 @@ hipError_t launch_side(HeadDesc *const *descs, int n_ctx, int side, int bits, co
 constexpr long long kPairMaxBlocks = 8192;
 
 // Token-heads up to which an append takes a wave per vector (above, a lane
-// per vector keeps the launch to a few waves' worth of work per CU).
+// per vector keeps the launch to a few waves' worth of work per CU).  Without
+// mirror rows to copy, a lane per vector with both sides in one launch is
+// faster from a few thousand up (measured: config 1's 2,048 tokens x 4 heads
+// 14.5 -> 11.5 us, config 2's 24 appends of 512 tokens x 14 heads 272 -> 228
+// us); with them it is slower (config 1 hybrid 15-17 -> 23-27 us, config 2
+// hybrid 305-309 -> 556-558 us).
 constexpr int kOneWaveMaxVectors = 16384;
+constexpr int kOneWaveMaxPacked = 4096;
 
 hipError_t launch_append(HeadDesc *const *descs, int n_ctx, int dim, int padded, int k_bits,
                          int v_bits, const float *keys, const float *vals, int n_tok,
-                         hipStream_t s) {
+                         hipStream_t s, bool mirror) {
   if (n_ctx <= 0 || n_tok <= 0) return hipSuccess;
+  // a lane per vector copies a mirror row by itself, a wave per vector with
+  // its 64 lanes: appends that copy rows stay a wave per vector up to
+  // kOneWaveMaxVectors, the others only up to kOneWaveMaxPacked
+  const long long one_wave_max = mirror ? kOneWaveMaxVectors : kOneWaveMaxPacked;
   if ((padded == 64 || padded == 128) && n_tok <= 65535 &&
-      (long long)n_ctx * n_tok <= kOneWaveMaxVectors) {
+      (long long)n_ctx * n_tok <= one_wave_max) {
     // few vectors: a wave per vector, a block per token and head (both sides;
     // the ring states in the kernel for one token, by commit_kernel for more)
     const float sp = sqrtf((float)padded), isp = 1.0f / sp;

@@ -411,6 +411,14 @@ struct Mha {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Whether appending n tokens to these contexts copies any to a hybrid mirror
+// (from the host's ring states; it picks the append's launch shape only).
+bool any_mirror(const std::vector<Ctx *> &cs, int n) {
+  for (const Ctx *c : cs)
+    if (aq::mirror_count(c->st, n, c->cap, c->hyb) > 0) return true;
+  return false;
+}
+
 struct DeviceGuard {
   int prev = -1;
   explicit DeviceGuard(int dev) {
@@ -580,7 +588,7 @@ bool flush_locked(Ctx *c, const char *fn, bool host_wait = false) {
     }
     if (e == hipSuccess)
       e = aq::launch_append(c->d_desc_list, 1, c->dim, c->padded, c->k_bits, c->v_bits, dk, dk + n,
-                            c->staged, s);
+                            c->staged, s, aq::mirror_count(c->st, c->staged, c->cap, c->hyb) > 0);
     if (hip_fail(e, fn)) return false;
     c->stage_seq = lib_end(c->device);
     c->st = aq::ring_after(c->st, c->staged, c->cap, c->hyb);
@@ -864,7 +872,7 @@ bool flush_all_locked(Mha *m, const char *fn, bool host_wait = false) {
   }
   if (e == hipSuccess)
     e = aq::launch_append(static_cast<aq::HeadDesc **>(m->d_list.p), H, c0->dim, c0->padded,
-                          c0->k_bits, c0->v_bits, dk, dk + per * H, S, s);
+                          c0->k_bits, c0->v_bits, dk, dk + per * H, S, s, any_mirror(m->heads, S));
   if (hip_fail(e, fn)) return false;
   m->stage_seq = lib_end(m->device);
   for (Ctx *c : m->heads) {
@@ -1297,7 +1305,8 @@ int adaptq_mha_append_all_device(adaptq_mha_t h, const float *d_keys, const floa
   hipError_t e = caller_begin(m->device, s);
   if (e == hipSuccess)
     e = aq::launch_append(static_cast<aq::HeadDesc **>(m->d_list.p), m->n_heads, c0->dim,
-                          c0->padded, c0->k_bits, c0->v_bits, d_keys, d_vals, n_tokens, s);
+                          c0->padded, c0->k_bits, c0->v_bits, d_keys, d_vals, n_tokens, s,
+                          any_mirror(m->heads, n_tokens));
   if (e == hipSuccess) e = caller_end(m->device, s);
   if (hip_fail(e, fn)) return -1;
   for (Ctx *c : m->heads) c->st = aq::ring_after(c->st, n_tokens, c->cap, c->hyb);
@@ -1348,7 +1357,8 @@ int adaptq_mha_append_compute_all_device(adaptq_mha_t h, const float *d_keys,
   if (n == -2) {  // the append and the decode as two launches
     const Ctx *c0 = m->heads[0];
     if (hip_fail(aq::launch_append(static_cast<aq::HeadDesc **>(m->d_list.p), m->n_heads, c0->dim,
-                                   c0->padded, c0->k_bits, c0->v_bits, d_keys, d_vals, 1, s),
+                                   c0->padded, c0->k_bits, c0->v_bits, d_keys, d_vals, 1, s,
+                                   any_mirror(m->heads, 1)),
                  fn))
       return -1;
     for (Ctx *c : m->heads) c->st = aq::ring_after(c->st, 1, c->cap, c->hyb);
@@ -1515,7 +1525,7 @@ int adaptq_ggml_append_f32_device(adaptq_mha_t h, const float *d_k, const float 
   if (e == hipSuccess) e = aq::launch_gather_rows(dv, d_v, H, n_tokens, head_dim, v_nb1, v_nb2, s);
   if (e == hipSuccess)
     e = aq::launch_append(static_cast<aq::HeadDesc **>(m->d_list.p), H, c0->dim, c0->padded,
-                          c0->k_bits, c0->v_bits, dk, dv, n_tokens, s);
+                          c0->k_bits, c0->v_bits, dk, dv, n_tokens, s, any_mirror(m->heads, n_tokens));
   if (e == hipSuccess) e = caller_end(m->device, s);
   if (hip_fail(e, fn)) return -1;
   for (Ctx *c : m->heads) c->st = aq::ring_after(c->st, n_tokens, c->cap, c->hyb);
@@ -1739,7 +1749,8 @@ int adaptq_plan_append_device(adaptq_plan_t h, const float *d_keys, const float 
   hipError_t e = caller_begin(p->device, s);
   if (e == hipSuccess)
     e = aq::launch_append(static_cast<aq::HeadDesc **>(p->d_list.p), (int)p->ctxs.size(), c0->dim,
-                          c0->padded, c0->k_bits, c0->v_bits, d_keys, d_vals, n_tokens, s);
+                          c0->padded, c0->k_bits, c0->v_bits, d_keys, d_vals, n_tokens, s,
+                          any_mirror(p->ctxs, n_tokens));
   if (e == hipSuccess) e = caller_end(p->device, s);
   if (hip_fail(e, fn)) return -1;
   // Every context takes the same n_tokens: update the host ring states and

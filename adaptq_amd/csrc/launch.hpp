@@ -10,9 +10,12 @@ namespace aq {
 // Quantise and insert n_tok tokens into each of n_ctx heads.
 // keys, vals: device [n_ctx][n_tok][dim] fp32.  All heads share padded,
 // k_bits, v_bits and dim.  Advances every head's device ring state.
+// mirror: whether any head may copy tokens to its hybrid mirror in this call
+// (from the host's view of the ring states); it only picks between launch
+// shapes, the result is the same either way.
 hipError_t launch_append(HeadDesc *const *d_descs, int n_ctx, int dim, int padded,
                          int k_bits, int v_bits, const float *keys, const float *vals,
-                         int n_tok, hipStream_t stream);
+                         int n_tok, hipStream_t stream, bool mirror);
 
 // Zero a head's device ring state (reset).
 hipError_t launch_reset_state(HeadDesc *const *d_descs, int n_ctx, hipStream_t stream);
