@@ -128,6 +128,26 @@ AQ_SEQ_HD int split_class(double P, double x, double del, int E) {
   return kUnc;
 }
 
+// Class of a thread's run of terms predicted from fp32 sums (P: s before the
+// run, within about 2^-19 P of the exact value when it comes from a scan of
+// at most 2^15 fp32 partial sums; loc: the run's own sum; jend: the terms
+// since the sum's start at the run's end): the grid exponent eu = B - 23
+// when [P - del, P + loc + del] with del = (jend + 64) 2^-22 (P + loc) lies
+// in the binade [2^B, 2^(B+1)) with room for the last rounding, else kUnc.
+// del is four times the chain's own drift bound plus the prefix error; a
+// prediction only chooses the path (the walk checks every class it uses).
+AQ_SEQ_HD int run_class_f32(float P, float loc, int jend) {
+  const float top = P + loc;
+  const float del = (float)(jend + 64) * 0x1p-22f * top;
+  const float lo = P - del, hi = top + del;
+  if (!(lo >= 0x1p-100f) || !(hi < 0x1p127f)) return kUnc;
+  uint32_t b;
+  __builtin_memcpy(&b, &lo, sizeof b);
+  const int B = (int)(b >> 23) - 127;  // lo in [2^B, 2^(B+1))
+  if (!(hi < __builtin_ldexpf(1.0f, B + 1) - __builtin_ldexpf(1.0f, B - 20))) return kUnc;
+  return B - 23;
+}
+
 // term_incr for a term known to fit its class: x / 2^eu is exact in fp32
 // (below 2^24), so the increment is its nearest integer; false for a tie.
 AQ_SEQ_HD bool scaled_incr(float x, int eu, uint32_t &r) {

@@ -671,39 +671,6 @@ __device__ __forceinline__ float key_p(uint64_t k) { return hi_p((uint32_t)(k >>
 __device__ __forceinline__ int key_i(uint64_t k) { return (int)(uint32_t)k; }
 
 
-// acc + s[0] + s[1] + ... + s[m-1], left to right, one lane.  s is 16-byte
-// aligned LDS; two register buffers alternate, so the reads of the next 32
-// values are in flight while the current 32 are added.
-__device__ __forceinline__ void load32(float4 (&r)[8], const float4 *s4, int b) {
-#pragma unroll
-  for (int k = 0; k < 8; ++k) r[k] = s4[8 * b + k];
-}
-__device__ __forceinline__ float add32(float acc, const float4 (&r)[8]) {
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    acc = __fadd_rn(acc, r[k].x);
-    acc = __fadd_rn(acc, r[k].y);
-    acc = __fadd_rn(acc, r[k].z);
-    acc = __fadd_rn(acc, r[k].w);
-  }
-  return acc;
-}
-__device__ float serial_sum(const float *s, int m, float acc) {
-  const float4 *s4 = reinterpret_cast<const float4 *>(s);
-  const int nb = m / 32;
-  float4 A[8], B[8];
-  if (nb > 0) load32(A, s4, 0);
-  for (int b = 0; b < nb; b += 2) {
-    if (b + 1 < nb) load32(B, s4, b + 1);
-    acc = add32(acc, A);
-    if (b + 1 >= nb) break;
-    if (b + 2 < nb) load32(A, s4, b + 2);
-    acc = add32(acc, B);
-  }
-  for (int i = 32 * nb; i < m; ++i) acc = __fadd_rn(acc, s[i]);
-  return acc;
-}
-
 // The reference's mass loop over quad sums q[0..m): while mass < v_mass, add
 // the next one.  Returns how many it takes; *mass is updated.  The sums are
 // >= 0, so the running mass never decreases (and stays NaN once NaN): the
@@ -963,25 +930,25 @@ __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, fl
     if (p0 + e < n && ev[e] > mx) mx = ev[e];
   mx = block_max(mx, sh);
 
-  // the exponentials' left-to-right sum (attention.cpp:422-426), one lane's
-  // chain (block_seq_sum is slower at these lengths: 4 heads x 2,048 tokens
-  // 8.9 -> 13.6 us).  The exponentials wait in LDS, not in registers,
-  // meanwhile.  Up to 4
-  // tokens a thread they stay there for the weights (step 5), above the keys
-  // the sort writes: sort_small_merge's sh.key[0, n) with n <= 2048 (its
-  // buffers are sh.cnt), the 4-bit sort's sh.key[0, 4096).  At 8 a thread
-  // the weights recompute them from the logits in lg.
+  // the exponentials' left-to-right sum (attention.cpp:422-426), bit for
+  // bit, by chain_sum_block: each thread classifies its own E terms, one
+  // wave walks (one lane's chain took 8.9 us for 4 heads x 2,048 tokens,
+  // block_seq_sum 13.6).  The exponentials also go to LDS (the walk's
+  // hardware terms read them there).  Up to 4 tokens a thread they stay
+  // there for the weights (step 5), above the keys the sort writes:
+  // sort_small_merge's sh.key[0, n) with n <= 2048 (its buffers are sh.cnt),
+  // the 4-bit sort's sh.key[0, 4096).  At 8 a thread the weights recompute
+  // them from the logits in lg.
+  static_assert(sizeof(ChainShared) <= sizeof(sh.cnt), "chain_sum_block's LDS in sh.cnt");
+  ChainShared &cs = *reinterpret_cast<ChainShared *>(sh.cnt);
   float *ef = reinterpret_cast<float *>(sh.key) + (E <= 2 ? 2048 : E == 4 ? 4096 : 0);
 #pragma unroll
-  for (int e = 0; e < E; ++e)
-    if (p0 + e < n) ef[p0 + e] = expf_ref(ev[e] - mx);
+  for (int e = 0; e < E; ++e) {
+    ev[e] = p0 + e < n ? expf_ref(ev[e] - mx) : 0.0f;
+    if (p0 + e < n) ef[p0 + e] = ev[e];
+  }
   __syncthreads();
-  if (tid == 0) sh.bcast[0] = 1.0f / serial_sum(ef, n, 0.0f);
-  __syncthreads();
-  const float inv = sh.bcast[0];
-#pragma unroll
-  for (int e = 0; e < E; ++e) ev[e] = ef[p0 + e];
-  __syncthreads();
+  const float inv = 1.0f / chain_sum_block<E, false>(ev, n, 0.0f, __builtin_inff(), ef, cs).s;
 
   // Keys are sorted less the smallest one, key_hi(inv): every e is at most
   // 1 (or NaN), so every p = e inv is at most inv (or NaN, whose key is the
@@ -1076,16 +1043,29 @@ __device__ __forceinline__ void select_small(const HeadDesc *d, float v_mass, fl
   __syncthreads();
   }
 
+  // the mass loop (attention.cpp:454-472): quad sums ((p0+p1)+p2)+p3 of the
+  // sorted order, EQ consecutive ones a thread, added while the mass is below
+  // v_mass by chain_sum_block; then, if every quad went in, the single tokens
+  // on one lane
+  constexpr int EQ = E >= 4 ? E / 4 : 1;
   const int n_quads = n / 4;
-  for (int q = tid; q < n_quads; q += blockDim.x)
-    sh.stage[q] = __fadd_rn(__fadd_rn(__fadd_rn(hi_p(sh.key[4 * q] + kmin), hi_p(sh.key[4 * q + 1] + kmin)),
-                                      hi_p(sh.key[4 * q + 2] + kmin)),
-                            hi_p(sh.key[4 * q + 3] + kmin));
+  float qv[EQ];
+#pragma unroll
+  for (int e = 0; e < EQ; ++e) {
+    const int q = tid * EQ + e;
+    qv[e] = 0.0f;
+    if (q < n_quads) {
+      qv[e] = __fadd_rn(__fadd_rn(__fadd_rn(hi_p(sh.key[4 * q] + kmin), hi_p(sh.key[4 * q + 1] + kmin)),
+                                  hi_p(sh.key[4 * q + 2] + kmin)),
+                        hi_p(sh.key[4 * q + 3] + kmin));
+      sh.stage[q] = qv[e];
+    }
+  }
   __syncthreads();
-  // the mass loop, on one lane (attention.cpp:454-472)
+  const SeqResult mq = chain_sum_block<EQ, true>(qv, n_quads, 0.0f, v_mass, sh.stage, cs);
   if (tid == 0) {
-    float mass = 0.0f;
-    int ii = 4 * mass_scan(sh.stage, n_quads, v_mass, &mass);
+    float mass = mq.s;
+    int ii = 4 * mq.count;
     for (; ii < n && mass < v_mass; ++ii) mass = __fadd_rn(mass, hi_p(sh.key[ii] + kmin));
     sh.cut = ii;
   }

@@ -291,6 +291,135 @@ static float model_global(const std::vector<float> &x, int T, int W, double bias
   return s;
 }
 
+// the value after segment k: the next segment's start, or the final sum
+static uint32_t k_end_of(int k, int nseg, const std::vector<uint32_t> &sst, uint32_t fin) {
+  return k + 1 < nseg ? sst[k + 1] : fin;
+}
+
+static long long g_wcases = 0, g_wsegs = 0, g_wredo = 0, g_wclean_stop = 0;
+
+// chain_sum_block (seqsum.hpp) serially.  Threads of E consecutive terms,
+// each classified as one (run_class_f32) from the prefix (times `bias`,
+// to plant mispredictions).  A segment ends at a hardware thread, at the
+// last clean thread before a different class, or at the last thread; its
+// record: the class of its clean threads (or none), the block's inclusive
+// sum of r at its end, its last thread.  The walk adds each segment's
+// increment to K (checked: s in the class's binade, K below 2^24) and then
+// its hardware thread's terms; a failed check redoes the whole chain.  The
+// stop: the first segment whose end reaches it; inside its clean part the
+// thread whose K range holds the threshold steps through its terms.
+static Res model_wave(const std::vector<float> &x, float s0, float stop, int E, double bias) {
+  const int m = (int)x.size(), nt = (m + E - 1) / E;
+  ++g_wcases;
+  for (float v : x)
+    if (!(v >= 0.0f && v <= 3.402823466e38f)) return chain(x, s0, stop);
+  if (!(s0 < stop) || m == 0) return {0, s0};
+  std::vector<int> cls(nt, kUnc);
+  std::vector<uint32_t> rs(nt, 0), Rb(nt, 0);
+  double P = (double)s0;
+  uint32_t run = 0;
+  for (int t = 0; t < nt; ++t) {
+    const int j0 = t * E;
+    float loc = 0.0f;
+    for (int e = 0; e < E && j0 + e < m; ++e) loc += x[j0 + e];
+    int c = run_class_f32((float)(P * bias), loc, j0 + E);
+    uint32_t r_sum = 0;
+    if (c != kUnc)
+      for (int e = 0; e < E && j0 + e < m; ++e) {
+        uint32_t r = 0;
+        if (!term_incr(x[j0 + e], c, r) || r >= (kTop >> 1)) c = kUnc;  // fast_incr's limits
+        r_sum += r;
+      }
+    if (c == kUnc || r_sum >= (kTop >> 1)) {
+      c = kUnc;
+      r_sum = 0;
+    }
+    cls[t] = c;
+    rs[t] = r_sum;
+    run += r_sum;
+    Rb[t] = run;
+    P += (double)loc;
+  }
+  struct Rec {
+    int cls;
+    uint32_t R;
+    int end;
+  };
+  std::vector<Rec> rec;
+  for (int t = 0; t < nt; ++t) {
+    const int c = cls[t], cn = t + 1 < nt ? cls[t + 1] : kNoClass;
+    if (c == kUnc || t == nt - 1 || (cn != kUnc && cn != c)) {
+      const int cp = t > 0 ? cls[t - 1] : kUnc;
+      rec.push_back({c != kUnc ? c : (cp != kUnc ? cp : kNoClass), Rb[t], t});
+    }
+  }
+  const int nseg = (int)rec.size();
+  g_wsegs += nseg;
+  // the walk, every segment, with the start and after-clean-part values
+  std::vector<uint32_t> sst(nseg), smid(nseg);
+  uint32_t wb = fbits(s0);
+  bool fail = false;
+  for (int k = 0; k < nseg; ++k) {
+    const uint32_t in = rec[k].R - (k ? rec[k - 1].R : 0u), mant = wb & 0x7FFFFFu;
+    sst[k] = wb;
+    if (rec[k].cls != kNoClass && !(((wb >> 23) == (uint32_t)(rec[k].cls + 150)) && mant + in < 0x800000u))
+      fail = true;
+    wb += in;
+    smid[k] = wb;
+    if (cls[rec[k].end] == kUnc) {
+      float sv = bfloat(wb);
+      for (int e = 0; e < E; ++e) {
+        const int i = rec[k].end * E + e;
+        sv = sv + (i < m ? x[i] : 0.0f);
+      }
+      wb = fbits(sv);
+    }
+  }
+  if (fail) {
+    ++g_wredo;
+    return chain(x, s0, stop);
+  }
+  if (!(bfloat(wb) >= stop)) return {m, bfloat(wb)};
+  int ks_seg = 0;
+  while (!(bfloat(k_end_of(ks_seg, nseg, sst, wb)) >= stop)) ++ks_seg;
+  const int k = ks_seg;
+  const int start = k ? rec[k - 1].end + 1 : 0;
+  if (bfloat(smid[k]) >= stop) {
+    // inside the clean part: the thread whose K range holds the threshold
+    ++g_wclean_stop;
+    const int c = rec[k].cls;
+    const uint32_t K0 = 0x800000u | (sst[k] & 0x7FFFFFu), ks = kstop_of(stop, c);
+    const uint32_t Rp = k ? rec[k - 1].R : 0u;
+    for (int t = start; t <= rec[k].end; ++t) {
+      if (cls[t] == kUnc) continue;
+      uint32_t Kb = K0 + (Rb[t] - rs[t] - Rp);
+      const uint32_t Ka = Kb + rs[t];
+      if (!(Kb < ks && Ka >= ks)) continue;
+      int e = 0;
+      for (; e < E; ++e) {
+        if (Kb >= ks) break;
+        uint32_t r = 0;
+        term_incr(t * E + e < m ? x[t * E + e] : 0.0f, c, r);
+        Kb += r;
+      }
+      const int cnt = t * E + e;
+      return {cnt < m ? cnt : m, bfloat((sst[k] & 0xFF800000u) | (Kb - 0x800000u))};
+    }
+    return {-1, 0.0f};  // unreachable
+  }
+  // inside the hardware thread's terms
+  const int t = rec[k].end;
+  float sv = bfloat(smid[k]);
+  for (int e = 0; e < E; ++e) {
+    const int i = t * E + e;
+    if (i >= m) return {m, sv};
+    if (!(sv < stop)) return {i, sv};
+    sv = sv + x[i];
+  }
+  const int cnt = t * E + E;
+  return {cnt < m ? cnt : m, sv};
+}
+
 static long long g_cases = 0, g_bad = 0;
 
 // No stop: the pre-classified path of the softmax sum against the chain.
@@ -311,6 +440,19 @@ static void check_global(const std::vector<float> &x, const char *what) {
 
 static void check(const std::vector<float> &x, float s0, float stop, const char *what) {
   const Res a = chain(x, s0, stop);
+  for (int E : {1, 2, 4, 8}) {
+    if ((int)x.size() > 1024 * E) continue;
+    for (double bias : {1.0, 1.05, 0.97}) {
+      const Res b = model_wave(x, s0, stop, E, bias);
+      ++g_cases;
+      if (a.count != b.count || fbits(a.s) != fbits(b.s)) {
+        if (g_bad < 10)
+          std::printf("MISMATCH (per thread) %s n=%zu E=%d bias=%g stop=%a: chain (%d, %a) model (%d, %a)\n",
+                      what, x.size(), E, bias, (double)stop, a.count, (double)a.s, b.count, (double)b.s);
+        ++g_bad;
+      }
+    }
+  }
   for (int T : {8, 4, 2, 1}) {
     const Res b = model(x, s0, stop, T);
     ++g_cases;
@@ -329,7 +471,7 @@ int main() {
   std::uniform_real_distribution<double> ud(0.0, 1.0);
   const float inf = INFINITY;
   for (int rep = 0; rep < 6; ++rep) {
-    for (int n : {257, 1000, 5000, 33000}) {
+    for (int n : {5, 65, 257, 1000, 2048, 5000, 8192, 33000}) {
       for (double sig : {0.05, 1.0, 4.0}) {
         // softmax exponentials, their sum, the probabilities sorted
         // descending, their quad sums and mass stops
@@ -396,5 +538,7 @@ int main() {
   std::printf("%lld cases, %lld mismatches, %lld of %lld chunks redone, %lld with a serial tail; "
               "pre-classified: %lld windows redone, %lld of %lld chunks past %d segments\n",
               g_cases, g_bad, g_redo, g_chunks, g_tail, g_gredo, g_gtail, g_gchunks, kMaxSeg);
+  std::printf("per thread: %lld sums, %lld segments, %lld redone, %lld stops inside a clean part\n",
+              g_wcases, g_wsegs, g_wredo, g_wclean_stop);
   return g_bad == 0 ? 0 : 1;
 }
