@@ -780,4 +780,35 @@ __device__ __forceinline__ SeqResult chain_sum_block(const float (&x)[E], int m,
   return res;
 }
 
+// The chain over any number of terms, chunks of kBlock kMaxT through
+// chain_sum_block, each from the exact sum the one before ended with (the
+// next chunk's terms are requested before a chunk is walked).  load(i) for
+// 0 <= i < n returns term i; xs: kBlock kMaxT floats of LDS.  Called by all
+// kBlock threads with uniform arguments.
+template <bool STOP, class Load>
+__device__ __forceinline__ SeqResult chain_sum_long(Load load, int n, float s, float stop, float *xs,
+                                                    ChainShared &cs) {
+  using namespace seqsum_detail;
+  constexpr int E = kMaxT, C = kBlock * kMaxT;
+  const int j0 = threadIdx.x * E;
+  float x[E];
+#pragma unroll
+  for (int k = 0; k < E; ++k) x[k] = j0 + k < n ? load(j0 + k) : 0.0f;
+  for (int c0 = 0; c0 < n; c0 += C) {
+    const int cn = n - c0 < C ? n - c0 : C;
+#pragma unroll
+    for (int k = 0; k < E; ++k) xs[j0 + k] = x[k];
+    __syncthreads();
+    float y[E];
+#pragma unroll
+    for (int k = 0; k < E; ++k) y[k] = c0 + C + j0 + k < n ? load(c0 + C + j0 + k) : 0.0f;
+    const SeqResult r = chain_sum_block<E, STOP>(x, cn, s, stop, xs, cs);
+    s = r.s;
+    if (STOP && r.count < cn) return SeqResult{c0 + r.count, s};
+#pragma unroll
+    for (int k = 0; k < E; ++k) x[k] = y[k];
+  }
+  return SeqResult{n, s};
+}
+
 }  // namespace aq

@@ -1433,71 +1433,11 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
   if (__syncthreads_or(nan_e)) {
     if (tid == 0) s_bcast[0] = __builtin_nanf("");
   } else {
-    // the walk over sparse_sum_classify_kernel's chunk tables, kSeqWin
-    // chunks at a time: their terms and concatenated tables staged in LDS
-    // (the next window's requested before this one's walk)
-    using namespace seqsum_detail;
-    static_assert(kSeqWin * kSeqChunk == kBlock * kMaxT, "a window fills the terms' LDS");
-    constexpr int WT = kSeqWin * kSeqT;  // terms per thread and window
-    float *xs = sh.seq.xs;
-    int *w_start = sh.w_start, *w_cls = sh.w_cls;
-    uint32_t *w_inc = sh.w_inc;
-    float *w_x0 = sh.w_x0, *w_x1 = sh.w_x1;
-    const uint32_t *tabs = lg_tables(lg, n);
-    const int nch = seq_chunks(n);
-    const int j0 = tid * WT;
-    // a window's terms (this thread's) and table entries (entry tid of each
-    // chunk's), returned by value so they stay in registers
-    struct Fetched {
-      float x[WT];
-      uint32_t start[kSeqWin], cls[kSeqWin], inc[kSeqWin], x0[kSeqWin], x1[kSeqWin], m[kSeqWin];
-    };
-    auto fetch = [&](int c) -> Fetched {  // the window starting at chunk c
-      Fetched f;
-      const int w0 = c * kSeqChunk;
-#pragma unroll
-      for (int k = 0; k < WT; ++k) f.x[k] = w0 + j0 + k < n ? lg[w0 + j0 + k] : 0.0f;
-#pragma unroll
-      for (int h = 0; h < kSeqWin; ++h) {
-        const uint32_t *tab = tabs + (size_t)(c + h) * kSeqTab;
-        const bool have = c + h < nch;
-        f.m[h] = have ? tab[0] : 0u;
-        const bool mine = have && tid < kTabEnt;
-        f.start[h] = mine ? tab[kTabStart + tid] : 0u;
-        f.cls[h] = mine ? tab[kTabCls + tid] : 0u;
-        f.inc[h] = mine ? tab[kTabInc + tid] : 0u;
-        f.x0[h] = mine ? tab[kTabX0 + tid] : 0u;
-        f.x1[h] = mine ? tab[kTabX1 + tid] : 0u;
-      }
-      return f;
-    };
-    float sv = 0.0f;
-    Fetched F = fetch(0);
-    for (int c = 0; c < nch; c += kSeqWin) {
-      const int w0 = c * kSeqChunk, wn = n - w0 < kSeqWin * kSeqChunk ? n - w0 : kSeqWin * kSeqChunk;
-#pragma unroll
-      for (int k = 0; k < WT; ++k) xs[j0 + k] = F.x[k];
-      int m = 0;
-#pragma unroll
-      for (int h = 0; h < kSeqWin; ++h) {
-        if (tid < (int)F.m[h]) {
-          w_start[m + tid] = (int)F.start[h];
-          w_cls[m + tid] = (int)F.cls[h];
-          w_inc[m + tid] = F.inc[h];
-          w_x0[m + tid] = __uint_as_float(F.x0[h]);
-          w_x1[m + tid] = __uint_as_float(F.x1[h]);
-        }
-        m += (int)F.m[h];
-      }
-      if (tid == 0) w_start[m] = w0 + wn;
-      __syncthreads();
-      if (c + kSeqWin < nch) F = fetch(c + kSeqWin);
-      sv = seq_walk_flat(xs, w0, wn, w_start, w_cls, w_inc, w_x0, w_x1, m, sv);
-      if (tid == 0) s_bcast[1] = sv;
-      __syncthreads();
-      sv = s_bcast[1];
-      __syncthreads();  // the window's LDS is refilled next
-    }
+    // the left-to-right sum of the exponentials in lg, 8,192 terms at a time
+    static_assert(sizeof(ChainShared) <= sizeof(sh.cnt), "chain_sum_block's LDS in sh.cnt");
+    ChainShared &cs = *reinterpret_cast<ChainShared *>(sh.cnt);
+    const float sv =
+        chain_sum_long<false>([lg](int i) { return lg[i]; }, n, 0.0f, __builtin_inff(), sh.seq.xs, cs).s;
     if (tid == 0) s_bcast[0] = 1.0f / sv;
   }
   __syncthreads();
@@ -1546,6 +1486,7 @@ __global__ __launch_bounds__(kSelThreads) void sparse_cut_kernel(HeadDesc *const
   __shared__ int s_cut;
   __shared__ uint64_t s_last;
   __shared__ SeqShared s_seq;
+  __shared__ ChainShared s_cs;
   const int item = blockIdx.x;
   const int tid = threadIdx.x;
   const HeadDesc *d = item_desc[item];
@@ -1594,7 +1535,7 @@ __global__ __launch_bounds__(kSelThreads) void sparse_cut_kernel(HeadDesc *const
       s_cut = ii;
     }
   } else {
-    const SeqResult rq = block_seq_sum<8>(quad, n_quads, 0.0f, v_mass, s_seq);
+    const SeqResult rq = chain_sum_long<true>(quad, n_quads, 0.0f, v_mass, s_seq.xs, s_cs);
     // the single tokens run only after every whole quad, i.e. over the last
     // n % 4 tokens at most (once the mass reaches v_mass they add nothing)
     if (tid == 0) {
@@ -2050,7 +1991,6 @@ hipError_t launch_decode_sparse(HeadDesc *const *descs, int n_items, const Decod
     if (e != hipSuccess) return e;
     if (n > kSelectInBlock) {
       sparse_exp_kernel<<<g1, kThreads, 0, s>>>(dsc, w, stride);
-      sparse_sum_classify_kernel<<<dim3(seq_chunks(n), cnt), kSelThreads, 0, s>>>(dsc, w, stride);
       e = hipGetLastError();
       if (e != hipSuccess) return e;
     }
