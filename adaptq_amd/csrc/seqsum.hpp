@@ -509,7 +509,8 @@ __device__ __forceinline__ SeqResult block_seq_sum(Load load, int n, float s, fl
 //      of its clean threads (or none), the block's inclusive sum of r at its
 //      end and its last thread;
 //   3. wave 0 walks the records in order without branches: K += the
-//      segment's increment, then the hardware thread's terms by fp32 adds,
+//      segment's increment, then the hardware thread's terms by fp32 adds
+//      (lane k adds record k's terms; the walk keeps lane i's sum),
 //      recording the value each segment starts from; then every record
 //      checks its own start in parallel (as block_seq_sum does: s in the
 //      class's binade, K below 2^24 after the clean threads); a failed check
@@ -679,7 +680,8 @@ __device__ __forceinline__ SeqResult chain_sum_block(const float (&x)[E], int m,
         for (int e = 0; e < E; ++e) lx[e] = (le & kRecHw) && lt * E + e < m ? xs[lt * E + e] : 0.0f;
         const int cnt = nseg - base < 64 ? nseg - base : 64;
         // the walk: the running sum's bits stay in a vector register (the
-        // same in every lane), so no step waits on a scalar copy
+        // same in every lane); every lane adds its own record's hardware
+        // terms to it and the one of record i is kept
         uint32_t wv = wb, sst = 0u, smid = 0u;
         for (int i = 0; i < cnt; ++i) {
           asm volatile("" : "+v"(wv));
@@ -689,8 +691,8 @@ __device__ __forceinline__ SeqResult chain_sum_block(const float (&x)[E], int m,
           if constexpr (STOP) smid = lane == i ? wv : smid;
           float sv = __uint_as_float(wv);
 #pragma unroll
-          for (int e = 0; e < E; ++e) sv = __fadd_rn(sv, rl_f(lx[e], i));
-          wv = __float_as_uint(sv);
+          for (int e = 0; e < E; ++e) sv = __fadd_rn(sv, lx[e]);
+          wv = (uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(sv), i);
         }
         wb = __builtin_amdgcn_readfirstlane(wv);
         // every record checks the value its clean threads started from
