@@ -102,7 +102,7 @@ __device__ __forceinline__ float2 query_lanes(const float *q, int dim, int P) {
   return v;
 }
 
-__device__ void rotate_query_exact(float *s_q, const float *q, int dim, int P,
+__device__ __forceinline__ void rotate_query_exact(float *s_q, const float *q, int dim, int P,
                                    const uint32_t *signs, float inv_sqrt_p, float sqrt_p,
                                    const float2 *preloaded = nullptr) {
   if (P == 64 || P == 128) {
@@ -447,30 +447,12 @@ __host__ __device__ constexpr int lg_blocks(int n) { return (n + kLgTokens - 1) 
 
 // The per-item workspace (floats, from lg): the n logits / exponentials /
 // weights and four scalars at [n] (1/sum, then the cut's selection), padded
-// to 16 bytes; kStat floats per logits block (its maximum logit, smallest and
-// largest exponential, NaN flag, then the exponentials' fp64 sum at 4-5);
-// then kSeqTab words per sum chunk (sparse_sum_classify_kernel's segment
-// table).  Rings above kSelectInBlock use all of it.
-constexpr int kStat = 8;
-constexpr int kSeqT = 2;  // terms per thread of a sum chunk (more blocks classify at once)
-constexpr int kSeqChunk = seqsum_detail::kBlock * kSeqT;  // terms per sum chunk
-static_assert(kSeqChunk % kLgTokens == 0, "sum chunks are whole logits blocks");
-// segment table of a chunk, flat (seq_walk_flat): [0] entries m (at most
-// kMaxSeg + 1: the chunk's first kMaxSeg segments, then its remaining terms
-// as one hardware segment), then start[], cls[], inc[], x0[], x1[] of
-// kTabEnt each
-constexpr int kTabEnt = seqsum_detail::kMaxSeg + 1;
-constexpr int kTabStart = 1, kTabCls = kTabStart + kTabEnt, kTabInc = kTabCls + kTabEnt,
-              kTabX0 = kTabInc + kTabEnt, kTabX1 = kTabX0 + kTabEnt,
-              kSeqTab = (kTabX1 + kTabEnt + 3) & ~3;
-// chunks walked together (their terms and concatenated tables staged in LDS)
-constexpr int kSeqWin = 4;
-__host__ __device__ constexpr int seq_chunks(int n) { return (n + kSeqChunk - 1) / kSeqChunk; }
+// to 16 bytes; then kStat floats per logits block (its maximum logit,
+// smallest and largest exponential, NaN flag).  Rings above kSelectInBlock
+// use all of it.
+constexpr int kStat = 4;
 __host__ __device__ constexpr size_t lg_words(int n) { return ((size_t)n + 4 + 3) & ~(size_t)3; }
 __device__ __forceinline__ float *lg_stats(float *lg, int n) { return lg + lg_words(n); }
-__device__ __forceinline__ uint32_t *lg_tables(float *lg, int n) {
-  return reinterpret_cast<uint32_t *>(lg + lg_words(n) + (size_t)kStat * lg_blocks(n));
-}
 
 template <int PT, int KB>
 __global__ __launch_bounds__(kThreads) void sparse_logits_kernel(HeadDesc *const *item_desc,
@@ -530,7 +512,6 @@ __global__ __launch_bounds__(kThreads) void sparse_logits_kernel(HeadDesc *const
 __global__ __launch_bounds__(kThreads) void sparse_exp_kernel(HeadDesc *const *item_desc, float *ws,
                                                               size_t ws_stride) {
   __shared__ float s_r[3][kThreads / 64];
-  __shared__ double s_d[kThreads / 64];
   const int item = blockIdx.y;
   const int n = item_desc[item]->st.size;
   if (n <= kSelectInBlock) return;  // select_small takes the logits
@@ -558,7 +539,6 @@ __global__ __launch_bounds__(kThreads) void sparse_exp_kernel(HeadDesc *const *i
   for (int w2 = 0; w2 < kThreads / 64; ++w2)
     if (s_r[0][w2] > mx) mx = s_r[0][w2];
   float e_lo = __builtin_inff(), e_hi = 0.0f;
-  double esum = 0.0;
   int nan_e = 0;
 #pragma unroll
   for (int k = 0; k < kLgPer; ++k) {
@@ -569,19 +549,16 @@ __global__ __launch_bounds__(kThreads) void sparse_exp_kernel(HeadDesc *const *i
       nan_e |= e != e;
       e_lo = fminf(e_lo, e);
       e_hi = fmaxf(e_hi, e);
-      esum += (double)e;
     }
   }
   for (int off = 32; off > 0; off >>= 1) {
     e_lo = fminf(e_lo, __shfl_xor(e_lo, off));
     e_hi = fmaxf(e_hi, __shfl_xor(e_hi, off));
-    esum += __shfl_xor(esum, off);
   }
   nan_e = __syncthreads_or(nan_e);  // also orders s_r[0]'s reads before the writes below
   if (lane == 0) {
     s_r[1][wave] = e_lo;
     s_r[2][wave] = e_hi;
-    s_d[wave] = esum;
   }
   __syncthreads();
   if (tid == 0) {
@@ -589,65 +566,10 @@ __global__ __launch_bounds__(kThreads) void sparse_exp_kernel(HeadDesc *const *i
       e_lo = fminf(e_lo, s_r[1][w2]);
       e_hi = fmaxf(e_hi, s_r[2][w2]);
     }
-    double t = 0.0;
-    for (int w2 = 0; w2 < kThreads / 64; ++w2) t += s_d[w2];
     float *sb = st + kStat * blockIdx.x;
     sb[1] = e_lo;
     sb[2] = e_hi;
     sb[3] = nan_e ? 1.0f : 0.0f;
-    *reinterpret_cast<double *>(sb + 4) = t;
-  }
-}
-
-// The fp64 prediction of the left-to-right sum before each chunk of
-// kSeqChunk exponentials comes from the exp kernel's block sums, so every
-// chunk of a ring is classified at once (seq_classify, one block a chunk,
-// the bound counting the terms since the sum's start) into its segment table;
-// the select kernel then walks the chunks in order with the exact sum.  The
-// walk checks every prediction it uses, so the result is the chain's
-// whatever the tables say.  Grid (chunks, items).
-__global__ __launch_bounds__(kSelThreads) void sparse_sum_classify_kernel(HeadDesc *const *item_desc,
-                                                                          float *ws, size_t ws_stride) {
-  using namespace seqsum_detail;
-  constexpr int T = kSeqT;
-  __shared__ SeqShared sh;
-  __shared__ double s_p[kWaves];
-  const int item = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int n = item_desc[item]->st.size;
-  if (n <= kSelectInBlock) return;
-  const int c0 = blockIdx.x * kSeqChunk;
-  if (c0 >= n) return;
-  float *lg = ws + (size_t)item * ws_stride;
-  const double *bs = reinterpret_cast<const double *>(lg_stats(lg, n) + 4);  // stride kStat / 2
-  const int j0 = tid * T, cn = n - c0 < kSeqChunk ? n - c0 : kSeqChunk;
-  float x[T];
-#pragma unroll
-  for (int k = 0; k < T; ++k) x[k] = j0 + k < cn ? lg[c0 + j0 + k] : 0.0f;
-  double p = 0.0;
-  for (int b = tid; b < c0 / kLgTokens; b += kSelThreads) p += bs[(size_t)b * (kStat / 2)];
-  for (int off = 32; off > 0; off >>= 1) p += __shfl_xor(p, off);
-  if (lane == 0) s_p[wave] = p;
-  __syncthreads();
-  double P0 = 0.0;
-  for (int w = 0; w < kWaves; ++w) P0 += s_p[w];
-  int cls[T];
-  uint32_t r[T];
-  uint64_t ex;
-  seq_classify<T>(x, cn, c0, P0, c0, sh, cls, r, ex);
-  uint32_t *tab = lg_tables(lg, n) + (size_t)blockIdx.x * kSeqTab;
-  const int ns_all = sh.nseg, ns = ns_all < kMaxSeg ? ns_all : kMaxSeg;
-  const int m = ns + (ns_all > kMaxSeg ? 1 : 0);
-  if (tid == 0) tab[0] = (uint32_t)m;
-  for (int i = tid; i < m; i += kSelThreads) {
-    const int st = sh.seg_start[i];
-    tab[kTabStart + i] = (uint32_t)st;
-    const int c = i < ns ? sh.seg_cls[i] : kUnc;  // past kMaxSeg: the rest, term by term
-    const uint64_t d = i < ns ? sh.seg_r[i + 1] - sh.seg_r[i] : 0u;
-    tab[kTabCls + i] = (uint32_t)c;
-    tab[kTabInc + i] = d >= kTop ? kTop : (uint32_t)d;
-    // a hardware segment's first two terms (it has at least one)
-    tab[kTabX0 + i] = __float_as_uint(c == kUnc ? lg[st] : 0.0f);
-    tab[kTabX1 + i] = __float_as_uint(c == kUnc && st + 1 < n ? lg[st + 1] : 0.0f);
   }
 }
 
@@ -723,32 +645,24 @@ __device__ __forceinline__ uint32_t waves_before(const uint32_t *wsum, int wave)
 }
 
 // Shared memory of the select kernel.  The small path (n <= kLdsSort) keeps
-// 32-bit keys, 16-bit token indices and 16 x kSelThreads 16-bit radix counts;
-// the large path keeps its sort keys in the workspace.
+// 32-bit keys, 16-bit token indices and 16 x kSelThreads 16-bit radix counts
+// (cnt also holds chain_sum_block's LDS); the large path keeps its sort keys
+// in the workspace and stages its sums' terms over the keys.
 struct SelectShared {
   union {
-    struct {
-      uint32_t key[kLdsSort];          // also the exponentials, as floats
-      uint16_t idx[kLdsSort];
-      uint16_t cnt[16 * kSelThreads];  // cnt[digit * kSelThreads + thread]
-    };
-    // rings above kSelectInBlock: a window's segment list (seq_walk_flat)
-    struct {
-      int w_start[kSeqWin * kTabEnt + 1];
-      int w_cls[kSeqWin * kTabEnt];
-      uint32_t w_inc[kSeqWin * kTabEnt];
-      float w_x0[kSeqWin * kTabEnt];
-      float w_x1[kSeqWin * kTabEnt];
-    };
+    uint32_t key[kLdsSort];  // also the exponentials, as floats
+    float xs[seqsum_detail::kBlock * seqsum_detail::kMaxT];  // chain_sum_long's terms
   };
+  uint16_t idx[kLdsSort];
+  uint16_t cnt[16 * kSelThreads];  // cnt[digit * kSelThreads + thread]
   __align__(16) float stage[kStage];
   float red[kSelThreads];
   __align__(16) uint32_t wsum[kSelThreads / 64];
   float bcast[2];
   int cut;
   uint64_t last;
-  SeqShared seq;
 };
+static_assert(kLdsSort == seqsum_detail::kBlock * seqsum_detail::kMaxT, "the sums' terms fit over the keys");
 
 // Block maximum with the reference's NaN-skipping compare (x > m ? x : m;
 // every partial maximum is a number, so the tree gives the sequential value).
@@ -1437,7 +1351,7 @@ __global__ __launch_bounds__(kSelThreads) void sparse_select_kernel(HeadDesc *co
     static_assert(sizeof(ChainShared) <= sizeof(sh.cnt), "chain_sum_block's LDS in sh.cnt");
     ChainShared &cs = *reinterpret_cast<ChainShared *>(sh.cnt);
     const float sv =
-        chain_sum_long<false>([lg](int i) { return lg[i]; }, n, 0.0f, __builtin_inff(), sh.seq.xs, cs).s;
+        chain_sum_long<false>([lg](int i) { return lg[i]; }, n, 0.0f, __builtin_inff(), sh.xs, cs).s;
     if (tid == 0) s_bcast[0] = 1.0f / sv;
   }
   __syncthreads();
@@ -1485,7 +1399,7 @@ __global__ __launch_bounds__(kSelThreads) void sparse_cut_kernel(HeadDesc *const
   __shared__ float s_bcast[2];
   __shared__ int s_cut;
   __shared__ uint64_t s_last;
-  __shared__ SeqShared s_seq;
+  __shared__ float s_xs[seqsum_detail::kBlock * seqsum_detail::kMaxT];
   __shared__ ChainShared s_cs;
   const int item = blockIdx.x;
   const int tid = threadIdx.x;
@@ -1535,7 +1449,7 @@ __global__ __launch_bounds__(kSelThreads) void sparse_cut_kernel(HeadDesc *const
       s_cut = ii;
     }
   } else {
-    const SeqResult rq = chain_sum_long<true>(quad, n_quads, 0.0f, v_mass, s_seq.xs, s_cs);
+    const SeqResult rq = chain_sum_long<true>(quad, n_quads, 0.0f, v_mass, s_xs, s_cs);
     // the single tokens run only after every whole quad, i.e. over the last
     // n % 4 tokens at most (once the mass reaches v_mass they add nothing)
     if (tid == 0) {
@@ -1896,13 +1810,8 @@ __global__ __launch_bounds__(kThreads) void sparse_finish_kernel(HeadDesc *const
 
 // Per item: the logits, then the exponentials, then the weights (n floats),
 // 1/sum at [n] for rings that sort outside the select kernel, and the
-// logits blocks' statistics from [n + 4]; the sum chunks' segment tables
-// only when some ring is longer than kSelectInBlock (the one-block selection
-// of shorter rings sums on one lane and never reads them).
-size_t item_stride(int n) {
-  return lg_words(n) + (size_t)kStat * lg_blocks(n) +
-         (n > kSelectInBlock ? (size_t)kSeqTab * seq_chunks(n) : 0);
-}
+// logits blocks' statistics from [n + 4].
+size_t item_stride(int n) { return lg_words(n) + (size_t)kStat * lg_blocks(n); }
 
 // Items per launch: the grid holds items in one dimension (at most 65,535).
 constexpr int kMaxItems = 65535;

@@ -309,7 +309,7 @@ int adaptq_plan_compute_device_static(adaptq_plan_t plan, const float *d_queries
  * fits one block per item (about 512 contexts or more at padded 64/128), else
  * (padded + 4) * 4 bytes per context and split; sparse-V plans need about
  * 4 + 4 * padded / 256 bytes per token of the longest ring per context up to
- * 8,192 tokens, and about 27 + 4 * padded / 256 bytes per token above.
+ * 8,192 tokens, and about 22 + 4 * padded / 256 bytes per token above.
  * Returns -1 on error (a null handle, or a context with staged host
  * appends). */
 long long adaptq_plan_workspace_bytes(adaptq_plan_t plan);

@@ -1,16 +1,14 @@
-"""The segment algorithm of block_seq_sum (adaptq_amd/csrc/seqsum.hpp: the
+"""The segment algorithm of chain_sum_block (adaptq_amd/csrc/seqsum.hpp: the
 reference's left-to-right fp32 sums of the sparse-V selection,
 attention.cpp:422-426 and :454-472, computed by a whole block) run on the host
 with the kernels' own per-term functions (seqsum_terms.hpp), against the
 plain fp32 chain: the count of terms added before the stop and the sum's bits
 must be equal on every sequence of tests/cpp/seqsum_check.cpp (softmax sums,
 sorted-probability quad sums with mass stops, stops at reached values,
-tie-heavy, subnormal, zero and wide-range terms).  The same file models the
-pre-classified softmax sum of rings above 8,192 tokens (sparse.hip:
-sparse_sum_classify_kernel and seq_walk_flat): chunks classified from the fp64
-prefix of all earlier terms, flat segment lists, windows of chunks walked
-together; with a planted 5% error in that prefix the walk's checks must send
-windows to the term-by-term redo and still give the chain's bits."""
+tie-heavy, subnormal, zero and wide-range terms), for 1 to 8 terms a thread
+and in chunks of 8,192 terms (chain_sum_long); with a planted 3-5% error in
+the prefix the walk's checks must send sums to the redo and still give the
+chain's bits."""
 import os
 import shutil
 import subprocess
@@ -31,5 +29,5 @@ def test_seqsum_model_equals_chain(tmp_path):
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0 and " 0 mismatches" in r.stdout, r.stdout
     # the planted misprediction reached the redo
-    redone = int(r.stdout.split("pre-classified: ")[1].split(" windows")[0])
+    redone = int(r.stdout.split(" segments, ")[1].split(" redone")[0])
     assert redone > 0, r.stdout
