@@ -108,10 +108,9 @@ __device__ __forceinline__ float rl_f(float v, int l) {
 //      segment's increment, then the hardware thread's terms by fp32 adds
 //      (lane k adds record k's terms; the walk keeps lane i's sum),
 //      recording the value each segment starts from; then every record
-//      checks its own start in parallel (as block_seq_sum does: s in the
-//      class's binade, K below 2^24 after the clean threads); a failed check
-//      redoes the whole chain on one lane, so the result is the chain's in
-//      every case;
+//      checks its own start in parallel (s in the class's binade, K below
+//      2^24 after the clean threads); a failed check redoes the whole chain
+//      on one lane, so the result is the chain's in every case;
 //   4. STOP (the stop tested before each term): it lies in the first segment
 //      whose end reaches it: in its hardware terms the walk tests them one by
 //      one, in its clean part the block finds the thread whose K range holds
