@@ -138,6 +138,15 @@ namespace seqsum_detail {
 // Inclusive scan of v over the wave by DPP (row shifts, then the row
 // broadcasts of lanes 15 and 31), for the prediction only: fp32 rounding in
 // any order is covered by run_class_f32's margin.
+// A block barrier that orders LDS only: global loads issued before it stay in
+// flight (the sums share nothing through global memory, and chain_sum_long's
+// next chunk is requested before a chunk is walked).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 template <int CTRL, int ROW_MASK, int BANK_MASK, bool BOUND>
 __device__ __forceinline__ uint32_t dpp_u(uint32_t x) {
   return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, ROW_MASK, BANK_MASK, BOUND);
@@ -202,7 +211,7 @@ __device__ __forceinline__ SeqResult chain_sum_block(const float (&x)[E], int m,
   const uint64_t bad_w = __ballot(bad);
   if (lane == 63) cs.wtot[wave] = inc;
   if (lane == 0) cs.wbad[wave] = bad_w != 0;
-  __syncthreads();
+  lds_barrier();
   float P = s0 + (inc - loc);
 #pragma unroll
   for (int w = 0; w < kWaves; ++w)
@@ -228,7 +237,7 @@ __device__ __forceinline__ SeqResult chain_sum_block(const float (&x)[E], int m,
   const uint32_t rin = wave_scan_dpp(rs);  // below 64 x 2^23: no wrap
   cs.cls[tid] = c;
   if (lane == 63) cs.wr[wave] = rin;
-  __syncthreads();
+  lds_barrier();
   // ---- 2. segment records ----
   uint32_t Rb = rin;  // the block's inclusive sum of r
 #pragma unroll
@@ -239,7 +248,7 @@ __device__ __forceinline__ SeqResult chain_sum_block(const float (&x)[E], int m,
   const bool end = has && (c == kUnc || tid == nt - 1 || (cn != kUnc && cn != c));
   const uint64_t em = __ballot(end);
   if (lane == 0) cs.wcnt[wave] = __popcll(em);
-  __syncthreads();
+  lds_barrier();
   int kidx = __popcll(em & ((1ull << lane) - 1ull)), nseg = 0;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) {
@@ -252,7 +261,7 @@ __device__ __forceinline__ SeqResult chain_sum_block(const float (&x)[E], int m,
     cs.rec_R[kidx] = Rb;
     cs.rec_end[kidx] = tid | (c == kUnc ? kRecHw : 0);
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- 3. the walk, on wave 0 ----
   if (wave == 0) {
@@ -348,7 +357,7 @@ __device__ __forceinline__ SeqResult chain_sum_block(const float (&x)[E], int m,
       cs.q_search = search;
     }
   }
-  __syncthreads();
+  lds_barrier();
   if constexpr (STOP) {
     if (cs.q_search) {
       if (tid >= cs.q_start && tid <= cs.q_end && c != kUnc) {
@@ -369,11 +378,11 @@ __device__ __forceinline__ SeqResult chain_sum_block(const float (&x)[E], int m,
           cs.s = __uint_as_float(cs.q_exp | (Kb - 0x800000u));
         }
       }
-      __syncthreads();
+      lds_barrier();
     }
   }
   const SeqResult res{cs.count, cs.s};
-  __syncthreads();
+  lds_barrier();
   return res;
 }
 
@@ -395,7 +404,7 @@ __device__ __forceinline__ SeqResult chain_sum_long(Load load, int n, float s, f
     const int cn = n - c0 < C ? n - c0 : C;
 #pragma unroll
     for (int k = 0; k < E; ++k) xs[j0 + k] = x[k];
-    __syncthreads();
+    lds_barrier();
     float y[E];
 #pragma unroll
     for (int k = 0; k < E; ++k) y[k] = c0 + C + j0 + k < n ? load(c0 + C + j0 + k) : 0.0f;
