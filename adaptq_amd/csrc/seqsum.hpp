@@ -117,6 +117,9 @@ __device__ __forceinline__ float rl_f(float v, int l) {
 //      kstop_of(stop) and that thread steps through its terms.
 // Non-finite or negative terms send the whole sum to one lane.
 
+// A record's last thread, with kRecHw when it is a hardware thread.
+constexpr int kRecHw = 0x8000, kRecThr = 0x7FFF;
+
 // LDS of chain_sum_block.
 struct ChainShared {
   int cls[seqsum_detail::kBlock];  // the thread's class, or kUnc
@@ -187,13 +190,23 @@ __device__ __forceinline__ bool fast_incr(float x, int eu, uint32_t &r) {
 
 }  // namespace seqsum_detail
 
-template <int E, bool STOP>
-__device__ __forceinline__ SeqResult chain_sum_block(const float (&x)[E], int m, float s0, float stop,
-                                                     const float *xs, ChainShared &cs) {
+// Steps 1 and 2 of chain_sum_block: every thread's class and increments,
+// predicted from s0 (the exact sum before the terms, or a prediction of it:
+// the walk checks every class it uses), and the segment records in cs (with
+// cs.wbad, a term not finite and >= 0, per wave).  Returns the thread's class,
+// the sum of its r, the block's inclusive sum of r at it, and the number of
+// records.  Ends with a barrier.
+struct ChainThread {
+  int c;
+  uint32_t rs, Rb;
+  int nseg;
+};
+
+template <int E>
+__device__ __forceinline__ ChainThread chain_records(const float (&x)[E], int m, float s0,
+                                                     ChainShared &cs) {
   using namespace seqsum_detail;
   static_assert(E >= 1 && E <= 8, "terms per thread");
-  constexpr int kRecHw = 0x8000, kRecThr = 0x7FFF;
-  if constexpr (!STOP) stop = __builtin_inff();
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j0 = tid * E;
   const int nt = (m + E - 1) / E;  // threads with terms
@@ -262,6 +275,20 @@ __device__ __forceinline__ SeqResult chain_sum_block(const float (&x)[E], int m,
     cs.rec_end[kidx] = tid | (c == kUnc ? kRecHw : 0);
   }
   lds_barrier();
+
+  return ChainThread{c, rs, Rb, nseg};
+}
+
+template <int E, bool STOP>
+__device__ __forceinline__ SeqResult chain_sum_block(const float (&x)[E], int m, float s0, float stop,
+                                                     const float *xs, ChainShared &cs) {
+  using namespace seqsum_detail;
+  if constexpr (!STOP) stop = __builtin_inff();
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j0 = tid * E;
+  const ChainThread ct = chain_records<E>(x, m, s0, cs);
+  const int c = ct.c, nseg = ct.nseg;
+  const uint32_t rs = ct.rs, Rb = ct.Rb;
 
   // ---- 3. the walk, on wave 0 ----
   if (wave == 0) {
