@@ -138,9 +138,6 @@ struct ChainShared {
 
 namespace seqsum_detail {
 
-// Inclusive scan of v over the wave by DPP (row shifts, then the row
-// broadcasts of lanes 15 and 31), for the prediction only: fp32 rounding in
-// any order is covered by run_class_f32's margin.
 // A block barrier that orders LDS only: global loads issued before it stay in
 // flight (the sums share nothing through global memory, and chain_sum_long's
 // next chunk is requested before a chunk is walked).
@@ -157,7 +154,8 @@ __device__ __forceinline__ uint32_t dpp_u(uint32_t x) {
 // Inclusive scan over the wave by DPP: row shifts by 1, 2, 3 (zero fill),
 // 4 (lanes 4..15 of each row) and 8 (lanes 8..15), then lane 15's total into
 // rows 1 and 3 and lane 31's into rows 2 and 3.  Exact for integers; for
-// floats the rounding of this order differs from a left-to-right sum.
+// floats the rounding of this order differs from a left-to-right sum, which
+// the prediction's margin covers (run_class_f32).
 template <class T>
 __device__ __forceinline__ T wave_scan_dpp(T v) {
   auto bits = [](T a) -> uint32_t {
