@@ -1512,10 +1512,21 @@ template <int PT, int KB, int VB, bool LOGITS_IN>
 __global__ __launch_bounds__(kSelThreads) void sparse_fused_kernel(
     HeadDesc *const *item_desc, const float *__restrict__ queries, float v_mass, float inv_sqrt_p,
     float sqrt_p, float *ws, size_t ws_stride, float *__restrict__ outs) {
-  __shared__ SelectShared sh;
-  __shared__ float s_q[PT];
-  __shared__ float s_cb[16];
-  __shared__ float s_cbk[16];
+  // one LDS object with the codebooks and the query first: their addresses
+  // stay below the 64 KB of a ds_read's immediate offset, so a codebook
+  // lookup is one read of the code's byte offset (a separate variable may be
+  // placed after the ~100 KB of SelectShared and cost an add per lookup)
+  struct FusedShared {
+    float cbk[16];
+    float cb[16];
+    float q[PT];
+    SelectShared sel;
+  };
+  __shared__ FusedShared fs;
+  SelectShared &sh = fs.sel;
+  float *const s_q = fs.q;
+  float *const s_cb = fs.cb;
+  float *const s_cbk = fs.cbk;
   constexpr int UB = VWord<VB>::bytes, CPU = VWord<VB>::codes;
   constexpr int U = PT * VB / 8 / UB;  // units per V row (4..16)
   constexpr int TPI = 64 / U;          // tokens per wave step
