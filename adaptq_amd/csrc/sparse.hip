@@ -1516,9 +1516,13 @@ __global__ __launch_bounds__(kSelThreads) void sparse_fused_kernel(
   // stay below the 64 KB of a ds_read's immediate offset, so a codebook
   // lookup is one read of the code's byte offset (a separate variable may be
   // placed after the ~100 KB of SelectShared and cost an add per lookup)
+  // V pair table (2- and 4-bit codes): two adjacent codes of a row, a
+  // nibble (2-bit) or a byte (4-bit), to their two centres in one read
+  constexpr int kPairs = VB == 2 ? 16 : VB == 4 ? 256 : 1;
   struct FusedShared {
     float cbk[16];
     float cb[16];
+    float2 cb2[kPairs];
     float q[PT];
     SelectShared sel;
   };
@@ -1541,6 +1545,9 @@ __global__ __launch_bounds__(kSelThreads) void sparse_fused_kernel(
     return;
   }
   if (tid < (1 << VB)) s_cb[tid] = cbv<VB>(tid);
+  if constexpr (VB == 2 || VB == 4) {
+    if (tid < kPairs) fs.cb2[tid] = make_float2(cbv<VB>(tid >> VB), cbv<VB>(tid & ((1 << VB) - 1)));
+  }
   if (tid < (1 << KB)) s_cbk[tid] = cbv<KB>(tid);
   float *lg = ws + (size_t)item * ws_stride;
   const int s0 = (int)(((long long)d->st.head - n + cap) % cap);
@@ -1609,10 +1616,23 @@ __global__ __launch_bounds__(kSelThreads) void sparse_fused_kernel(
       }
     }
 #pragma unroll
-    for (int j = 0; j < UNR; ++j)
+    for (int j = 0; j < UNR; ++j) {
+      if constexpr (VB == 2 || VB == 4) {
+        // codes 2k and 2k + 1 share a nibble (2-bit) or byte (4-bit), the
+        // first in its high bits; the same products in the same order as one
+        // code at a time
 #pragma unroll
-      for (int c = 0; c < CPU; ++c)
-        acc[c] = fmaf(s_cb[(bits[j] >> vcode_shift<VB>(c)) & ((1u << VB) - 1u)], wt[j], acc[c]);
+        for (int k = 0; k < CPU / 2; ++k) {
+          const float2 cv = fs.cb2[(bits[j] >> (vcode_shift<VB>(2 * k + 1))) & (uint32_t)(kPairs - 1)];
+          acc[2 * k] = fmaf(cv.x, wt[j], acc[2 * k]);
+          acc[2 * k + 1] = fmaf(cv.y, wt[j], acc[2 * k + 1]);
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < CPU; ++c)
+          acc[c] = fmaf(s_cb[(bits[j] >> vcode_shift<VB>(c)) & ((1u << VB) - 1u)], wt[j], acc[c]);
+      }
+    }
   }
   // the TPI token groups of a wave (lanes u + U * sub), then the waves in order
 #pragma unroll
