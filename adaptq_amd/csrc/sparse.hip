@@ -1516,9 +1516,10 @@ __global__ __launch_bounds__(kSelThreads) void sparse_fused_kernel(
   // stay below the 64 KB of a ds_read's immediate offset, so a codebook
   // lookup is one read of the code's byte offset (a separate variable may be
   // placed after the ~100 KB of SelectShared and cost an add per lookup)
-  // V pair table (2- and 4-bit codes): two adjacent codes of a row, a
-  // nibble (2-bit) or a byte (4-bit), to their two centres in one read
-  constexpr int kPairs = VB == 2 ? 16 : VB == 4 ? 256 : 1;
+  // V pair table (2-bit codes): a nibble of a row, two adjacent codes, to
+  // their two centres in one read (16 entries: no bank conflicts; a 256-entry
+  // byte table for 4-bit codes conflicts and is slower)
+  constexpr int kPairs = VB == 2 ? 16 : 1;
   struct FusedShared {
     float cbk[16];
     float cb[16];
@@ -1545,8 +1546,8 @@ __global__ __launch_bounds__(kSelThreads) void sparse_fused_kernel(
     return;
   }
   if (tid < (1 << VB)) s_cb[tid] = cbv<VB>(tid);
-  if constexpr (VB == 2 || VB == 4) {
-    if (tid < kPairs) fs.cb2[tid] = make_float2(cbv<VB>(tid >> VB), cbv<VB>(tid & ((1 << VB) - 1)));
+  if constexpr (VB == 2) {
+    if (tid < kPairs) fs.cb2[tid] = make_float2(cbv<2>(tid >> 2), cbv<2>(tid & 3));
   }
   if (tid < (1 << KB)) s_cbk[tid] = cbv<KB>(tid);
   float *lg = ws + (size_t)item * ws_stride;
@@ -1617,10 +1618,9 @@ __global__ __launch_bounds__(kSelThreads) void sparse_fused_kernel(
     }
 #pragma unroll
     for (int j = 0; j < UNR; ++j) {
-      if constexpr (VB == 2 || VB == 4) {
-        // codes 2k and 2k + 1 share a nibble (2-bit) or byte (4-bit), the
-        // first in its high bits; the same products in the same order as one
-        // code at a time
+      if constexpr (VB == 2) {
+        // codes 2k and 2k + 1 share a nibble, the first in its high bits; the
+        // same products in the same order as one code at a time
 #pragma unroll
         for (int k = 0; k < CPU / 2; ++k) {
           const float2 cv = fs.cb2[(bits[j] >> (vcode_shift<VB>(2 * k + 1))) & (uint32_t)(kPairs - 1)];
